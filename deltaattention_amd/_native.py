@@ -1,0 +1,86 @@
+"""ctypes binding of libdeltaattn.so (the C ABI declared in include/deltaattn.h).
+
+There is no fallback: if the library is missing or fails to load, every operation
+raises ``NativeLibraryError``.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "libdeltaattn.so")
+
+DA_BF16 = 1
+DA_I32 = 3
+DA_F32 = 4
+DA_VARIANT = {"hybrid": 0, "sanity": 1, "pure_phase1": 2}
+DA_NUM_STRIDES = 24
+
+# (name, restype, argtypes) for every symbol of include/deltaattn.h
+_P, _I, _L, _F = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float
+SIGNATURES = {
+    "da_last_error": (ctypes.c_char_p, []),
+    "da_version": (_I, []),
+    "da_select": (_I, [_P, _I, _L, _L, _L, _L, _L, _L, _L, _F, _I, _L, _L, _P, _P, _P]),
+    "da_pack_workspace_size": (_L, [_L, _L, _L]),
+    "da_pack": (_I, [_P, _P, _P, _I, _L, _L, _L, _L, _L, _L, _L, _L, _L, _L, _L, _P, _P, _P, _P,
+                     _P, _P, _P, _L, _P]),
+    "da_hybrid_workspace_size": (_L, [_L, _L, _L]),
+    "da_hybrid_prefill": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _P, _I, _L, _L, _L, _L, _L, _L, _P,
+                               _L, _P, _L, _F, _I, _I, _P, _L, _P]),
+    "da_dense_prefill": (_I, [_P, _P, _P, _P, _I, _L, _L, _L, _L, _L, _L, _P, _I, _F, _P]),
+}
+
+
+class NativeLibraryError(RuntimeError):
+    """libdeltaattn.so is missing or could not be loaded."""
+
+
+class DeltaAttnError(RuntimeError):
+    """A C-ABI call returned an error status."""
+
+    def __init__(self, what: str, code: int, message: str):
+        super().__init__(f"{what} failed ({code}): {message}")
+        self.code = code
+
+
+_lock = threading.Lock()
+_lib = None
+
+
+def lib() -> ctypes.CDLL:
+    """Load libdeltaattn.so once; raise NativeLibraryError if it is not there."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not os.path.exists(LIB_PATH):
+                raise NativeLibraryError(
+                    f"{LIB_PATH} is not built; run `python -m deltaattention_amd.build` "
+                    "(there is no non-native fallback)")
+            try:
+                handle = ctypes.CDLL(LIB_PATH)
+            except OSError as e:
+                raise NativeLibraryError(f"cannot load {LIB_PATH}: {e}") from e
+            for name, (res, args) in SIGNATURES.items():
+                fn = getattr(handle, name)
+                fn.restype = res
+                fn.argtypes = args
+            _lib = handle
+    return _lib
+
+
+def check(rc: int, what: str) -> None:
+    if rc != 0:
+        msg = lib().da_last_error()
+        raise DeltaAttnError(what, rc, msg.decode() if msg else "")
+
+
+def strides_array(values) -> ctypes.Array:
+    arr = (ctypes.c_int64 * DA_NUM_STRIDES)()
+    for i, v in enumerate(values):
+        arr[i] = int(v)
+    return arr

@@ -1,0 +1,604 @@
+// Causal GQA flash prefill on gfx950: the dense control and the two-phase
+// compressed (delta) prefill share one kernel.
+//
+// Replaces _attn_fwd_flat (flashAttention.py:5-91) and
+// hybrid_compressed_flash_kernel / _sanity / pure_phase1_flash_kernel
+// (deltaFlashAttention.py:9-357) with their wrappers (modeling_llama.py:306-451).
+//
+// Work decomposition.  A workgroup is 4 waves; each wave owns 32 query rows of one
+// query head.  The 4 waves always read the same KV head: with a GQA group of 4 they
+// are the 4 query heads of the group on the same 32 rows, so every K/V tile staged
+// in LDS serves 4 heads (repeat_kv is never materialised).  With smaller groups the
+// waves split 64 or 128 rows instead.  The rows of a workgroup lie inside one
+// logical 128-row query block of the reference, so the whole workgroup follows the
+// reference's schedule for that block.
+//
+// Logical schedule (deltaFlashAttention.py:58-113).  Phase 1 takes packed blocks of
+// 128 anchors while their maximum timestamp is < start_m - W; Phase 2 covers dense
+// keys from ((last + 1) / 128) * 128 to the diagonal.  The prefix of safe packed
+// blocks is found by a binary search over the per-head prefix maxima of the block
+// maxima (hybrid_schedule_kernel), which reproduces the reference's
+// stop-at-first-unsafe-block loop for any timestamps, including its zero-padding
+// behaviour (fully padded blocks have maximum 0).
+//
+// MFMA formulation.  Scores are computed transposed, S^T = K Q^T, with
+// v_mfma_f32_32x32x16_bf16: K (32 keys x 16 dims) comes from LDS as the A operand,
+// Q^T stays in registers as the B operand for the whole key loop.  In the S^T
+// accumulator a lane holds one query and 16 keys, so the row max and row sum of the
+// online softmax are mostly in-lane (one exchange with lane ^ 32 per tile).  The
+// output is accumulated transposed too, O^T += V^T P^T: the bf16 probabilities are
+// already in the B-operand layout, and V^T comes from an LDS tile that the loader
+// transposes while staging it.
+//
+// Pipeline.  Tiles of 64 keys (K: 16 KiB, V^T: 16 KiB, counts and timestamps:
+// 512 B) are double-buffered in LDS; the global loads of tile t+1 are issued before
+// tile t is computed and written to the other buffer afterwards, with one barrier
+// per tile.  Two workgroups fit per CU (66.5 KiB LDS each).
+//
+// Softmax numerics.  exp2 with the softmax scale folded in: p = 2^(s*c - m*c) with
+// c = scale * log2(e) -- the same values as exp(s*scale - m*scale).  In Phase 1
+// p is multiplied by the anchor count in fp32 and then rounded to bf16 for the
+// P.V product while l accumulates the fp32 weights (deltaFlashAttention.py:86-98).
+#include "da_common.hpp"
+
+namespace da {
+
+constexpr int kD = 128;
+constexpr int kTileN = 64;
+constexpr int kKBytes = kTileN * kD * 2;
+constexpr int kVBytes = kD * kTileN * 2;
+constexpr int kStageBytes = kKBytes + kVBytes + kTileN * 4 + kTileN * 4;
+constexpr int kBlock = 128;  // logical block of the reference schedule
+
+enum Variant : int { kHybrid = 0, kSanity = 1, kPure = 2, kDense = 3 };
+
+struct AttnArgs {
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  const uint16_t* kp;
+  const uint16_t* vp;
+  const int32_t* ts;
+  const void* cnt;
+  uint16_t* out;
+  int64_t sq_b, sq_h, sq_n;
+  int64_t sk_b, sk_h, sk_n;
+  int64_t sv_b, sv_h, sv_n;
+  int64_t skp_b, skp_h, skp_n;
+  int64_t svp_b, svp_h, svp_n;
+  int64_t so_b, so_h, so_n;
+  int64_t sts_b, sts_h;
+  int64_t scnt_b, scnt_h;
+  int B, Hq, Hkv, G, Nq, Nk;
+  int P_host;
+  const int32_t* P_dev;
+  int window;
+  float scale_log2;  // softmax scale * log2(e)
+  int no_count;
+  int cnt_is_float;
+  int causal;
+  const int32_t* sched;  // [B*Hkv][2][nblk_cap]: block maxima, prefix maxima
+  int nblk_cap;
+  int hpw;          // query heads per workgroup (4, 2 or 1)
+  int rows_per_wg;  // 32 * (4 / hpw)
+  int n_row_groups;
+  int units;        // B * Hkv * (G / hpw)
+};
+
+__device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// LDS byte offsets inside a stage.
+__device__ __forceinline__ int k_lds_off(int row, int chunk) {
+  return row * (kD * 2) + ((chunk ^ (row & 15)) << 4);
+}
+__device__ __forceinline__ int vt_lds_off(int d, int granule) {
+  return kKBytes + d * (kTileN * 2) + ((granule ^ ((d >> 1) & 15)) << 3);
+}
+constexpr int kCntOff = kKBytes + kVBytes;
+constexpr int kTsOff = kCntOff + kTileN * 4;
+
+struct TileRegs {
+  u32x4 k[4];
+  u32x4 v[4];
+  float cnt;
+  int ts;
+};
+
+// Global -> registers for one 64-key tile.  Thread tid loads 16-byte chunk
+// (tid % 16) of keys 4 * (tid / 16) + j, j = 0..3.
+__device__ __forceinline__ void load_tile(TileRegs& r, const uint16_t* kbase, const uint16_t* vbase,
+                                          int64_t sk_n, int64_t sv_n, int key0, int limit,
+                                          int tid, bool with_meta, const int32_t* tsrow,
+                                          const void* cntrow, int cnt_is_float, int no_count,
+                                          int meta_limit, int ts_oob) {
+  const int chunk = tid & 15;
+  const int kg = tid >> 4;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const int key = key0 + kg * 4 + j;
+    if (key < limit) {
+      r.k[j] = *(const u32x4*)(kbase + (int64_t)key * sk_n + chunk * 8);
+      r.v[j] = *(const u32x4*)(vbase + (int64_t)key * sv_n + chunk * 8);
+    } else {
+      r.k[j] = u32x4{0, 0, 0, 0};
+      r.v[j] = u32x4{0, 0, 0, 0};
+    }
+  }
+  if (with_meta && tid < kTileN) {
+    const int key = key0 + tid;
+    if (key < meta_limit) {
+      if (no_count)
+        r.cnt = 1.0f;
+      else if (cnt_is_float)
+        r.cnt = ((const float*)cntrow)[key];
+      else
+        r.cnt = (float)((const int32_t*)cntrow)[key];
+      r.ts = tsrow ? tsrow[key] : 0;
+    } else {
+      r.cnt = 0.0f;
+      r.ts = ts_oob;
+    }
+  }
+}
+
+__device__ __forceinline__ void store_tile(const TileRegs& r, char* stage, int tid, bool with_meta) {
+  const int chunk = tid & 15;
+  const int kg = tid >> 4;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) *(u32x4*)(stage + k_lds_off(kg * 4 + j, chunk)) = r.k[j];
+  // transpose 4 keys x 8 dims into 8 rows (dims) of 4 keys
+#pragma unroll
+  for (int w = 0; w < 4; ++w) {
+    const uint32_t a = r.v[0][w], b = r.v[1][w], c = r.v[2][w], d = r.v[3][w];
+    const int d0 = chunk * 8 + 2 * w;
+    u32x2 lo, hi;
+    lo[0] = (a & 0xffffu) | (b << 16);
+    lo[1] = (c & 0xffffu) | (d << 16);
+    hi[0] = (a >> 16) | (b & 0xffff0000u);
+    hi[1] = (c >> 16) | (d & 0xffff0000u);
+    *(u32x2*)(stage + vt_lds_off(d0, kg)) = lo;
+    *(u32x2*)(stage + vt_lds_off(d0 + 1, kg)) = hi;
+  }
+  if (with_meta && tid < kTileN) {
+    ((float*)(stage + kCntOff))[tid] = r.cnt;
+    ((int*)(stage + kTsOff))[tid] = r.ts;
+  }
+}
+
+template <int VARIANT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void attn_kernel(AttnArgs a) {
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int hl = lane >> 5;   // which half of the wave
+  const int ql = lane & 31;   // query column of this lane
+
+  // ---- workgroup -> (unit, row group): XCD-aware, longest rows first ----
+  const int wg = blockIdx.x;
+  int unit, rg;
+  if ((a.units & 7) == 0) {
+    const int xcd = wg & 7, idx = wg >> 3, upx = a.units >> 3;
+    unit = xcd * upx + idx % upx;
+    rg = a.n_row_groups - 1 - idx / upx;
+  } else {
+    unit = wg % a.units;
+    rg = a.n_row_groups - 1 - wg / a.units;
+  }
+  const int hunits = a.G / a.hpw;
+  const int bg = unit / hunits;  // b * Hkv + g
+  const int hu = unit - bg * hunits;
+  const int b = bg / a.Hkv, g = bg - (bg / a.Hkv) * a.Hkv;
+  const int h = g * a.G + hu * a.hpw + (wid % a.hpw);
+  const int R0 = rg * a.rows_per_wg;
+  const int r0w = R0 + (wid / a.hpw) * 32;  // first row of this wave
+  const int wg_end = R0 + a.rows_per_wg;    // one past the last row of the workgroup
+  const int start_m = (R0 / kBlock) * kBlock;
+
+  // ---- schedule ----
+  int P = a.P_host;
+  if (a.P_dev) P = min(*a.P_dev, a.P_host);
+  int n1 = 0, ds = 0;
+  int kend = a.causal ? min(a.Nk, wg_end) : a.Nk;
+  if (VARIANT == kHybrid || VARIANT == kSanity) {
+    const int nblk = (P + kBlock - 1) / kBlock;
+    const int32_t* bmax = a.sched + (int64_t)bg * 2 * a.nblk_cap;
+    const int32_t* pmax = bmax + a.nblk_cap;
+    const int thr = start_m - a.window;
+    int lo = 0, hi = nblk;
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      if (pmax[mid] < thr) lo = mid + 1; else hi = mid;
+    }
+    const int n_safe = lo;
+    const int last = n_safe > 0 ? bmax[n_safe - 1] : -1;
+    ds = max(0, ((last + 1) / kBlock) * kBlock);
+    if (VARIANT == kHybrid) n1 = n_safe * (kBlock / kTileN);
+    kend = min(a.Nk, wg_end);
+  } else if (VARIANT == kPure) {
+    n1 = (P + kTileN - 1) / kTileN;
+    kend = 0;
+  }
+  const int n2 = kend > ds ? (kend - ds + kTileN - 1) / kTileN : 0;
+  const int ntiles = n1 + n2;
+
+  const uint16_t* kp_base = a.kp + (int64_t)b * a.skp_b + (int64_t)g * a.skp_h;
+  const uint16_t* vp_base = a.vp + (int64_t)b * a.svp_b + (int64_t)g * a.svp_h;
+  const uint16_t* k_base = a.k + (int64_t)b * a.sk_b + (int64_t)g * a.sk_h;
+  const uint16_t* v_base = a.v + (int64_t)b * a.sv_b + (int64_t)g * a.sv_h;
+  const int32_t* ts_row = a.ts ? a.ts + (int64_t)b * a.sts_b + (int64_t)g * a.sts_h : nullptr;
+  const char* cnt_row = a.cnt ? (const char*)a.cnt + ((int64_t)b * a.scnt_b + (int64_t)g * a.scnt_h) * 4 : nullptr;
+  const bool meta = (VARIANT == kHybrid || VARIANT == kPure);
+
+  // ---- Q^T in registers (B operand): lane (ql, hl) holds dims 16t + 8hl .. +7 ----
+  bf16x8 qreg[kD / 16];
+  {
+    const int row = r0w + ql;
+    const uint16_t* qrow = a.q + (int64_t)b * a.sq_b + (int64_t)h * a.sq_h + (int64_t)row * a.sq_n;
+#pragma unroll
+    for (int t = 0; t < kD / 16; ++t) {
+      u32x4 w = (row < a.Nq) ? *(const u32x4*)(qrow + 16 * t + 8 * hl) : u32x4{0, 0, 0, 0};
+      qreg[t] = __builtin_bit_cast(bf16x8, w);
+    }
+  }
+
+  f32x16 o[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) o[i] = f32x16{};
+  float m_i = -INFINITY, l_i = 0.0f;
+  const float c = a.scale_log2;
+
+  TileRegs regs;
+  auto tile_src = [&](int t, const uint16_t*& kb, const uint16_t*& vb, int64_t& skn, int64_t& svn,
+                      int& key0, int& limit, bool& ph1) {
+    ph1 = t < n1;
+    if (ph1) {
+      kb = kp_base; vb = vp_base; skn = a.skp_n; svn = a.svp_n; key0 = t * kTileN; limit = P;
+    } else {
+      kb = k_base; vb = v_base; skn = a.sk_n; svn = a.sv_n; key0 = ds + (t - n1) * kTileN; limit = a.Nk;
+    }
+  };
+
+  if (ntiles > 0) {
+    const uint16_t *kb, *vb; int64_t skn, svn; int key0, limit; bool ph1;
+    tile_src(0, kb, vb, skn, svn, key0, limit, ph1);
+    load_tile(regs, kb, vb, skn, svn, key0, limit, tid, meta && ph1, ts_row, cnt_row,
+              a.cnt_is_float, a.no_count, P, a.Nk + 1);
+    store_tile(regs, smem, tid, meta && ph1);
+  }
+  __syncthreads();
+
+  for (int t = 0; t < ntiles; ++t) {
+    char* stage = smem + (t & 1) * kStageBytes;
+    const bool has_next = t + 1 < ntiles;
+    bool next_ph1 = false;
+    if (has_next) {
+      const uint16_t *kb, *vb; int64_t skn, svn; int key0, limit;
+      tile_src(t + 1, kb, vb, skn, svn, key0, limit, next_ph1);
+      load_tile(regs, kb, vb, skn, svn, key0, limit, tid, meta && next_ph1, ts_row, cnt_row,
+                a.cnt_is_float, a.no_count, P, a.Nk + 1);
+    }
+
+    const bool ph1 = t < n1;
+    const int key0 = ph1 ? t * kTileN : ds + (t - n1) * kTileN;
+    // wave-uniform skip of tiles entirely above this wave's rows (causal)
+    const bool skip = !ph1 && a.causal && key0 > r0w + 31;
+    if (!skip) {
+      // ---- S^T = K Q^T for two 32-key blocks ----
+      f32x16 s[2];
+#pragma unroll
+      for (int kb2 = 0; kb2 < 2; ++kb2) {
+        s[kb2] = f32x16{};
+        const int krow = kb2 * 32 + ql;
+#pragma unroll
+        for (int tt = 0; tt < kD / 16; ++tt) {
+          const u32x4 w = *(const u32x4*)(stage + k_lds_off(krow, 2 * tt + hl));
+          s[kb2] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, w), qreg[tt],
+                                                            s[kb2], 0, 0, 0);
+        }
+      }
+      // ---- masks ----
+      const int row = r0w + ql;
+      if (VARIANT == kPure) {
+        const float* cl = (const float*)(stage + kCntOff);
+        const int* tl = (const int*)(stage + kTsOff);
+#pragma unroll
+        for (int kb2 = 0; kb2 < 2; ++kb2)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) {
+            const int kl = kb2 * 32 + 8 * (r >> 2) + 4 * hl + (r & 3);
+            const bool ok = cl[kl] > 0.0f && tl[kl] <= row;  // deltaFlashAttention.py:321-330
+            if (!ok) s[kb2][r] = -INFINITY;
+          }
+      } else if (!ph1) {
+        const bool need = (a.causal && key0 + kTileN - 1 > r0w) || key0 + kTileN > a.Nk;
+        if (need) {
+#pragma unroll
+          for (int kb2 = 0; kb2 < 2; ++kb2)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const int key = key0 + kb2 * 32 + 8 * (r >> 2) + 4 * hl + (r & 3);
+              const bool ok = key < a.Nk && (!a.causal || key <= row);
+              if (!ok) s[kb2][r] = -INFINITY;
+            }
+        }
+      }
+      // ---- online softmax ----
+      float mx = -INFINITY;
+#pragma unroll
+      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, fmaxf(s[0][r], s[1][r]));
+      mx = fmaxf(mx, swap_halves(mx));
+      const float m_new = fmaxf(m_i, mx);
+      const float m_use = (m_new == -INFINITY) ? 0.0f : m_new;
+      const float alpha = exp2_fast((m_i - m_use) * c);
+      const float neg = -m_use * c;
+      uint32_t pb[16];
+      float psum = 0.0f;
+      const bool weighted = (VARIANT == kPure) || (VARIANT == kHybrid && ph1);
+      const float* cl = (const float*)(stage + kCntOff);
+#pragma unroll
+      for (int kb2 = 0; kb2 < 2; ++kb2) {
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) {
+          f32x4 w4 = f32x4{1.0f, 1.0f, 1.0f, 1.0f};
+          if (weighted) w4 = *(const f32x4*)(cl + kb2 * 32 + 8 * r4 + 4 * hl);
+          float p[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            p[e] = exp2_fast(__builtin_fmaf(s[kb2][4 * r4 + e], c, neg));
+            if (weighted) p[e] *= w4[e];
+            psum += p[e];
+          }
+          pb[kb2 * 8 + 2 * r4] = pack_bf16x2(p[0], p[1]);
+          pb[kb2 * 8 + 2 * r4 + 1] = pack_bf16x2(p[2], p[3]);
+        }
+      }
+      l_i = l_i * alpha + psum;
+      m_i = m_new;
+      if (__ballot(alpha != 1.0f)) {
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+#pragma unroll
+          for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
+      }
+      // ---- O^T += V^T P^T ----
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int kb2 = u >> 1, half = u & 1;
+        u32x4 pw;
+        pw[0] = pb[kb2 * 8 + 4 * half + 0];
+        pw[1] = pb[kb2 * 8 + 4 * half + 1];
+        pw[2] = pb[kb2 * 8 + 4 * half + 2];
+        pw[3] = pb[kb2 * 8 + 4 * half + 3];
+        const bf16x8 pbv = __builtin_bit_cast(bf16x8, pw);
+#pragma unroll
+        for (int db = 0; db < 4; ++db) {
+          const int d = db * 32 + ql;
+          const u32x2 v0 = *(const u32x2*)(stage + vt_lds_off(d, 4 * u + hl));
+          const u32x2 v1 = *(const u32x2*)(stage + vt_lds_off(d, 4 * u + 2 + hl));
+          u32x4 vw;
+          vw[0] = v0[0]; vw[1] = v0[1]; vw[2] = v1[0]; vw[3] = v1[1];
+          o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, vw), pbv, o[db],
+                                                           0, 0, 0);
+        }
+      }
+    }
+    if (has_next) store_tile(regs, smem + ((t + 1) & 1) * kStageBytes, tid, meta && next_ph1);
+    __syncthreads();
+  }
+
+  // ---- finalize: out = acc / l ----
+  const float l_tot = l_i + swap_halves(l_i);
+  float inv;
+  if (VARIANT == kPure)
+    inv = l_tot > 0.0f ? 1.0f / l_tot : 1.0f;  // deltaFlashAttention.py:353-354
+  else
+    inv = 1.0f / l_tot;
+  const int row = r0w + ql;
+  if (row < a.Nq) {
+    uint16_t* orow = a.out + (int64_t)b * a.so_b + (int64_t)h * a.so_h + (int64_t)row * a.so_n;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        u32x2 w;
+        w[0] = pack_bf16x2(o[db][4 * j + 0] * inv, o[db][4 * j + 1] * inv);
+        w[1] = pack_bf16x2(o[db][4 * j + 2] * inv, o[db][4 * j + 3] * inv);
+        *(u32x2*)(orow + db * 32 + 8 * j + 4 * hl) = w;
+      }
+  }
+}
+
+// Per (batch, kv head): maxima of packed blocks of 128 timestamps (lanes at or
+// beyond P read seq_len_k + 1, deltaFlashAttention.py:70) and their prefix maxima.
+__global__ __launch_bounds__(256) void hybrid_schedule_kernel(const int32_t* __restrict__ ts,
+                                                              int64_t sts_b, int64_t sts_h,
+                                                              int Hkv, int P_host,
+                                                              const int32_t* P_dev, int Nk,
+                                                              int nblk_cap,
+                                                              int32_t* __restrict__ sched) {
+  __shared__ int32_t s_bmax[4096];
+  __shared__ int32_t s_wave[4];
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int bg = blockIdx.x;
+  const int b = bg / Hkv, g = bg - (bg / Hkv) * Hkv;
+  int P = P_host;
+  if (P_dev) P = min(*P_dev, P_host);
+  const int nblk = (P + kBlock - 1) / kBlock;
+  const int32_t* row = ts + (int64_t)b * sts_b + (int64_t)g * sts_h;
+  for (int jb = wid; jb < nblk; jb += 4) {
+    const int i0 = jb * kBlock + lane, i1 = i0 + 64;
+    int m = max(i0 < P ? row[i0] : Nk + 1, i1 < P ? row[i1] : Nk + 1);
+#pragma unroll
+    for (int d = 32; d >= 1; d >>= 1) m = max(m, __shfl_xor(m, d, 64));
+    if (lane == 0) s_bmax[jb] = m;
+  }
+  __syncthreads();
+  const int per = (nblk + 255) / 256;
+  const int j0 = min(tid * per, nblk), j1 = min(j0 + per, nblk);
+  int mloc = INT_MIN;
+  for (int j = j0; j < j1; ++j) mloc = max(mloc, s_bmax[j]);
+  int incl = mloc;
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int o = __shfl_up(incl, d, 64);
+    if (lane >= d) incl = max(incl, o);
+  }
+  if (lane == 63) s_wave[wid] = incl;
+  __syncthreads();
+  int pre = INT_MIN;
+  for (int w2 = 0; w2 < wid; ++w2) pre = max(pre, s_wave[w2]);
+  int excl = __shfl_up(incl, 1, 64);  // maximum over earlier lanes of this wave
+  if (lane == 0) excl = INT_MIN;
+  int run = max(pre, excl);
+  int32_t* bm = sched + (int64_t)bg * 2 * nblk_cap;
+  int32_t* pm = bm + nblk_cap;
+  for (int j = j0; j < j1; ++j) {
+    run = max(run, s_bmax[j]);
+    bm[j] = s_bmax[j];
+    pm[j] = run;
+  }
+}
+
+template <int V>
+static int allow_lds(size_t bytes) {
+  static int done = 0;
+  if (!done) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_kernel<V>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+    if (e != hipSuccess) return set_error(DA_ERR_HIP, "hipFuncSetAttribute: %s", hipGetErrorString(e));
+    done = 1;
+  }
+  return DA_OK;
+}
+
+static int launch_attn(int variant, AttnArgs& a, hipStream_t st) {
+  const size_t lds = 2 * kStageBytes;
+  const unsigned grid = (unsigned)((int64_t)a.n_row_groups * a.units);
+  int rc = DA_OK;
+  switch (variant) {
+    case kHybrid: rc = allow_lds<kHybrid>(lds); break;
+    case kSanity: rc = allow_lds<kSanity>(lds); break;
+    case kPure: rc = allow_lds<kPure>(lds); break;
+    default: rc = allow_lds<kDense>(lds); break;
+  }
+  if (rc) return rc;
+  switch (variant) {
+    case kHybrid:
+      hipLaunchKernelGGL(attn_kernel<kHybrid>, dim3(grid), dim3(256), lds, st, a);
+      break;
+    case kSanity:
+      hipLaunchKernelGGL(attn_kernel<kSanity>, dim3(grid), dim3(256), lds, st, a);
+      break;
+    case kPure:
+      hipLaunchKernelGGL(attn_kernel<kPure>, dim3(grid), dim3(256), lds, st, a);
+      break;
+    default:
+      hipLaunchKernelGGL(attn_kernel<kDense>, dim3(grid), dim3(256), lds, st, a);
+      break;
+  }
+  return check_launch("attention kernel");
+}
+
+static bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
+
+static int fill_common(AttnArgs& a, const void* q, const void* k, const void* v, void* out,
+                       int64_t B, int64_t Hq, int64_t Hkv, int64_t Nq, int64_t Nk, int64_t D,
+                       const int64_t* st, float scale, const char* who) {
+  DA_REQUIRE(q && k && v && out && st, "%s: null pointer", who);
+  DA_REQUIRE(B > 0 && Hq > 0 && Hkv > 0 && Nq > 0 && Nk > 0, "%s: empty shape", who);
+  if (D != kD) return set_error(DA_ERR_UNSUPPORTED, "%s: head_dim must be 128 (got %lld)", who, (long long)D);
+  DA_REQUIRE(Hq % Hkv == 0, "%s: Hq (%lld) must be a multiple of Hkv (%lld)", who, (long long)Hq, (long long)Hkv);
+  DA_REQUIRE(Nq < (1ll << 30) && Nk < (1ll << 30), "%s: sequence too long", who);
+  DA_REQUIRE(scale > 0.0f, "%s: scale must be positive", who);
+  for (int i = 0; i < 18; ++i)
+    DA_REQUIRE((st[i] & 7) == 0, "%s: strides must be multiples of 8 elements (stride %d = %lld)", who, i, (long long)st[i]);
+  DA_REQUIRE(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out), "%s: tensors must be 16-byte aligned", who);
+  a.q = (const uint16_t*)q; a.k = (const uint16_t*)k; a.v = (const uint16_t*)v; a.out = (uint16_t*)out;
+  a.sq_b = st[DA_STRIDE_Q]; a.sq_h = st[DA_STRIDE_Q + 1]; a.sq_n = st[DA_STRIDE_Q + 2];
+  a.sk_b = st[DA_STRIDE_K]; a.sk_h = st[DA_STRIDE_K + 1]; a.sk_n = st[DA_STRIDE_K + 2];
+  a.sv_b = st[DA_STRIDE_V]; a.sv_h = st[DA_STRIDE_V + 1]; a.sv_n = st[DA_STRIDE_V + 2];
+  a.so_b = st[DA_STRIDE_OUT]; a.so_h = st[DA_STRIDE_OUT + 1]; a.so_n = st[DA_STRIDE_OUT + 2];
+  a.B = (int)B; a.Hq = (int)Hq; a.Hkv = (int)Hkv; a.G = (int)(Hq / Hkv);
+  a.Nq = (int)Nq; a.Nk = (int)Nk;
+  a.scale_log2 = scale * 1.4426950408889634f;
+  a.hpw = (a.G % 4 == 0) ? 4 : (a.G % 2 == 0 ? 2 : 1);
+  a.rows_per_wg = 32 * (4 / a.hpw);
+  a.n_row_groups = (int)((Nq + a.rows_per_wg - 1) / a.rows_per_wg);
+  a.units = (int)(B * Hkv * (a.G / a.hpw));
+  DA_REQUIRE((int64_t)a.n_row_groups * a.units < (1ll << 31), "%s: grid too large", who);
+  return DA_OK;
+}
+
+}  // namespace da
+
+using namespace da;
+
+extern "C" int64_t da_hybrid_workspace_size(int64_t B, int64_t Hkv, int64_t num_packed) {
+  const int64_t nblk = (num_packed + kBlock - 1) / kBlock;
+  return B * Hkv * 2 * (nblk > 0 ? nblk : 1) * (int64_t)sizeof(int32_t);
+}
+
+extern "C" int da_hybrid_prefill(const void* q, const void* k, const void* v, const void* k_packed,
+                                 const void* v_packed, const int32_t* timestamps,
+                                 const void* counts, int counts_dtype, void* out, int dtype,
+                                 int64_t B, int64_t Hq, int64_t Hkv, int64_t Nq, int64_t Nk,
+                                 int64_t D, const int64_t* strides, int64_t num_packed,
+                                 const int32_t* num_packed_dev, int64_t window, float scale,
+                                 int variant, int no_count, void* workspace,
+                                 int64_t workspace_bytes, void* stream) {
+  if (dtype != DA_BF16) return set_error(DA_ERR_UNSUPPORTED, "da_hybrid_prefill: only bf16 is supported");
+  AttnArgs a = {};
+  int rc = fill_common(a, q, k, v, out, B, Hq, Hkv, Nq, Nk, D, strides, scale, "da_hybrid_prefill");
+  if (rc) return rc;
+  DA_REQUIRE(variant == DA_VARIANT_HYBRID || variant == DA_VARIANT_SANITY ||
+                 variant == DA_VARIANT_PURE_PHASE1,
+             "da_hybrid_prefill: unknown variant %d", variant);
+  DA_REQUIRE(k_packed && v_packed && timestamps && counts, "da_hybrid_prefill: null packed tensor");
+  DA_REQUIRE(counts_dtype == DA_I32 || counts_dtype == DA_F32, "da_hybrid_prefill: counts must be int32 or fp32");
+  DA_REQUIRE(num_packed > 0 && num_packed <= 4096 * kBlock, "da_hybrid_prefill: num_packed must be in [1, %d]", 4096 * kBlock);
+  DA_REQUIRE(window >= 0 && window < (1ll << 30), "da_hybrid_prefill: window must be >= 0");
+  DA_REQUIRE(aligned16(k_packed) && aligned16(v_packed), "da_hybrid_prefill: packed tensors must be 16-byte aligned");
+  DA_REQUIRE(strides[DA_STRIDE_TS + 2] == 1 && strides[DA_STRIDE_CNT + 2] == 1,
+             "da_hybrid_prefill: timestamps and counts must be contiguous along the packed axis");
+  if (!workspace || workspace_bytes < da_hybrid_workspace_size(B, Hkv, num_packed))
+    return set_error(DA_ERR_WORKSPACE, "da_hybrid_prefill: workspace of %lld bytes required",
+                     (long long)da_hybrid_workspace_size(B, Hkv, num_packed));
+  a.kp = (const uint16_t*)k_packed; a.vp = (const uint16_t*)v_packed;
+  a.ts = timestamps; a.cnt = counts;
+  a.skp_b = strides[DA_STRIDE_KP]; a.skp_h = strides[DA_STRIDE_KP + 1]; a.skp_n = strides[DA_STRIDE_KP + 2];
+  a.svp_b = strides[DA_STRIDE_VP]; a.svp_h = strides[DA_STRIDE_VP + 1]; a.svp_n = strides[DA_STRIDE_VP + 2];
+  a.sts_b = strides[DA_STRIDE_TS]; a.sts_h = strides[DA_STRIDE_TS + 1];
+  a.scnt_b = strides[DA_STRIDE_CNT]; a.scnt_h = strides[DA_STRIDE_CNT + 1];
+  a.P_host = (int)num_packed;
+  a.P_dev = num_packed_dev;
+  a.window = (int)window;
+  a.no_count = no_count ? 1 : 0;
+  a.cnt_is_float = counts_dtype == DA_F32;
+  a.causal = 1;
+  a.nblk_cap = (int)((num_packed + kBlock - 1) / kBlock);
+  a.sched = (const int32_t*)workspace;
+  hipStream_t st = (hipStream_t)stream;
+  if (variant != DA_VARIANT_PURE_PHASE1) {
+    hipLaunchKernelGGL(hybrid_schedule_kernel, dim3((unsigned)(B * Hkv)), dim3(256), 0, st,
+                       timestamps, a.sts_b, a.sts_h, (int)Hkv, (int)num_packed, num_packed_dev,
+                       (int)Nk, a.nblk_cap, (int32_t*)workspace);
+    rc = check_launch("da_hybrid_prefill(schedule)");
+    if (rc) return rc;
+  }
+  const int kv = variant == DA_VARIANT_HYBRID ? kHybrid : (variant == DA_VARIANT_SANITY ? kSanity : kPure);
+  return launch_attn(kv, a, st);
+}
+
+extern "C" int da_dense_prefill(const void* q, const void* k, const void* v, void* out, int dtype,
+                                int64_t B, int64_t Hq, int64_t Hkv, int64_t Nq, int64_t Nk,
+                                int64_t D, const int64_t* strides, int causal, float scale,
+                                void* stream) {
+  if (dtype != DA_BF16) return set_error(DA_ERR_UNSUPPORTED, "da_dense_prefill: only bf16 is supported");
+  AttnArgs a = {};
+  int rc = fill_common(a, q, k, v, out, B, Hq, Hkv, Nq, Nk, D, strides, scale, "da_dense_prefill");
+  if (rc) return rc;
+  a.kp = a.k; a.vp = a.v;
+  a.causal = causal ? 1 : 0;
+  a.P_host = 0;
+  return launch_attn(kDense, a, (hipStream_t)stream);
+}

@@ -1,0 +1,256 @@
+// Index + pack + counts on gfx950, fused and free of host synchronisation.
+//
+// Replaces index_map = cumsum(keep) - 1 and P = max count with its .item()
+// (modeling_llama.py:655-656), parallel_scatter_pack_kv_kernel
+// (tritonModules.py:72-132, launch modeling_llama.py:658-680) and the run-length
+// scatter_add_ (modeling_llama.py:682-685).
+//
+// pack_scan_kernel (one workgroup per (batch, kv head)): the keep mask is read in
+// 64-row groups; a ballot gives each group's anchor count and first anchor.  A
+// block-wide exclusive scan gives every group's first packed index and a suffix
+// minimum gives the first anchor after each group, which ends the run of the
+// group's last anchor.  The head's anchor count c goes to anchor_counts.
+//
+// pack_scatter_kernel (one wave per 64-row group): rank = popcount of the lower
+// keep bits, packed index = group offset + rank, timestamp = row, count = next
+// anchor - row (the number of rows index_map sends to this anchor).  The wave
+// copies the anchor rows of K and V (one coalesced row per step) and every
+// workgroup zero-fills its share of the padding rows [c, P) of its head, so the
+// packed tensors equal the reference's zero-initialised ones.  P = max_g c_g is
+// computed on the device and written to num_packed.
+#include "da_common.hpp"
+
+namespace da {
+
+constexpr int kMaxGroups = 8192;  // N <= 524288
+
+__device__ __forceinline__ int wave_incl_scan_add(int v, int lane) {
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int o = __shfl_up(v, d, 64);
+    if (lane >= d) v += o;
+  }
+  return v;
+}
+
+__device__ __forceinline__ int wave_incl_scan_min(int v, int lane) {
+#pragma unroll
+  for (int d = 1; d < 64; d <<= 1) {
+    const int o = __shfl_up(v, d, 64);
+    if (lane >= d) v = min(v, o);
+  }
+  return v;
+}
+
+__device__ __forceinline__ int wave_reduce_max(int v) {
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) v = max(v, __shfl_xor(v, d, 64));
+  return v;
+}
+
+__global__ __launch_bounds__(256) void pack_scan_kernel(const int32_t* __restrict__ keep,
+                                                        int64_t N, int ngroups,
+                                                        int32_t* __restrict__ ws_off,
+                                                        int32_t* __restrict__ ws_next,
+                                                        int32_t* __restrict__ anchor_counts) {
+  __shared__ int32_t s_info[kMaxGroups];  // count | first << 8
+  __shared__ int32_t s_wave[4];
+  __shared__ int32_t s_suffix[256];
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int64_t bh = blockIdx.x;
+  const int32_t* krow = keep + bh * N;
+
+  for (int g = wid; g < ngroups; g += 4) {
+    const int64_t r = (int64_t)g * 64 + lane;
+    const bool kp = r < N && krow[r] != 0;
+    const uint64_t bits = __ballot(kp);
+    if (lane == 0) {
+      const int cnt = __popcll(bits);
+      const int first = bits ? __builtin_ctzll(bits) : 64;
+      s_info[g] = cnt | (first << 8);
+    }
+  }
+  __syncthreads();
+
+  // Each thread owns a contiguous slice of groups.
+  const int per = (ngroups + 255) / 256;
+  const int g0 = min(tid * per, ngroups), g1 = min(g0 + per, ngroups);
+  int sum = 0;
+  int first_pos = (int)N;  // first anchor inside the slice (N if none)
+  for (int g = g1 - 1; g >= g0; --g) {
+    const int info = s_info[g];
+    sum += info & 0xff;
+    if (info & 0xff) first_pos = g * 64 + (info >> 8);
+  }
+  // exclusive prefix sum of the slice sums
+  int incl = wave_incl_scan_add(sum, lane);
+  if (lane == 63) s_wave[wid] = incl;
+  __syncthreads();
+  int wave_prefix = 0;
+  for (int w2 = 0; w2 < wid; ++w2) wave_prefix += s_wave[w2];
+  const int total = s_wave[0] + s_wave[1] + s_wave[2] + s_wave[3];
+  int run = wave_prefix + incl - sum;
+  __syncthreads();
+  // suffix minimum of first_pos over later slices: scan the reversed sequence
+  s_suffix[tid] = first_pos;
+  __syncthreads();
+  const int rv = s_suffix[255 - tid];
+  int rincl = wave_incl_scan_min(rv, lane);
+  if (lane == 63) s_wave[wid] = rincl;
+  __syncthreads();
+  int rpre = (int)N;
+  for (int w2 = 0; w2 < wid; ++w2) rpre = min(rpre, s_wave[w2]);
+  rincl = min(rincl, rpre);  // min over original slices [255 - tid, 255]
+  __syncthreads();
+  s_suffix[255 - tid] = rincl;
+  __syncthreads();
+  int nxt = (tid < 255) ? s_suffix[tid + 1] : (int)N;
+
+  int32_t* off_row = ws_off + bh * ngroups;
+  int32_t* next_row = ws_next + bh * ngroups;
+  for (int g = g0; g < g1; ++g) {
+    off_row[g] = run;
+    run += s_info[g] & 0xff;
+  }
+  for (int g = g1 - 1; g >= g0; --g) {
+    next_row[g] = nxt;
+    const int info = s_info[g];
+    if (info & 0xff) nxt = g * 64 + (info >> 8);
+  }
+  if (tid == 0) anchor_counts[bh] = total;
+}
+
+__global__ __launch_bounds__(256) void pack_scatter_kernel(
+    const int32_t* __restrict__ keep, const uint16_t* __restrict__ k,
+    const uint16_t* __restrict__ v, int64_t sk_b, int64_t sk_h, int64_t sk_n, int64_t sv_b,
+    int64_t sv_h, int64_t sv_n, int Hkv, int64_t N, int D, int ngroups, int BH,
+    int64_t capacity, const int32_t* __restrict__ ws_off, const int32_t* __restrict__ ws_next,
+    const int32_t* __restrict__ anchor_counts, uint16_t* __restrict__ kp,
+    uint16_t* __restrict__ vp, int32_t* __restrict__ ts, int32_t* __restrict__ cnt,
+    int32_t* __restrict__ num_packed) {
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int64_t bh = blockIdx.y;
+  const int64_t b = bh / Hkv, h = bh - (bh / Hkv) * Hkv;
+  const int g = blockIdx.x * 4 + wid;
+
+  int P = 0;
+  for (int i = lane; i < BH; i += 64) P = max(P, anchor_counts[i]);
+  P = wave_reduce_max(P);
+  const int c = anchor_counts[bh];
+  if (blockIdx.x == 0 && blockIdx.y == 0 && tid == 0) *num_packed = P;
+
+  const int64_t prow = bh * capacity;  // first packed row of this head
+  const int nw = D >> 1;               // 4-byte words per row
+  if (g < ngroups) {
+    const int64_t r = (int64_t)g * 64 + lane;
+    const bool is_anchor = r < N && keep[bh * N + r] != 0;
+    const uint64_t bits = __ballot(is_anchor);
+    const int off = ws_off[bh * ngroups + g];
+    if (is_anchor) {
+      const int rank = __popcll(bits & ((1ull << lane) - 1ull));
+      const uint64_t higher = (lane == 63) ? 0ull : (bits >> (lane + 1)) << (lane + 1);
+      const int next = higher ? g * 64 + __builtin_ctzll(higher) : ws_next[bh * ngroups + g];
+      const int64_t dst = off + rank;
+      if (dst < capacity) {
+        ts[prow + dst] = (int32_t)r;                // tritonModules.py:131-132
+        cnt[prow + dst] = (int32_t)(next - r);      // modeling_llama.py:683-685
+      }
+    }
+    // Copy the anchor rows; four rows per step to keep loads in flight.
+    const uint16_t* kbase = k + b * sk_b + h * sk_h + 2 * lane;
+    const uint16_t* vbase = v + b * sv_b + h * sv_h + 2 * lane;
+    const bool act = lane < nw;
+    uint64_t rem = bits;
+    int64_t dst = off;
+    while (rem) {
+      int rows[4];
+      int nr = 0;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        rows[j] = rem ? (int)__builtin_ctzll(rem) : -1;
+        if (rem) {
+          rem &= rem - 1ull;
+          ++nr;
+        }
+      }
+      uint32_t kw[4], vw[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int64_t src = (int64_t)g * 64 + rows[j];
+        kw[j] = (act && j < nr) ? *(const uint32_t*)(kbase + src * sk_n) : 0u;
+        vw[j] = (act && j < nr) ? *(const uint32_t*)(vbase + src * sv_n) : 0u;
+      }
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int64_t d = dst + j;
+        if (act && j < nr && d < capacity) {
+          *(uint32_t*)(kp + (prow + d) * D + 2 * lane) = kw[j];
+          *(uint32_t*)(vp + (prow + d) * D + 2 * lane) = vw[j];
+        }
+      }
+      dst += nr;
+    }
+  }
+
+  // Zero padding rows [c, min(P, capacity)) of this head, 256 rows per workgroup.
+  const int64_t pad_end = (P < capacity) ? P : capacity;
+  const int64_t r0 = (int64_t)c + (int64_t)blockIdx.x * 256;
+  for (int i = tid; i < 256 * nw; i += 256) {
+    const int64_t row = r0 + i / nw;
+    const int wd = i % nw;
+    if (row < pad_end) {
+      *(uint32_t*)(kp + (prow + row) * D + 2 * wd) = 0u;
+      *(uint32_t*)(vp + (prow + row) * D + 2 * wd) = 0u;
+      if (wd == 0) {
+        ts[prow + row] = 0;
+        cnt[prow + row] = 0;
+      }
+    }
+  }
+}
+
+}  // namespace da
+
+using namespace da;
+
+extern "C" int64_t da_pack_workspace_size(int64_t B, int64_t Hkv, int64_t N) {
+  const int64_t ngroups = (N + 63) / 64;
+  return 2 * B * Hkv * ngroups * (int64_t)sizeof(int32_t);
+}
+
+extern "C" int da_pack(const int32_t* keep, const void* k, const void* v, int dtype, int64_t B,
+                       int64_t Hkv, int64_t N, int64_t D, int64_t sk_b, int64_t sk_h, int64_t sk_n,
+                       int64_t sv_b, int64_t sv_h, int64_t sv_n, int64_t capacity, void* k_packed,
+                       void* v_packed, int32_t* timestamps, int32_t* counts,
+                       int32_t* anchor_counts, int32_t* num_packed, void* workspace,
+                       int64_t workspace_bytes, void* stream) {
+  DA_REQUIRE(keep && k && v && k_packed && v_packed && timestamps && counts && anchor_counts &&
+                 num_packed,
+             "da_pack: null pointer");
+  if (dtype != DA_BF16) return set_error(DA_ERR_UNSUPPORTED, "da_pack: only bf16 is supported");
+  DA_REQUIRE(B > 0 && Hkv > 0 && N > 0 && D > 0 && capacity > 0, "da_pack: empty shape");
+  if (D > 128 || (D & 1)) return set_error(DA_ERR_UNSUPPORTED, "da_pack: head_dim must be even and <= 128");
+  const int64_t ngroups = (N + 63) / 64;
+  if (ngroups > kMaxGroups) return set_error(DA_ERR_UNSUPPORTED, "da_pack: sequence longer than %d", kMaxGroups * 64);
+  DA_REQUIRE(B * Hkv < 65536, "da_pack: too many heads");
+  DA_REQUIRE(((sk_b | sk_h | sk_n | sv_b | sv_h | sv_n) & 1) == 0 && ((uintptr_t)k & 3) == 0 &&
+                 ((uintptr_t)v & 3) == 0 && ((uintptr_t)k_packed & 3) == 0 &&
+                 ((uintptr_t)v_packed & 3) == 0,
+             "da_pack: rows must be 4-byte aligned");
+  if (!workspace || workspace_bytes < da_pack_workspace_size(B, Hkv, N))
+    return set_error(DA_ERR_WORKSPACE, "da_pack: workspace of %lld bytes required",
+                     (long long)da_pack_workspace_size(B, Hkv, N));
+  hipStream_t st = (hipStream_t)stream;
+  int32_t* ws_off = (int32_t*)workspace;
+  int32_t* ws_next = ws_off + B * Hkv * ngroups;
+  hipLaunchKernelGGL(pack_scan_kernel, dim3((unsigned)(B * Hkv)), dim3(256), 0, st, keep, N,
+                     (int)ngroups, ws_off, ws_next, anchor_counts);
+  int rc = check_launch("da_pack(scan)");
+  if (rc) return rc;
+  hipLaunchKernelGGL(pack_scatter_kernel, dim3((unsigned)((ngroups + 3) / 4), (unsigned)(B * Hkv)),
+                     dim3(256), 0, st, keep, (const uint16_t*)k, (const uint16_t*)v, sk_b, sk_h,
+                     sk_n, sv_b, sv_h, sv_n, (int)Hkv, N, (int)D, (int)ngroups, (int)(B * Hkv),
+                     capacity, ws_off, ws_next, anchor_counts, (uint16_t*)k_packed,
+                     (uint16_t*)v_packed, timestamps, counts, num_packed);
+  return check_launch("da_pack(scatter)");
+}

@@ -1,0 +1,247 @@
+"""Native DeltaAttention prefill operations on torch tensors (ROCm, gfx950).
+
+Every operation calls libdeltaattn.so through its C ABI on the current HIP stream;
+tensors only provide device memory and streams.  There is no CPU fallback.
+
+Layouts follow the reference: K, V are [B, Hkv, N, D] (post-RoPE keys), Q and the
+output are [B, Hq, N, D]; query head h uses KV head h // (Hq // Hkv), which is what
+``repeat_kv`` materialises in the reference (modeling_llama.py:223-232) -- here it is
+never materialised.
+"""
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+from typing import Optional, Tuple
+
+import torch
+
+from . import _native
+from ._native import DA_BF16, DA_F32, DA_I32, DA_VARIANT, check, lib, strides_array
+
+__all__ = ["PackedKV", "chunking", "select", "pack", "hybrid_prefill", "dense_prefill",
+           "delta_prefill"]
+
+
+def _stream() -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _require_device(*ts: torch.Tensor) -> None:
+    for t in ts:
+        if t is not None and t.device.type != "cuda":
+            raise ValueError("deltaattention_amd operations take GPU tensors "
+                             f"(got a tensor on {t.device}); there is no CPU path")
+
+
+def _require_bf16(*ts: torch.Tensor) -> None:
+    for t in ts:
+        if t.dtype != torch.bfloat16:
+            raise TypeError(f"expected bfloat16 tensors, got {t.dtype}")
+
+
+def _last_dim_contig(t: torch.Tensor) -> torch.Tensor:
+    return t if t.stride(-1) == 1 else t.contiguous()
+
+
+def chunking(seq_len: int, chunk_size: int = 0, divide_to: int = 0) -> Tuple[int, int]:
+    """(chunk size, chunk count) as modeling_llama.py:602-610 computes them."""
+    if seq_len <= 0:
+        raise ValueError("seq_len must be positive")
+    if chunk_size > 0:
+        cs = min(chunk_size, seq_len)
+        return cs, max(1, (seq_len + cs - 1) // cs)
+    parts = 1 if divide_to == 0 else divide_to
+    return (seq_len + parts - 1) // parts, parts
+
+
+def select(k: torch.Tensor, threshold: float, chunk_size: int = 512, divide_to: int = 0,
+           metric: str = "euclidean", keep: Optional[torch.Tensor] = None,
+           chunk_counts: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Delta-mode anchor selection (tritonModules.py:7-69 via modeling_llama.py:634-653).
+
+    ``metric == "cosine"`` selects the cosine test (keep iff cos < threshold); every
+    other string is Euclidean (keep iff ||k - anchor||^2 > threshold^2), exactly as
+    modeling_llama.py:639-642.  Returns keep [B, Hkv, N] int32 and chunk counts
+    [B, Hkv, num_chunks] int32.
+    """
+    _require_device(k)
+    _require_bf16(k)
+    k = _last_dim_contig(k)
+    B, H, N, D = k.shape
+    cs, nc = chunking(N, chunk_size, divide_to)
+    use_cos = metric == "cosine"
+    thr = float(threshold) if use_cos else float(threshold) ** 2
+    if keep is None:
+        keep = torch.zeros((B, H, N), dtype=torch.int32, device=k.device)
+    if chunk_counts is None:
+        chunk_counts = torch.empty((B, H, nc), dtype=torch.int32, device=k.device)
+    rc = lib().da_select(k.data_ptr(), DA_BF16, B, H, N, D, k.stride(0), k.stride(1), k.stride(2),
+                         ctypes.c_float(thr), 1 if use_cos else 0, cs, nc, keep.data_ptr(),
+                         chunk_counts.data_ptr(), _stream())
+    check(rc, "da_select")
+    return keep, chunk_counts
+
+
+@dataclass
+class PackedKV:
+    """Packed anchors of every (batch, kv head).
+
+    k_packed/v_packed [B, Hkv, capacity, D], timestamps/counts [B, Hkv, capacity] int32;
+    rows [0, c) hold the anchors of a head, rows [c, P) are zero padding, rows at or
+    beyond P are not defined.  anchor_counts [B, Hkv] int32 holds c, num_packed [1]
+    int32 holds P = max c on the device (no host synchronisation).
+    """
+    k_packed: torch.Tensor
+    v_packed: torch.Tensor
+    timestamps: torch.Tensor
+    counts: torch.Tensor
+    anchor_counts: torch.Tensor
+    num_packed: torch.Tensor
+
+    @property
+    def capacity(self) -> int:
+        return self.k_packed.shape[2]
+
+    def trimmed(self) -> "PackedKV":
+        """Views cut to P rows (reads P back to the host, as modeling_llama.py:656)."""
+        P = int(self.num_packed.item())
+        return PackedKV(self.k_packed[:, :, :P], self.v_packed[:, :, :P],
+                        self.timestamps[:, :, :P], self.counts[:, :, :P],
+                        self.anchor_counts, self.num_packed)
+
+
+def pack(keep: torch.Tensor, k: torch.Tensor, v: torch.Tensor, capacity: Optional[int] = None,
+         out: Optional[PackedKV] = None) -> PackedKV:
+    """Index + pack + counts (modeling_llama.py:655-685, tritonModules.py:72-132).
+
+    ``capacity`` (rows per head of the outputs) defaults to N, which always holds every
+    anchor, so nothing waits for P on the host.
+    """
+    _require_device(keep, k, v)
+    _require_bf16(k, v)
+    k, v = _last_dim_contig(k), _last_dim_contig(v)
+    keep = keep.contiguous()
+    if keep.dtype != torch.int32:
+        keep = keep.to(torch.int32)
+    B, H, N, D = k.shape
+    if capacity is None:
+        capacity = N if out is None else out.capacity
+    dev = k.device
+    if out is None:
+        out = PackedKV(
+            torch.empty((B, H, capacity, D), dtype=k.dtype, device=dev),
+            torch.empty((B, H, capacity, D), dtype=v.dtype, device=dev),
+            torch.empty((B, H, capacity), dtype=torch.int32, device=dev),
+            torch.empty((B, H, capacity), dtype=torch.int32, device=dev),
+            torch.empty((B, H), dtype=torch.int32, device=dev),
+            torch.empty((1,), dtype=torch.int32, device=dev))
+    for t in (out.k_packed, out.v_packed, out.timestamps, out.counts):
+        if not t.is_contiguous():
+            raise ValueError("packed outputs must be contiguous")
+    ws_bytes = lib().da_pack_workspace_size(B, H, N)
+    ws = torch.empty((max(1, ws_bytes),), dtype=torch.uint8, device=dev)
+    rc = lib().da_pack(keep.data_ptr(), k.data_ptr(), v.data_ptr(), DA_BF16, B, H, N, D,
+                       k.stride(0), k.stride(1), k.stride(2), v.stride(0), v.stride(1),
+                       v.stride(2), out.capacity, out.k_packed.data_ptr(), out.v_packed.data_ptr(),
+                       out.timestamps.data_ptr(), out.counts.data_ptr(),
+                       out.anchor_counts.data_ptr(), out.num_packed.data_ptr(), ws.data_ptr(),
+                       ws_bytes, _stream())
+    check(rc, "da_pack")
+    return out
+
+
+def _attn_strides(q, k, v, out, kp=None, vp=None, ts=None, cnt=None):
+    vals = [0] * 24
+    for base, t in ((0, q), (3, k), (6, v), (9, kp), (12, vp), (15, out)):
+        if t is not None:
+            vals[base:base + 3] = [t.stride(0), t.stride(1), t.stride(2)]
+    for base, t in ((18, ts), (21, cnt)):
+        if t is not None:
+            vals[base:base + 3] = [t.stride(0), t.stride(1), t.stride(2)]
+    return strides_array(vals)
+
+
+def hybrid_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, k_packed: torch.Tensor,
+                   v_packed: torch.Tensor, timestamps: torch.Tensor, counts: torch.Tensor,
+                   window: int = 128, scale: Optional[float] = None, variant: str = "hybrid",
+                   no_count: bool = False, num_packed_dev: Optional[torch.Tensor] = None,
+                   out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Two-phase compressed prefill (deltaFlashAttention.py:9-357) with GQA indexing.
+
+    k_packed etc. hold P = k_packed.shape[2] rows per head (or, when ``num_packed_dev``
+    is given, that many of them); counts may be int32 or float32.
+    """
+    if variant not in DA_VARIANT:
+        raise ValueError(f"variant must be one of {sorted(DA_VARIANT)}")
+    _require_device(q, k, v, k_packed, v_packed, timestamps, counts)
+    _require_bf16(q, k, v, k_packed, v_packed)
+    q, k, v = _last_dim_contig(q), _last_dim_contig(k), _last_dim_contig(v)
+    k_packed, v_packed = _last_dim_contig(k_packed), _last_dim_contig(v_packed)
+    timestamps = _last_dim_contig(timestamps)
+    counts = _last_dim_contig(counts)
+    if timestamps.dtype != torch.int32:
+        timestamps = timestamps.to(torch.int32)
+    if counts.dtype not in (torch.int32, torch.float32):
+        counts = counts.to(torch.float32)
+    B, Hq, Nq, D = q.shape
+    Hkv, Nk = k.shape[1], k.shape[2]
+    P = k_packed.shape[2]
+    if scale is None:
+        scale = D ** -0.5
+    if out is None:
+        out = torch.empty_like(q)
+    ws_bytes = lib().da_hybrid_workspace_size(B, Hkv, max(P, 1))
+    ws = torch.empty((max(1, ws_bytes),), dtype=torch.uint8, device=q.device)
+    st = _attn_strides(q, k, v, out, k_packed, v_packed, timestamps, counts)
+    rc = lib().da_hybrid_prefill(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), k_packed.data_ptr(), v_packed.data_ptr(),
+        timestamps.data_ptr(), counts.data_ptr(),
+        DA_F32 if counts.dtype == torch.float32 else DA_I32, out.data_ptr(), DA_BF16,
+        B, Hq, Hkv, Nq, Nk, D, st, P, _ptr(num_packed_dev), int(window), ctypes.c_float(scale),
+        DA_VARIANT[variant], 1 if no_count else 0, ws.data_ptr(), ws_bytes, _stream())
+    check(rc, "da_hybrid_prefill")
+    return out
+
+
+def dense_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: bool = True,
+                  scale: Optional[float] = None, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Dense flash prefill (flashAttention.py:5-130) with GQA indexing."""
+    _require_device(q, k, v)
+    _require_bf16(q, k, v)
+    q, k, v = _last_dim_contig(q), _last_dim_contig(k), _last_dim_contig(v)
+    B, Hq, Nq, D = q.shape
+    Hkv, Nk = k.shape[1], k.shape[2]
+    if scale is None:
+        scale = D ** -0.5
+    if out is None:
+        out = torch.empty_like(q)
+    st = _attn_strides(q, k, v, out)
+    rc = lib().da_dense_prefill(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), DA_BF16,
+                                B, Hq, Hkv, Nq, Nk, D, st, 1 if causal else 0,
+                                ctypes.c_float(scale), _stream())
+    check(rc, "da_dense_prefill")
+    return out
+
+
+def delta_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, threshold: float,
+                  chunk_size: int = 512, divide_to: int = 0, metric: str = "euclidean",
+                  window: int = 128, scale: Optional[float] = None, variant: str = "hybrid",
+                  no_count: bool = False, keep: Optional[torch.Tensor] = None,
+                  return_packed: bool = False):
+    """select -> pack -> hybrid prefill with P kept on the device (no host sync).
+
+    Restates PATH 1 of LlamaAttention.forward (modeling_llama.py:600-749) for the delta
+    packing mode; pass ``keep`` to use a mask from another packing mode.
+    """
+    if keep is None:
+        keep, _ = select(k, threshold, chunk_size, divide_to, metric)
+    packed = pack(keep, k, v)
+    out = hybrid_prefill(q, k, v, packed.k_packed, packed.v_packed, packed.timestamps,
+                         packed.counts, window=window, scale=scale, variant=variant,
+                         no_count=no_count, num_packed_dev=packed.num_packed)
+    return (out, packed) if return_packed else out

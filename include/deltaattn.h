@@ -1,0 +1,150 @@
+/*
+ * deltaattn.h -- C ABI of the MI355X (gfx950) DeltaAttention prefill path.
+ *
+ * Every entry point takes raw device pointers, int64 element strides for the
+ * (batch, head, sequence) dimensions (the head dimension must be contiguous),
+ * sizes, and a hipStream_t passed as void*.  Nothing allocates device memory:
+ * scratch space comes in through a caller-provided workspace whose size the
+ * matching *_workspace_size function returns.  Calls enqueue work on the given
+ * stream and return without synchronising.  The library is stateless and
+ * reentrant; the only per-thread state is the text of the last error.
+ *
+ * Return value: DA_OK (0) or a negative DA_ERR_* code; da_last_error() then
+ * holds a message.
+ *
+ * The reference (Emruur/DeltaAttention) is Python + Triton with no FFI; each
+ * entry point names the reference kernel/launch it replaces.
+ */
+#ifndef DELTAATTN_H
+#define DELTAATTN_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DA_OK 0
+#define DA_ERR_INVALID (-1)     /* bad argument (shape, stride, null pointer) */
+#define DA_ERR_UNSUPPORTED (-2) /* valid but not implemented (dtype, head_dim) */
+#define DA_ERR_HIP (-3)         /* HIP runtime error while launching */
+#define DA_ERR_WORKSPACE (-4)   /* workspace missing or too small */
+
+/* element types */
+#define DA_BF16 1
+#define DA_I32 3
+#define DA_F32 4
+
+/* attention variants (deltaFlashAttention.py kernels) */
+#define DA_VARIANT_HYBRID 0      /* hybrid_compressed_flash_kernel, :9-146 */
+#define DA_VARIANT_SANITY 1      /* hybrid_compressed_flash_kernel_sanity, :149-259 */
+#define DA_VARIANT_PURE_PHASE1 2 /* pure_phase1_flash_kernel, :262-357 */
+
+/* Text of the last error on the calling thread ("" when none). */
+const char* da_last_error(void);
+
+/* ABI version of this library. */
+int da_version(void);
+
+/*
+ * Delta-mode anchor selection.  Replaces chunked_eval_kernel
+ * (tritonModules.py:7-69) and its launch (modeling_llama.py:634-653).
+ *
+ * k: [B, Hkv, N, D] bf16, strides (sk_b, sk_h, sk_n), D even and <= 128.
+ * threshold: tau^2 for Euclidean, tau for cosine (modeling_llama.py:641-642).
+ * chunk_size / num_chunks: from the chunking rule of modeling_llama.py:602-610.
+ * keep: [B, Hkv, N] int32 contiguous, 1 for anchors and 0 otherwise (rows of
+ *   chunks that start at or beyond N are not written).
+ * chunk_counts: [B, Hkv, num_chunks] int32 contiguous (0 for empty chunks).
+ * The squared distance (or cosine) is fp32 over a fixed pairwise reduction
+ * tree, so the result is deterministic and bit-identical to the CPU oracle.
+ */
+int da_select(const void* k, int dtype, int64_t B, int64_t Hkv, int64_t N, int64_t D,
+              int64_t sk_b, int64_t sk_h, int64_t sk_n, float threshold, int use_cosine,
+              int64_t chunk_size, int64_t num_chunks, int32_t* keep, int32_t* chunk_counts,
+              void* stream);
+
+/*
+ * Index + pack + counts.  Replaces index_map / P (modeling_llama.py:655-656),
+ * parallel_scatter_pack_kv_kernel (tritonModules.py:72-132, launch
+ * modeling_llama.py:658-680) and the count scatter_add_ (:682-685), fused, with
+ * P kept on the device (no host synchronisation).
+ *
+ * keep: [B, Hkv, N] int32 contiguous; keep[..., 0] must be 1 (every mode of the
+ *   reference guarantees it, modeling_llama.py:623/630 and tritonModules.py:41).
+ * k, v: [B, Hkv, N, D] bf16 with strides (s*_b, s*_h, s*_n).
+ * capacity: rows allocated per head in the packed outputs; must be >= P
+ *   (N always suffices).
+ * k_packed, v_packed: [B, Hkv, capacity, D] contiguous; rows [0, c) receive the
+ *   anchor rows, rows [c, P) are zero-filled (the reference's zero padding).
+ * timestamps, counts: [B, Hkv, capacity] int32 contiguous: anchor position and run
+ *   length; padding rows get 0.
+ * anchor_counts: [B, Hkv] int32 (c per head); num_packed: [1] int32 (P).
+ * workspace: da_pack_workspace_size() bytes of device memory.
+ */
+int64_t da_pack_workspace_size(int64_t B, int64_t Hkv, int64_t N);
+int da_pack(const int32_t* keep, const void* k, const void* v, int dtype, int64_t B,
+            int64_t Hkv, int64_t N, int64_t D, int64_t sk_b, int64_t sk_h, int64_t sk_n,
+            int64_t sv_b, int64_t sv_h, int64_t sv_n, int64_t capacity, void* k_packed,
+            void* v_packed, int32_t* timestamps, int32_t* counts, int32_t* anchor_counts,
+            int32_t* num_packed, void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * Two-phase compressed flash prefill with GQA.  Replaces
+ * hybrid_compressed_flash_kernel / _sanity / pure_phase1_flash_kernel
+ * (deltaFlashAttention.py:9-357) and their wrappers (modeling_llama.py:306-451)
+ * including the repeat_kv expansion (:701-708): query head h reads KV head
+ * h / (Hq / Hkv) directly.
+ *
+ * q, out: [B, Hq, Nq, D] bf16; k, v: [B, Hkv, Nk, D] bf16;
+ * k_packed, v_packed: [B, Hkv, >=P, D] bf16; timestamps: [B, Hkv, >=P] int32;
+ * counts: [B, Hkv, >=P] int32 or fp32 (counts_dtype DA_I32 / DA_F32).
+ * num_packed: P (rows of the packed tensors that are read); if num_packed_dev
+ *   is non-null the device value is used instead (it must be <= num_packed).
+ * window: dense window W >= 0 (modeling_llama.py:716); scale > 0 (:289).
+ * no_count: every count, padding included, is 1 (modeling_llama.py:323-324).
+ * Logical schedule: 128-row query blocks x 128-anchor packed blocks exactly as
+ * the reference (Phase 1 stops at the first packed block whose maximum
+ * timestamp is >= start_m - W; Phase 2 starts at ((last+1)/128)*128).
+ * D must be 128; Hq % Hkv == 0.
+ */
+int64_t da_hybrid_workspace_size(int64_t B, int64_t Hkv, int64_t num_packed);
+int da_hybrid_prefill(const void* q, const void* k, const void* v, const void* k_packed,
+                      const void* v_packed, const int32_t* timestamps, const void* counts,
+                      int counts_dtype, void* out, int dtype, int64_t B, int64_t Hq,
+                      int64_t Hkv, int64_t Nq, int64_t Nk, int64_t D, const int64_t* strides,
+                      int64_t num_packed, const int32_t* num_packed_dev, int64_t window,
+                      float scale, int variant, int no_count, void* workspace,
+                      int64_t workspace_bytes, void* stream);
+
+/*
+ * Dense flash prefill (the uncompressed control).  Replaces _attn_fwd_flat and
+ * triton_flash_attention (flashAttention.py:5-130) with GQA handled by head
+ * indexing instead of repeat_kv.
+ * q, out: [B, Hq, Nq, D]; k, v: [B, Hkv, Nk, D]; causal: mask j > i.
+ */
+int da_dense_prefill(const void* q, const void* k, const void* v, void* out, int dtype,
+                     int64_t B, int64_t Hq, int64_t Hkv, int64_t Nq, int64_t Nk, int64_t D,
+                     const int64_t* strides, int causal, float scale, void* stream);
+
+/*
+ * strides for da_hybrid_prefill / da_dense_prefill: int64[3 * 8] element strides
+ * (batch, head, sequence) of, in order: q, k, v, k_packed, v_packed, out,
+ * timestamps (sequence stride must be 1), counts (sequence stride must be 1).
+ * da_dense_prefill reads the q, k, v and out triples only.
+ */
+#define DA_STRIDE_Q 0
+#define DA_STRIDE_K 3
+#define DA_STRIDE_V 6
+#define DA_STRIDE_KP 9
+#define DA_STRIDE_VP 12
+#define DA_STRIDE_OUT 15
+#define DA_STRIDE_TS 18
+#define DA_STRIDE_CNT 21
+#define DA_NUM_STRIDES 24
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DELTAATTN_H */

@@ -1,0 +1,186 @@
+"""GPU parity of the HIP kernels against the CPU oracle and the reference's golden vectors.
+
+Bars: selection and indexing are bit-exact; attention outputs (bf16) are within
+max-abs 2e-2 and mean-abs 1e-3 of the fp32 oracle on the same bf16 inputs.
+"""
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import announce
+from oracle import delta_oracle as O
+from oracle import select_oracle_c as OC
+
+pytestmark = pytest.mark.gpu
+
+MAX_ABS = 2e-2
+MEAN_ABS = 1e-3
+HERE = os.path.dirname(os.path.abspath(__file__))
+
+
+def _bf16_inputs(B, Hq, Hkv, N, D, seed, rho=0.9):
+    from deltaattention_amd import synth
+    q, k, v = synth.make_layer_inputs(B, Hq, Hkv, N, D, rho=rho, seed=seed, rope_base=10000.0)
+    return q, k, v
+
+
+def _close(got, want, what):
+    got = np.asarray(got, dtype=np.float32)
+    want = np.asarray(want, dtype=np.float32)
+    assert np.isfinite(got).all(), f"{what}: non-finite output"
+    err = np.abs(got - want)
+    mx, mean = float(err.max()), float(err.mean())
+    print(f"{what}: max-abs {mx:.3e} mean-abs {mean:.3e}", flush=True)
+    assert mx <= MAX_ABS and mean <= MEAN_ABS, f"{what}: max-abs {mx:.3e}, mean-abs {mean:.3e}"
+
+
+# --------------------------------------------------------------------------------------
+# selection + packing: bit-exact
+# --------------------------------------------------------------------------------------
+@pytest.mark.parametrize("metric,tau,chunk,divide_to", [
+    ("euclidean", 9.0, 512, 0),
+    ("euclidian", 7.5, 100, 0),      # any non-"cosine" string is Euclidean
+    ("cosine", 0.85, 512, 0),
+    ("euclidean", 8.0, 0, 3),        # divide_to chunking
+    ("euclidean", 0.0, 64, 0),       # tau 0: every distinct row is kept
+])
+def test_select_bitexact(gpu, metric, tau, chunk, divide_to):
+    from deltaattention_amd import ops
+    q, k, v = _bf16_inputs(2, 2, 2, 3000, 128, seed=11)
+    announce(f"select {metric} tau={tau} chunk={chunk} divide_to={divide_to} N=3000")
+    keep, cc = ops.select(k.to(gpu), tau, chunk, divide_to, metric)
+    torch.cuda.synchronize()
+    ok, occ = OC.select_delta(k.float().numpy(), tau, chunk, divide_to, metric)
+    keep_h = keep.cpu().numpy()
+    cc_h = cc.cpu().numpy()
+    assert (cc_h == occ).all(), "chunk counts differ"
+    assert (keep_h == ok).all(), f"keep differs at {np.argwhere(keep_h != ok)[:5]}"
+
+
+def test_select_bitexact_config1_shape(gpu):
+    """Config-1 key shape (8 KV heads x 32768 x 128, bf16), chunk 512."""
+    from deltaattention_amd import ops, synth
+    k = synth.make_layer_inputs(1, 8, 8, 32768, 128, seed=1)[1]
+    for tau in (8.0, 11.0):
+        announce(f"select config1 N=32768 tau={tau}")
+        keep, cc = ops.select(k.to(gpu), tau, 512)
+        ok, occ = OC.select_delta(k.float().numpy(), tau, 512)
+        assert (cc.cpu().numpy() == occ).all()
+        assert (keep.cpu().numpy() == ok).all()
+
+
+@pytest.mark.parametrize("N,tau", [(3000, 10.0), (777, 7.0), (4096, 0.0)])
+def test_pack_exact(gpu, N, tau):
+    from deltaattention_amd import ops
+    q, k, v = _bf16_inputs(1, 4, 3, N, 128, seed=5)
+    announce(f"pack N={N} tau={tau}")
+    kg, vg = k.to(gpu), v.to(gpu)
+    keep, _ = ops.select(kg, tau, 512)
+    packed = ops.pack(keep, kg, vg)
+    torch.cuda.synchronize()
+    ref = O.pack(k.float().numpy(), v.float().numpy(), keep.cpu().numpy())
+    P = int(packed.num_packed.item())
+    assert P == ref["P"]
+    assert (packed.anchor_counts.cpu().numpy() == ref["anchor_counts"]).all()
+    assert (packed.timestamps[:, :, :P].cpu().numpy() == ref["timestamps"]).all()
+    assert (packed.counts[:, :, :P].cpu().numpy() == ref["counts"]).all()
+    assert torch.equal(packed.k_packed[:, :, :P].float().cpu(), torch.from_numpy(ref["k_packed"]))
+    assert torch.equal(packed.v_packed[:, :, :P].float().cpu(), torch.from_numpy(ref["v_packed"]))
+
+
+def test_pack_periodic_and_exact_capacity(gpu):
+    """Periodic keep mask (modeling_llama.py:626-632) packed into buffers of exactly P rows."""
+    from deltaattention_amd import ops
+    q, k, v = _bf16_inputs(1, 2, 2, 1000, 128, seed=6)
+    keep = torch.from_numpy(O.select_periodic(1, 2, 1000, 0.3))
+    ref = O.pack(k.float().numpy(), v.float().numpy(), keep.numpy())
+    announce("pack periodic capacity=P")
+    packed = ops.pack(keep.to(gpu), k.to(gpu), v.to(gpu), capacity=ref["P"])
+    assert (packed.counts.cpu().numpy() == ref["counts"]).all()
+    assert (packed.timestamps.cpu().numpy() == ref["timestamps"]).all()
+    assert torch.equal(packed.k_packed.float().cpu(), torch.from_numpy(ref["k_packed"]))
+
+
+# --------------------------------------------------------------------------------------
+# dense flash prefill
+# --------------------------------------------------------------------------------------
+@pytest.mark.parametrize("B,Hq,Hkv,N,causal", [
+    (1, 8, 2, 700, True),
+    (2, 4, 4, 513, True),
+    (1, 6, 3, 384, True),
+    (1, 4, 1, 300, False),
+])
+def test_dense_vs_oracle(gpu, B, Hq, Hkv, N, causal):
+    from deltaattention_amd import ops
+    q, k, v = _bf16_inputs(B, Hq, Hkv, N, 128, seed=3)
+    announce(f"dense B={B} Hq={Hq} Hkv={Hkv} N={N} causal={causal}")
+    out = ops.dense_prefill(q.to(gpu), k.to(gpu), v.to(gpu), causal=causal)
+    ref = O.dense_attention(q.float().numpy(), k.float().numpy(), v.float().numpy(), causal)
+    _close(out.float().cpu().numpy(), ref, f"dense N={N}")
+
+
+# --------------------------------------------------------------------------------------
+# hybrid prefill against the reference's own outputs (golden vectors, D=32 zero-padded)
+# --------------------------------------------------------------------------------------
+@pytest.mark.parametrize("case", ["A", "B", "C", "D"])
+@pytest.mark.parametrize("variant", ["hybrid", "sanity", "pure_phase1"])
+def test_hybrid_golden(gpu, case, variant):
+    """The golden inputs are bf16-exact with D=32; zero-padding D to 128 leaves every
+    score (and the selection) unchanged, the scale stays 32**-0.5, and the first 32
+    output dims are compared with the reference's interpreter outputs."""
+    from deltaattention_amd import ops
+    z = np.load(os.path.join(HERE, "golden", "hybrid_golden.npz"))
+    g = lambda n: z[f"{case}/{n}"]
+    q, k, v, keep = g("q"), g("k"), g("v"), g("keep")
+    W, no_count = int(g("window")), bool(g("no_count"))
+    D = q.shape[-1]
+    pad = lambda a: torch.from_numpy(np.pad(a, [(0, 0)] * 3 + [(0, 128 - D)])).to(torch.bfloat16).to(gpu)
+    qg, kg, vg = pad(q), pad(k), pad(v)
+    announce(f"golden case {case} {variant}")
+    packed = ops.pack(torch.from_numpy(keep).to(gpu), kg, vg)
+    out = ops.hybrid_prefill(qg, kg, vg, packed.k_packed, packed.v_packed, packed.timestamps,
+                             packed.counts, window=W, scale=D ** -0.5, variant=variant,
+                             no_count=no_count, num_packed_dev=packed.num_packed)
+    got = out.float().cpu().numpy()
+    assert np.all(got[..., D:] == 0)
+    _close(got[..., :D], g(f"out_{variant}"), f"golden {case}/{variant}")
+
+
+# --------------------------------------------------------------------------------------
+# end-to-end delta prefill against the oracle
+# --------------------------------------------------------------------------------------
+@pytest.mark.parametrize("B,Hq,Hkv,N,tau,W,variant,no_count", [
+    (1, 8, 2, 2048, 10.0, 128, "hybrid", False),
+    (1, 4, 4, 1500, 9.0, 0, "hybrid", False),
+    (1, 4, 2, 1100, 8.0, 300, "hybrid", True),
+    (2, 8, 2, 1024, 10.0, 128, "sanity", False),
+    (1, 4, 2, 900, 9.0, 128, "pure_phase1", False),
+    (1, 8, 2, 3000, 12.0, 128, "hybrid", False),
+    (1, 2, 1, 2048, 1e6, 128, "hybrid", False),   # only chunk starts are anchors
+])
+def test_delta_prefill_vs_oracle(gpu, B, Hq, Hkv, N, tau, W, variant, no_count):
+    from deltaattention_amd import ops
+    q, k, v = _bf16_inputs(B, Hq, Hkv, N, 128, seed=N + Hq)
+    announce(f"delta_prefill B={B} Hq={Hq} Hkv={Hkv} N={N} tau={tau} W={W} {variant} nc={no_count}")
+    out = ops.delta_prefill(q.to(gpu), k.to(gpu), v.to(gpu), tau, 512, window=W, variant=variant,
+                            no_count=no_count)
+    kf, vf = k.float().numpy(), v.float().numpy()
+    keep, _ = OC.select_delta(kf, tau, 512)
+    p = O.pack(kf, vf, keep)
+    ref = O.hybrid_attention(q.float().numpy(), kf, vf, p["k_packed"], p["v_packed"],
+                             p["timestamps"], p["counts"], W, variant=variant, no_count=no_count)
+    _close(out.float().cpu().numpy(), ref, f"delta {variant} N={N}")
+
+
+def test_hybrid_float_counts_matches_int(gpu):
+    from deltaattention_amd import ops
+    q, k, v = _bf16_inputs(1, 4, 1, 1024, 128, seed=9)
+    qg, kg, vg = q.to(gpu), k.to(gpu), v.to(gpu)
+    announce("hybrid fp32 counts vs int32 counts")
+    keep, _ = ops.select(kg, 10.0, 512)
+    pk = ops.pack(keep, kg, vg).trimmed()
+    a = ops.hybrid_prefill(qg, kg, vg, pk.k_packed, pk.v_packed, pk.timestamps, pk.counts)
+    b = ops.hybrid_prefill(qg, kg, vg, pk.k_packed, pk.v_packed, pk.timestamps, pk.counts.float())
+    assert torch.equal(a, b)
