@@ -1,0 +1,228 @@
+#!/usr/bin/env python3
+"""DeltaAttention prefill benchmark on one MI355X.
+
+Metric: prefill attention ms/layer and speedup over the dense flash
+prefill, Llama-3-8B GQA shape (32 query heads, 8 KV heads, head_dim 128), bf16, causal.
+A step is one layer's delta prefill attention: anchor selection -> index/pack/counts ->
+two-phase hybrid prefill, on synthetic inputs already resident in HBM (the work the
+reference times as time_get_row_delta + time_delta_mm_pattern,
+modeling_llama.py:612-754).
+
+Default workload is config 1 (N = 32768, r = 4); ``--config 2`` runs N = 131072 with
+``--ratio`` in {2, 4, 8}.  The threshold tau is calibrated on the seeded keys so that the
+realised compression is r (smallest tau with keep rate <= 1/r).
+
+``--only {delta,hybrid,dense,compress}`` runs just that part for K steps (used for
+rocprofv3 captures) and prints a short line instead of the JSON record.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+HBM_PEAK_GBS = 8000.0
+BF16_PEAK_TFLOPS = 2500.0
+
+
+def parse_args():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--config", type=int, default=1, choices=(1, 2))
+    ap.add_argument("--ratio", type=float, default=4.0)
+    ap.add_argument("--seq", type=int, default=0, help="override the sequence length")
+    ap.add_argument("--window", type=int, default=128)
+    ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--only", choices=("delta", "hybrid", "dense", "compress"), default=None)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-sample-blocks", type=int, default=24,
+                    help="query blocks (all heads) the CPU baseline runs")
+    return ap.parse_args()
+
+
+def log(msg):
+    print(f"[bench] {msg}", file=sys.stderr, flush=True)
+
+
+def cpu_baseline(q, k, v, tau, window, alg_total, sample_blocks):
+    """Time the CPU restatement (oracle, a 'port' of the reference math) on a bounded
+    sample: full selection + packing, and the hybrid attention for ``sample_blocks``
+    evenly spaced query blocks of every head, extrapolated to the layer by the exact
+    algorithmic-FLOP ratio."""
+    import numpy as np
+    from threadpoolctl import threadpool_limits
+    from oracle import delta_oracle as O
+    from oracle import select_oracle_c as OC
+    from deltaattention_amd import metrics
+
+    cores = min(16, os.cpu_count() or 1)
+    qf = q.float().cpu().numpy()
+    kf = k.float().cpu().numpy()
+    vf = v.float().cpu().numpy()
+    B, Hq, N, D = qf.shape
+    with threadpool_limits(limits=cores):
+        t0 = time.perf_counter()
+        keep, _ = OC.select_delta(kf, tau, 512)
+        p = O.pack(kf, vf, keep)
+        t_compress = time.perf_counter() - t0
+        nqb = (N + 127) // 128
+        blocks = sorted(set(np.linspace(0, nqb - 1, sample_blocks).round().astype(int).tolist()))
+        t0 = time.perf_counter()
+        O.hybrid_attention(qf, kf, vf, p["k_packed"], p["v_packed"], p["timestamps"], p["counts"],
+                           window, q_blocks=blocks)
+        t_sample = time.perf_counter() - t0
+    # algorithmic FLOPs of the sampled blocks
+    n_safe, last, ds = metrics.hybrid_schedule(p["timestamps"], p["P"], N, N, window)
+    G = Hq // kf.shape[1]
+    c = p["anchor_counts"].reshape(B, -1, 1)
+    start = np.arange(nqb)[None, None] * 128
+    rows = np.minimum(128, N - start)
+    pairs = rows * np.minimum(n_safe * 128, c) + rows * (start - ds + 1) + rows * (rows - 1) // 2
+    sample_flops = 4.0 * D * float(pairs[:, :, blocks].sum() * G)
+    t_attn = t_sample * alg_total / sample_flops
+    ms = 1e3 * (t_compress + t_attn)
+    return {"value": round(ms, 1), "unit": "ms/layer", "cores": cores, "kind": "port",
+            "sample": (f"oracle select+pack over all {B * kf.shape[1]} KV heads "
+                       f"({1e3 * t_compress:.0f} ms) + hybrid attention for {len(blocks)} of {nqb} "
+                       f"query blocks x {Hq} heads ({t_sample:.1f} s), extrapolated by the "
+                       f"algorithmic-FLOP ratio; BLAS threads={cores}, host {platform.processor() or platform.machine()}")}
+
+
+def main():
+    args = parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on exactly one GPU; multi-GPU runs are not "
+                                   "part of it (the path shards by KV head, see DESIGN.md)",
+                          "n_gpus": args.gpus}))
+        sys.exit(2)
+    import numpy as np
+    import torch
+    from deltaattention_amd import metrics, ops, synth
+
+    dev = torch.device("cuda:0")
+    N = args.seq or (32768 if args.config == 1 else 131072)
+    B, Hq, Hkv, D = 1, 32, 8, 128
+    W = args.window
+    log(f"config {args.config}: N={N} r={args.ratio} W={W}")
+    q, k, v = synth.make_layer_inputs(B, Hq, Hkv, N, D, rope_base=500000.0, seed=args.seed,
+                                      device=dev, qv_on_device=True)
+    torch.cuda.synchronize()
+    tau, r_real = synth.calibrate_threshold(k, args.ratio)
+    log(f"calibrated tau={tau:.4f} realised r={r_real:.3f}")
+
+    def step():
+        return ops.delta_prefill(q, k, v, tau, 512, window=W)
+
+    # ---- per-part timing helpers (HIP events on the launch stream) ----
+    def time_loop(fn, iters):
+        st = torch.cuda.current_stream()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        torch.cuda.synchronize()
+        e0.record(st)
+        for _ in range(iters):
+            fn()
+        e1.record(st)
+        e1.synchronize()
+        return e0.elapsed_time(e1) / iters
+
+    keep, _ = ops.select(k, tau, 512)
+    packed = ops.pack(keep, k, v)
+    torch.cuda.synchronize()
+    P = int(packed.num_packed.item())
+    ts_h = packed.timestamps[:, :, :P].cpu().numpy()
+    c_h = packed.anchor_counts.cpu().numpy()
+    out_h = torch.empty_like(q)
+    out_d = torch.empty_like(q)
+
+    def hybrid_only():
+        ops.hybrid_prefill(q, k, v, packed.k_packed, packed.v_packed, packed.timestamps,
+                           packed.counts, window=W, num_packed_dev=packed.num_packed, out=out_h)
+
+    def dense_only():
+        ops.dense_prefill(q, k, v, causal=True, out=out_d)
+
+    def compress_only():
+        kk, _ = ops.select(k, tau, 512)
+        ops.pack(kk, k, v, out=packed)
+
+    if args.only:
+        fn = {"delta": step, "hybrid": hybrid_only, "dense": dense_only, "compress": compress_only}[args.only]
+        for _ in range(args.warmup):
+            fn()
+        ms = time_loop(fn, args.steps)
+        print(f"only={args.only} N={N} r={r_real:.3f} steps={args.steps} ms/launch={ms:.4f}", flush=True)
+        return
+
+    # ---- the contract's timed region: K full steps ----
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step()
+    torch.cuda.synchronize()
+    ms_step = 1e3 * (time.perf_counter() - t0) / args.steps
+    log(f"delta step {ms_step:.3f} ms")
+
+    iters = max(3, args.steps)
+    for _ in range(2):
+        hybrid_only(); dense_only(); compress_only()
+    ms_hybrid = time_loop(hybrid_only, iters)
+    ms_dense = time_loop(dense_only, iters)
+    ms_compress = time_loop(compress_only, iters)
+    log(f"hybrid {ms_hybrid:.3f} ms  dense {ms_dense:.3f} ms  compress {ms_compress:.4f} ms")
+
+    fl = metrics.hybrid_flops(ts_h, c_h, P, N, Hq, D, W)
+    dense_fl = metrics.dense_flops(B, Hq, N, D)
+    cbytes = metrics.compression_bytes(N, D, c_h)
+    hyb_tflops = fl["algorithmic"] / (ms_hybrid * 1e-3) / 1e12
+    dense_tflops = dense_fl / (ms_dense * 1e-3) / 1e12
+
+    rec = {
+        "metric": "prefill attn ms/layer + speedup vs dense FA at 32K/128K, Llama-3-8B GQA",
+        "value": round(ms_step, 4),
+        "unit": "ms/layer",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": (f"synthetic: AR(1) keys rho=0.9 sigma=0.44 + RoPE base 5e5, Gaussian Q/V, "
+                 f"seed {args.seed}; Euclidean tau={tau:.4f} calibrated to r={args.ratio:g} "
+                 f"(realised {r_real:.3f}), chunk 512, W={W}"),
+        "config": {"workload": (f"config{args.config}: delta prefill attention, one layer, "
+                                f"B={B} Hq={Hq} Hkv={Hkv} D={D} N={N} bf16 causal r={args.ratio:g}"),
+                   "seq_len": N, "global_batch": B, "parallelism": "none (1 GPU)"},
+        "speedup_vs_dense": round(ms_dense / ms_step, 3),
+        "kernel_speedup_vs_dense": round(ms_dense / ms_hybrid, 3),
+        "dense_ms_per_layer": round(ms_dense, 4),
+        "hybrid_kernel_ms": round(ms_hybrid, 4),
+        "compress_ms": round(ms_compress, 4),
+        "compress_gbs": round(cbytes / (ms_compress * 1e-3) / 1e9, 1),
+        "hybrid_tflops": round(hyb_tflops, 1),
+        "dense_tflops": round(dense_tflops, 1),
+        "dense_mfma_frac": round(dense_tflops / BF16_PEAK_TFLOPS, 4),
+        "realised_ratio": round(r_real, 3),
+        "roofline": {"bound": "mfma", "achieved": round(hyb_tflops, 2), "peak": BF16_PEAK_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(hyb_tflops / BF16_PEAK_TFLOPS, 4),
+                     "traffic": None,
+                     "kernel": "attn_kernel<hybrid> (da_hybrid_prefill)",
+                     "algorithmic_flops": fl["algorithmic"]},
+    }
+    if not args.no_cpu_baseline:
+        log("cpu baseline (oracle sample) ...")
+        rec["cpu_baseline"] = cpu_baseline(q, k, v, tau, W, fl["algorithmic"], args.cpu_sample_blocks)
+    print(json.dumps(rec), flush=True)
+
+
+if __name__ == "__main__":
+    main()

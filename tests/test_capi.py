@@ -1,0 +1,98 @@
+"""The C ABI (include/deltaattn.h): the library loads, exports every declared symbol, and
+rejects bad arguments before touching the GPU."""
+import ctypes
+import os
+import re
+
+import pytest
+
+from deltaattention_amd import _native
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+HEADER = os.path.join(os.path.dirname(HERE), "include", "deltaattn.h")
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(da_[a-z_0-9]+)\s*\(", text)))
+
+
+def test_header_declares_the_expected_entry_points():
+    assert declared_symbols() == sorted([
+        "da_last_error", "da_version", "da_select", "da_pack_workspace_size", "da_pack",
+        "da_hybrid_workspace_size", "da_hybrid_prefill", "da_dense_prefill"])
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _native.lib()
+    for name in declared_symbols():
+        assert hasattr(lib, name), name
+        assert name in _native.SIGNATURES, f"{name} has no ctypes signature"
+    assert lib.da_version() == 1
+
+
+def _err():
+    return _native.lib().da_last_error().decode()
+
+
+def test_select_rejects_null_and_dtype():
+    lib = _native.lib()
+    f = ctypes.c_float(1.0)
+    assert lib.da_select(None, 1, 1, 1, 8, 128, 0, 0, 0, f, 0, 8, 1, None, None, None) == -1
+    assert "null" in _err()
+    fake = ctypes.c_void_p(1 << 20)
+    assert lib.da_select(fake, 4, 1, 1, 8, 128, 0, 0, 128, f, 0, 8, 1, fake, fake, None) == -2
+    assert lib.da_select(fake, 1, 1, 1, 8, 130, 0, 0, 130, f, 0, 8, 1, fake, fake, None) == -2
+    assert "head_dim" in _err()
+    assert lib.da_select(fake, 1, 1, 1, 8, 128, 0, 0, 129, f, 0, 8, 1, fake, fake, None) == -1
+    assert lib.da_select(fake, 1, 1, 1, 8, 128, 0, 0, 128, f, 0, 0, 1, fake, fake, None) == -1
+
+
+def test_pack_rejects_small_workspace():
+    lib = _native.lib()
+    fake = ctypes.c_void_p(1 << 20)
+    need = lib.da_pack_workspace_size(1, 8, 32768)
+    assert need == 2 * 8 * 512 * 4
+    rc = lib.da_pack(fake, fake, fake, 1, 1, 8, 32768, 128, 0, 0, 128, 0, 0, 128, 32768, fake, fake,
+                     fake, fake, fake, fake, fake, need - 4, None)
+    assert rc == -4 and "workspace" in _err()
+
+
+def test_attention_rejects_bad_shapes():
+    lib = _native.lib()
+    fake = ctypes.c_void_p(1 << 20)
+    st = _native.strides_array([0] * 24)
+    f = ctypes.c_float(0.088)
+    # head_dim 64 is not supported by the attention kernels
+    assert lib.da_dense_prefill(fake, fake, fake, fake, 1, 1, 4, 2, 64, 64, 64, st, 1, f, None) == -2
+    # Hq not a multiple of Hkv
+    assert lib.da_dense_prefill(fake, fake, fake, fake, 1, 1, 6, 4, 64, 64, 128, st, 1, f, None) == -1
+    # negative scale
+    assert lib.da_dense_prefill(fake, fake, fake, fake, 1, 1, 4, 2, 64, 64, 128, st, 1,
+                                ctypes.c_float(-1.0), None) == -1
+    # negative window / unknown variant / missing workspace
+    args = [fake] * 7
+    assert lib.da_hybrid_prefill(*args, 3, fake, 1, 1, 4, 2, 64, 64, 128, st, 10, None, -1,
+                                 f, 0, 0, fake, 1 << 20, None) == -1
+    assert lib.da_hybrid_prefill(*args, 3, fake, 1, 1, 4, 2, 64, 64, 128, st, 10, None, 0,
+                                 f, 7, 0, fake, 1 << 20, None) == -1
+    st2 = _native.strides_array([0] * 18 + [0, 0, 1, 0, 0, 1])
+    assert lib.da_hybrid_prefill(*args, 3, fake, 1, 1, 4, 2, 64, 64, 128, st2, 10, None, 0,
+                                 f, 0, 0, None, 0, None) == -4
+
+
+def test_workspace_sizes():
+    lib = _native.lib()
+    assert lib.da_hybrid_workspace_size(1, 8, 8192) == 8 * 2 * 64 * 4
+    assert lib.da_hybrid_workspace_size(2, 8, 1) == 2 * 8 * 2 * 1 * 4
+
+
+def test_ops_refuse_cpu_tensors():
+    torch = pytest.importorskip("torch")
+    from deltaattention_amd import ops
+    k = torch.zeros(1, 1, 16, 128, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="no CPU path"):
+        ops.select(k, 1.0)
+    with pytest.raises(ValueError, match="no CPU path"):
+        ops.dense_prefill(k, k, k)

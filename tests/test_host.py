@@ -1,0 +1,61 @@
+"""Host-side logic: chunking, the schedule and FLOP accounting, synthetic inputs."""
+import numpy as np
+import pytest
+import torch
+
+from deltaattention_amd import metrics, ops, synth
+from oracle import delta_oracle as O
+
+
+@pytest.mark.parametrize("n,cs,dt", [(1050, 100, 0), (300, 512, 0), (10, 0, 4), (3, 0, 5), (7, 0, 0)])
+def test_chunking_matches_oracle(n, cs, dt):
+    assert ops.chunking(n, cs, dt) == O.chunking(n, cs, dt)
+
+
+def test_metrics_schedule_matches_oracle():
+    rng = np.random.default_rng(2)
+    N = 2000
+    keep = (rng.random((2, 3, N)) < 0.25).astype(np.int32)
+    keep[..., 0] = 1
+    keep[1, 2, 700:] = 0       # a short head -> fully padded blocks
+    k = rng.standard_normal((2, 3, N, 8)).astype(np.float32)
+    p = O.pack(k, k, keep)
+    for W in (0, 128, 400):
+        a = metrics.hybrid_schedule(p["timestamps"], p["P"], N, N, W)
+        b = O.hybrid_schedule(p["timestamps"], p["P"], N, N, W)
+        for x, y in zip(a, b[:3]):
+            assert (np.asarray(x) == y).all()
+
+
+def test_hybrid_flops_counts_pairs():
+    """The algorithmic pair count equals the brute-force weighted-key count (real anchors
+    only, plus dense keys ds..i per row)."""
+    rng = np.random.default_rng(4)
+    N, Hq, Hkv = 900, 4, 2
+    keep = (rng.random((1, Hkv, N)) < 0.3).astype(np.int32)
+    keep[..., 0] = 1
+    k = rng.standard_normal((1, Hkv, N, 8)).astype(np.float32)
+    p = O.pack(k, k, keep)
+    W = 128
+    fl = metrics.hybrid_flops(p["timestamps"], p["anchor_counts"], p["P"], N, Hq, 128, W)
+    n_safe, last, ds, _ = O.hybrid_schedule(p["timestamps"], p["P"], N, N, W)
+    pairs = 0
+    for g in range(Hkv):
+        for qb in range((N + 127) // 128):
+            a = min(int(n_safe[0, g, qb]) * 128, int(p["anchor_counts"][0, g]))
+            for i in range(qb * 128, min(N, qb * 128 + 128)):
+                pairs += a + max(0, i - int(ds[0, g, qb]) + 1)
+    assert fl["algorithmic"] == 4.0 * 128 * pairs * (Hq // Hkv)
+    assert metrics.dense_flops(1, 32, 32768, 128) == pytest.approx(8.796e12, rel=1e-3)
+
+
+def test_synth_is_deterministic_and_ar1():
+    a = synth.ar1_keys(1, 2, 4000, 16, seed=3)
+    b = synth.ar1_keys(1, 2, 4000, 16, seed=3)
+    assert torch.equal(a, b)
+    x = a.numpy()
+    assert abs(x.var() - 1.0) < 0.15
+    r = (x[:, :, 1:] * x[:, :, :-1]).mean() / x.var()
+    assert abs(r - 0.9) < 0.03
+    q, k, v = synth.make_layer_inputs(1, 4, 2, 256, 128, seed=1)
+    assert q.dtype == torch.bfloat16 and k.shape == (1, 2, 256, 128) and q.shape == (1, 4, 256, 128)
