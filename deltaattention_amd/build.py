@@ -19,9 +19,12 @@ LIB = os.path.join(HERE, "libdeltaattn.so")
 ARCH = os.environ.get("DELTAATTN_ARCH", "gfx950")
 
 # -packed-fp32-ops: never emit v_pk_{add,mul,fma}_f32.
+# -fno-honor-nans: max/min need no NaN canonicalisation (infinities stay honoured; the
+# kernels mask with -inf).
 HIPCC_FLAGS = [
     "-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+    "-fno-honor-nans",
     "-Wall", "-Wno-unused-result", "-Wno-unused-function",
 ]
 

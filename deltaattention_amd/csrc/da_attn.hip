@@ -91,8 +91,18 @@ __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_ex
 __device__ __forceinline__ int k_lds_off(int row, int chunk) {
   return row * (kD * 2) + ((chunk ^ (row & 15)) << 4);
 }
-__device__ __forceinline__ int vt_lds_off(int d, int granule) {
-  return kKBytes + d * (kTileN * 2) + ((granule ^ ((d >> 1) & 15)) << 3);
+// V^T rows (one per head dimension) hold the 64 keys of the tile permuted so that
+// the 8 keys one lane feeds to a P.V MFMA -- keys 16u + 4h + {0..3} and
+// 16u + 8 + 4h + {0..3} -- form 16-byte chunk 2u + h.  A group of 4 consecutive keys
+// 4kg..4kg+3 is the 8-byte half (kg >> 1) & 1 of chunk 2 (kg >> 2) + (kg & 1).
+// Chunks are XOR-swizzled with (d & 7) ^ ((d >> 3) & 1) so that 8 (or 16) consecutive
+// rows read at one chunk index hit distinct banks.
+__device__ __forceinline__ int vt_swz(int d) { return (d & 7) ^ ((d >> 3) & 1); }
+__device__ __forceinline__ int vt_lds_chunk(int d, int chunk) {
+  return kKBytes + d * (kTileN * 2) + ((chunk ^ vt_swz(d)) << 4);
+}
+__device__ __forceinline__ int vt_lds_group(int d, int kg) {
+  return vt_lds_chunk(d, 2 * (kg >> 2) + (kg & 1)) + (((kg >> 1) & 1) << 3);
 }
 constexpr int kCntOff = kKBytes + kVBytes;
 constexpr int kTsOff = kCntOff + kTileN * 4;
@@ -104,25 +114,26 @@ struct TileRegs {
   int ts;
 };
 
-// Global -> registers for one 64-key tile.  Thread tid loads 16-byte chunk
-// (tid % 16) of keys 4 * (tid / 16) + j, j = 0..3.
+// Global -> registers for one 64-key tile.  For K, thread tid loads 16-byte chunk
+// (tid % 16) of keys 4 * (tid / 16) + j, j = 0..3 (a wave writes whole 256-byte K
+// rows).  For V the roles swap -- chunk tid / 16 of keys 4 * (tid % 16) + j -- so that
+// after the in-register transpose the 16 lanes of one chunk write one complete
+// 128-byte V^T row, which keeps the LDS stores free of bank conflicts.
 __device__ __forceinline__ void load_tile(TileRegs& r, const uint16_t* kbase, const uint16_t* vbase,
                                           int64_t sk_n, int64_t sv_n, int key0, int limit,
                                           int tid, bool with_meta, const int32_t* tsrow,
                                           const void* cntrow, int cnt_is_float, int no_count,
                                           int meta_limit, int ts_oob) {
-  const int chunk = tid & 15;
-  const int kg = tid >> 4;
+  const int chunk = tid & 15, kg = tid >> 4;    // K mapping
+  const int vchunk = tid >> 4, vkg = tid & 15;  // V mapping
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int key = key0 + kg * 4 + j;
-    if (key < limit) {
-      r.k[j] = *(const u32x4*)(kbase + (int64_t)key * sk_n + chunk * 8);
-      r.v[j] = *(const u32x4*)(vbase + (int64_t)key * sv_n + chunk * 8);
-    } else {
-      r.k[j] = u32x4{0, 0, 0, 0};
-      r.v[j] = u32x4{0, 0, 0, 0};
-    }
+    r.k[j] = key < limit ? *(const u32x4*)(kbase + (int64_t)key * sk_n + chunk * 8)
+                         : u32x4{0, 0, 0, 0};
+    const int vkey = key0 + vkg * 4 + j;
+    r.v[j] = vkey < limit ? *(const u32x4*)(vbase + (int64_t)vkey * sv_n + vchunk * 8)
+                          : u32x4{0, 0, 0, 0};
   }
   if (with_meta && tid < kTileN) {
     const int key = key0 + tid;
@@ -142,22 +153,24 @@ __device__ __forceinline__ void load_tile(TileRegs& r, const uint16_t* kbase, co
 }
 
 __device__ __forceinline__ void store_tile(const TileRegs& r, char* stage, int tid, bool with_meta) {
-  const int chunk = tid & 15;
-  const int kg = tid >> 4;
+  const int chunk = tid & 15, kg = tid >> 4;
+  const int vchunk = tid >> 4, vkg = tid & 15;
 #pragma unroll
   for (int j = 0; j < 4; ++j) *(u32x4*)(stage + k_lds_off(kg * 4 + j, chunk)) = r.k[j];
   // transpose 4 keys x 8 dims into 8 rows (dims) of 4 keys
 #pragma unroll
   for (int w = 0; w < 4; ++w) {
     const uint32_t a = r.v[0][w], b = r.v[1][w], c = r.v[2][w], d = r.v[3][w];
-    const int d0 = chunk * 8 + 2 * w;
+    const int d0 = vchunk * 8 + 2 * w;
+    // v_perm_b32 picks bytes of {S0 = high word, S1 = low word}: 0x05040100 gives
+    // (lo16(a), lo16(b)), 0x07060302 gives (hi16(a), hi16(b)).
     u32x2 lo, hi;
-    lo[0] = (a & 0xffffu) | (b << 16);
-    lo[1] = (c & 0xffffu) | (d << 16);
-    hi[0] = (a >> 16) | (b & 0xffff0000u);
-    hi[1] = (c >> 16) | (d & 0xffff0000u);
-    *(u32x2*)(stage + vt_lds_off(d0, kg)) = lo;
-    *(u32x2*)(stage + vt_lds_off(d0 + 1, kg)) = hi;
+    lo[0] = __builtin_amdgcn_perm(b, a, 0x05040100u);
+    lo[1] = __builtin_amdgcn_perm(d, c, 0x05040100u);
+    hi[0] = __builtin_amdgcn_perm(b, a, 0x07060302u);
+    hi[1] = __builtin_amdgcn_perm(d, c, 0x07060302u);
+    *(u32x2*)(stage + vt_lds_group(d0, vkg)) = lo;
+    *(u32x2*)(stage + vt_lds_group(d0 + 1, vkg)) = hi;
   }
   if (with_meta && tid < kTileN) {
     ((float*)(stage + kCntOff))[tid] = r.cnt;
@@ -325,13 +338,15 @@ void attn_kernel(AttnArgs a) {
       // ---- online softmax ----
       float mx = -INFINITY;
 #pragma unroll
-      for (int r = 0; r < 16; ++r) mx = fmaxf(mx, fmaxf(s[0][r], s[1][r]));
+      for (int r = 0; r < 16; ++r) mx = __builtin_fmaxf(mx, __builtin_fmaxf(s[0][r], s[1][r]));
       mx = fmaxf(mx, swap_halves(mx));
       const float m_new = fmaxf(m_i, mx);
       const float m_use = (m_new == -INFINITY) ? 0.0f : m_new;
       const float alpha = exp2_fast((m_i - m_use) * c);
       const float neg = -m_use * c;
-      uint32_t pb[16];
+      // P^T as four B operands (16 keys each): operand u = 2 * kb2 + (r4 >> 1) holds
+      // S^T registers 8 * (r4 >> 1) .. +7 of block kb2.
+      u32x4 pw[4];
       float psum = 0.0f;
       const bool weighted = (VARIANT == kPure) || (VARIANT == kHybrid && ph1);
       const float* cl = (const float*)(stage + kCntOff);
@@ -346,10 +361,10 @@ void attn_kernel(AttnArgs a) {
           for (int e = 0; e < 4; ++e) {
             p[e] = exp2_fast(__builtin_fmaf(s[kb2][4 * r4 + e], c, neg));
             if (weighted) p[e] *= w4[e];
-            psum += p[e];
           }
-          pb[kb2 * 8 + 2 * r4] = pack_bf16x2(p[0], p[1]);
-          pb[kb2 * 8 + 2 * r4 + 1] = pack_bf16x2(p[2], p[3]);
+          psum += (p[0] + p[1]) + (p[2] + p[3]);
+          pw[2 * kb2 + (r4 >> 1)][(r4 & 1) * 2 + 0] = pack_bf16x2(p[0], p[1]);
+          pw[2 * kb2 + (r4 >> 1)][(r4 & 1) * 2 + 1] = pack_bf16x2(p[2], p[3]);
         }
       }
       l_i = l_i * alpha + psum;
@@ -363,20 +378,11 @@ void attn_kernel(AttnArgs a) {
       // ---- O^T += V^T P^T ----
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        const int kb2 = u >> 1, half = u & 1;
-        u32x4 pw;
-        pw[0] = pb[kb2 * 8 + 4 * half + 0];
-        pw[1] = pb[kb2 * 8 + 4 * half + 1];
-        pw[2] = pb[kb2 * 8 + 4 * half + 2];
-        pw[3] = pb[kb2 * 8 + 4 * half + 3];
-        const bf16x8 pbv = __builtin_bit_cast(bf16x8, pw);
+        const bf16x8 pbv = __builtin_bit_cast(bf16x8, pw[u]);
 #pragma unroll
         for (int db = 0; db < 4; ++db) {
           const int d = db * 32 + ql;
-          const u32x2 v0 = *(const u32x2*)(stage + vt_lds_off(d, 4 * u + hl));
-          const u32x2 v1 = *(const u32x2*)(stage + vt_lds_off(d, 4 * u + 2 + hl));
-          u32x4 vw;
-          vw[0] = v0[0]; vw[1] = v0[1]; vw[2] = v1[0]; vw[3] = v1[1];
+          const u32x4 vw = *(const u32x4*)(stage + vt_lds_chunk(d, 2 * u + hl));
           o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, vw), pbv, o[db],
                                                            0, 0, 0);
         }
