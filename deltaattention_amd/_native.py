@@ -31,6 +31,11 @@ SIGNATURES = {
     "da_hybrid_prefill": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _P, _I, _L, _L, _L, _L, _L, _L, _P,
                                _L, _P, _L, _F, _I, _I, _P, _L, _P]),
     "da_dense_prefill": (_I, [_P, _P, _P, _P, _I, _L, _L, _L, _L, _L, _L, _P, _I, _F, _P]),
+    "da_decode_update": (_I, [_P, _P, _I, _L, _L, _L, _L, _L, _P, _P, _L, _L, _L, _P, _P, _L, _L,
+                              _L, _P, _P, _L, _L, _P, _L, _L, _L, _L, _F, _I, _P]),
+    "da_decode_workspace_size": (_L, [_L, _L, _L, _L]),
+    "da_decode_attention": (_I, [_P, _I, _L, _L, _L, _L, _L, _L, _P, _P, _L, _L, _L, _P, _L, _L,
+                                 _P, _L, _P, _P, _L, _L, _L, _L, _L, _F, _P, _L, _L, _P, _L, _P]),
 }
 
 

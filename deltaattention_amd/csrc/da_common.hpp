@@ -67,4 +67,29 @@ __device__ __forceinline__ float readlane_f32(float v, int lane) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
 }
 
+// Fixed-order fp32 sum over a wave where lane l holds the pair sum of head-dimension
+// slots 2l and 2l+1 (level 1 of a perfect pairwise tree over 128 slots): DPP lane^1,
+// lane^2, 8-lane mirror and 16-lane mirror give levels 2-5, then (r0 + r1) + (r2 + r3)
+// over the four 16-lane row sums.  The result is wave-uniform.
+__device__ __forceinline__ float wave_tree_sum(float t) {
+#pragma clang fp contract(off)
+  t = t + dpp_f32<kDppXor1>(t);
+  t = t + dpp_f32<kDppXor2>(t);
+  t = t + dpp_f32<kDppHalfMirror>(t);
+  t = t + dpp_f32<kDppMirror>(t);
+  const float r0 = readlane_f32(t, 0);
+  const float r1 = readlane_f32(t, 16);
+  const float r2 = readlane_f32(t, 32);
+  const float r3 = readlane_f32(t, 48);
+  return (r0 + r1) + (r2 + r3);
+}
+
+// x0*y0 + x1*y1 with both products rounded (no fused multiply-add).
+__device__ __forceinline__ float pair_dot(float x0, float x1, float y0, float y1) {
+#pragma clang fp contract(off)
+  const float p0 = x0 * y0;
+  const float p1 = x1 * y1;
+  return p0 + p1;
+}
+
 }  // namespace da

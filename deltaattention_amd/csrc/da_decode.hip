@@ -1,0 +1,351 @@
+// Delta decoding on gfx950: the compressed-cache update and q_len = 1 attention.
+//
+// decode_update_kernel replaces fused_hybrid_decode_update_kernel
+// (deltaDecoding.py:9-104).  One wave per (batch, kv head): when the exact ring is
+// full, the token in slot exact_len % W is evicted and either merged into the last
+// packed anchor (count + 1) when it is close enough -- Euclidean dist^2 <= tau^2 or
+// cosine >= tau, computed with the same fixed pairwise fp32 tree as the selection --
+// or appended as a new anchor (count 1, timestamp total - W).  The new token then
+// takes the ring slot.
+//
+// decode_attn_kernel + decode_combine_kernel replace fused_hybrid_decode_kernel
+// (deltaDecoding.py:236-362).  The key list of a kv head is its packed anchors
+// [0, length) followed by the ring slots [0, exact_len).  Packed scores get
+// + log(count) (so a count-c anchor weighs like c equal keys, and padding with count 0
+// gets no weight); ring scores are unmasked.  The list is cut into slices of 256 keys;
+// one workgroup scores a slice for all query heads of the group (the key and value
+// rows are read once per group), keeps the slice's max / sum / P.V partials, and the
+// combine kernel merges the slices exactly (rescaling by exp(m_s - M)).  As in the
+// reference, P is rounded to bf16 before the P.V product while the row sum stays fp32.
+#include "da_common.hpp"
+
+namespace da {
+
+struct DecodeUpdateArgs {
+  const uint16_t* new_k;
+  const uint16_t* new_v;
+  int64_t sn_b, sn_h;
+  uint16_t* kx;
+  uint16_t* vx;
+  int64_t sx_b, sx_h, sx_s;
+  uint16_t* kp;
+  uint16_t* vp;
+  int64_t sp_b, sp_h, sp_s;
+  int32_t* counts;
+  int32_t* ts;
+  int64_t sc_b, sc_h;
+  int32_t* lengths;
+  int64_t capacity;
+  int64_t exact_len, total_len, window;
+  int B, H, D;
+  float thr;
+};
+
+template <bool COS>
+__global__ __launch_bounds__(256) void decode_update_kernel(DecodeUpdateArgs a) {
+#pragma clang fp contract(off)
+  const int lane = threadIdx.x & 63;
+  const int w = blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (w >= a.B * a.H) return;
+  const int b = w / a.H, h = w - (w / a.H) * a.H;
+  const bool act = 2 * lane < a.D;
+  const int64_t widx = a.exact_len % a.window;                       // :35
+  uint16_t* ring_k = a.kx + b * a.sx_b + h * a.sx_h + 2 * lane;
+  uint16_t* ring_v = a.vx + b * a.sx_b + h * a.sx_h + 2 * lane;
+  uint16_t* pk = a.kp + b * a.sp_b + h * a.sp_h + 2 * lane;
+  uint16_t* pv = a.vp + b * a.sp_b + h * a.sp_h + 2 * lane;
+  int32_t* cnt = a.counts + b * a.sc_b + h * a.sc_h;
+  int32_t* tsr = a.ts + b * a.sc_b + h * a.sc_h;
+  if (a.exact_len >= a.window) {                                     // :54
+    const uint32_t ek = act ? *(const uint32_t*)(ring_k + widx * a.sx_s) : 0u;
+    const uint32_t ev = act ? *(const uint32_t*)(ring_v + widx * a.sx_s) : 0u;
+    const int plen = a.lengths[w];
+    bool merge = false;
+    if (plen > 0) {                                                  // :61-77
+      const uint32_t lk = act ? *(const uint32_t*)(pk + (int64_t)(plen - 1) * a.sp_s) : 0u;
+      const float e0 = bf16_lo(ek), e1 = bf16_hi(ek), l0 = bf16_lo(lk), l1 = bf16_hi(lk);
+      if (COS) {
+        const float eps = 1e-8f;
+        const float dot = wave_tree_sum(pair_dot(e0, e1, l0, l1));
+        const float ne = __fsqrt_rn(wave_tree_sum(pair_dot(e0, e1, e0, e1)) + eps);
+        const float nl = __fsqrt_rn(wave_tree_sum(pair_dot(l0, l1, l0, l1)) + eps);
+        merge = __fdiv_rn(dot, ne * nl) >= a.thr;
+      } else {
+        const float d0 = e0 - l0, d1 = e1 - l1;
+        merge = wave_tree_sum(pair_dot(d0, d1, d0, d1)) <= a.thr;
+      }
+    }
+    if (merge) {                                                     // :78-82
+      if (lane == 0) cnt[plen - 1] += 1;
+    } else if (plen < a.capacity) {                                  // :83-96
+      if (act) {
+        *(uint32_t*)(pk + (int64_t)plen * a.sp_s) = ek;
+        *(uint32_t*)(pv + (int64_t)plen * a.sp_s) = ev;
+      }
+      if (lane == 0) {
+        cnt[plen] = 1;
+        tsr[plen] = (int32_t)(a.total_len - a.window);
+        a.lengths[w] = plen + 1;
+      }
+    }
+  }
+  // insert the new token into the ring (:101-104)
+  if (act) {
+    const uint32_t nk = *(const uint32_t*)(a.new_k + b * a.sn_b + h * a.sn_h + 2 * lane);
+    const uint32_t nv = *(const uint32_t*)(a.new_v + b * a.sn_b + h * a.sn_h + 2 * lane);
+    *(uint32_t*)(ring_k + widx * a.sx_s) = nk;
+    *(uint32_t*)(ring_v + widx * a.sx_s) = nv;
+  }
+}
+
+constexpr int kDecSlice = 256;
+constexpr int kDecMaxG = 8;
+constexpr int kDecD = 128;
+
+struct DecodeAttnArgs {
+  const uint16_t* q;
+  int64_t sq_b, sq_h;
+  const uint16_t* kp;
+  const uint16_t* vp;
+  int64_t sp_b, sp_h, sp_s;
+  const int32_t* counts;
+  int64_t sc_b, sc_h;
+  const int32_t* lengths;
+  int64_t capacity;
+  const uint16_t* kx;
+  const uint16_t* vx;
+  int64_t sx_b, sx_h, sx_s;
+  int exact_len;
+  float scale;
+  uint16_t* out;
+  int64_t so_b, so_h;
+  float* part;      // [B*Hkv][nslice][G][D + 2]: max, sum, P.V partial
+  int nslice;
+  int B, Hq, Hkv, G;
+};
+
+__device__ __forceinline__ float block_reduce(float v, float* sh, bool is_max) {
+  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) {
+    const float o = __shfl_xor(v, d, 64);
+    v = is_max ? __builtin_fmaxf(v, o) : v + o;
+  }
+  __syncthreads();
+  if (lane == 0) sh[wid] = v;
+  __syncthreads();
+  const float r = is_max ? __builtin_fmaxf(__builtin_fmaxf(sh[0], sh[1]), __builtin_fmaxf(sh[2], sh[3]))
+                         : (sh[0] + sh[1]) + (sh[2] + sh[3]);
+  return r;
+}
+
+__global__ __launch_bounds__(256) void decode_attn_kernel(DecodeAttnArgs a) {
+  __shared__ float s_q[kDecMaxG][kDecD];
+  __shared__ float s_p[kDecMaxG][kDecSlice];
+  __shared__ float s_acc[4][kDecMaxG][kDecD];
+  __shared__ float s_red[4];
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int bg = blockIdx.x, slice = blockIdx.y;
+  const int b = bg / a.Hkv, g = bg - (bg / a.Hkv) * a.Hkv;
+  const int G = a.G;
+  int plen = a.lengths[bg];
+  plen = plen < 0 ? 0 : (plen > a.capacity ? (int)a.capacity : plen);
+  const int total = plen + a.exact_len;
+  const int j0 = slice * kDecSlice;
+  if (j0 >= total) return;  // the combine kernel skips slices past the end
+
+  for (int i = tid; i < G * kDecD; i += 256) {
+    const int hh = i / kDecD, d = i - hh * kDecD;
+    const uint16_t* qrow = a.q + b * a.sq_b + (int64_t)(g * G + hh) * a.sq_h;
+    s_q[hh][d] = __uint_as_float((uint32_t)qrow[d] << 16);
+  }
+  __syncthreads();
+
+  // ---- scores: thread t scores key j0 + t for every head of the group ----
+  const int j = j0 + tid;
+  const bool valid = j < total;
+  float sc[kDecMaxG];
+#pragma unroll
+  for (int hh = 0; hh < kDecMaxG; ++hh) sc[hh] = -INFINITY;
+  if (valid) {
+    const uint16_t* krow;
+    float bias = 0.0f;
+    if (j < plen) {
+      krow = a.kp + b * a.sp_b + g * a.sp_h + (int64_t)j * a.sp_s;
+      const int c = a.counts[b * a.sc_b + g * a.sc_h + j];
+      bias = __logf((float)c);  // log(0) = -inf: padding anchors get no weight (:309-311)
+      if (c <= 0) bias = -INFINITY;
+    } else {
+      krow = a.kx + b * a.sx_b + g * a.sx_h + (int64_t)(j - plen) * a.sx_s;
+    }
+    float acc[kDecMaxG];
+#pragma unroll
+    for (int hh = 0; hh < kDecMaxG; ++hh) acc[hh] = 0.0f;
+#pragma unroll 4
+    for (int c8 = 0; c8 < kDecD / 8; ++c8) {
+      const u32x4 w = *(const u32x4*)(krow + 8 * c8);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float k0 = bf16_lo(w[e]), k1 = bf16_hi(w[e]);
+#pragma unroll
+        for (int hh = 0; hh < kDecMaxG; ++hh) {
+          if (hh < G) {
+            acc[hh] = __builtin_fmaf(s_q[hh][8 * c8 + 2 * e], k0, acc[hh]);
+            acc[hh] = __builtin_fmaf(s_q[hh][8 * c8 + 2 * e + 1], k1, acc[hh]);
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int hh = 0; hh < kDecMaxG; ++hh)
+      if (hh < G) sc[hh] = acc[hh] * a.scale + bias;
+  }
+
+  // ---- per-head slice max and sum; bf16-rounded weights to LDS ----
+  float* part = a.part + ((int64_t)bg * a.nslice + slice) * G * (kDecD + 2);
+  for (int hh = 0; hh < G; ++hh) {
+    const float m = block_reduce(sc[hh], s_red, true);
+    const float p = (sc[hh] == -INFINITY) ? 0.0f : __expf(sc[hh] - m);
+    const float l = block_reduce(p, s_red, false);
+    s_p[hh][tid] = __uint_as_float((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)p) << 16);
+    if (tid == 0) {
+      part[hh * (kDecD + 2)] = m;
+      part[hh * (kDecD + 2) + 1] = l;
+    }
+  }
+  __syncthreads();
+
+  // ---- P.V: wave w covers keys [64w, 64w + 64) of the slice, lane l dims 2l, 2l+1 ----
+  float av[kDecMaxG][2];
+#pragma unroll
+  for (int hh = 0; hh < kDecMaxG; ++hh) av[hh][0] = av[hh][1] = 0.0f;
+  for (int jj = wid * 64; jj < wid * 64 + 64; ++jj) {
+    const int jk = j0 + jj;
+    if (jk >= total) break;
+    const uint16_t* vrow = jk < plen ? a.vp + b * a.sp_b + g * a.sp_h + (int64_t)jk * a.sp_s
+                                     : a.vx + b * a.sx_b + g * a.sx_h + (int64_t)(jk - plen) * a.sx_s;
+    const uint32_t w = *(const uint32_t*)(vrow + 2 * lane);
+    const float v0 = bf16_lo(w), v1 = bf16_hi(w);
+#pragma unroll
+    for (int hh = 0; hh < kDecMaxG; ++hh)
+      if (hh < G) {
+        av[hh][0] = __builtin_fmaf(s_p[hh][jj], v0, av[hh][0]);
+        av[hh][1] = __builtin_fmaf(s_p[hh][jj], v1, av[hh][1]);
+      }
+  }
+#pragma unroll
+  for (int hh = 0; hh < kDecMaxG; ++hh)
+    if (hh < G) {
+      s_acc[wid][hh][2 * lane] = av[hh][0];
+      s_acc[wid][hh][2 * lane + 1] = av[hh][1];
+    }
+  __syncthreads();
+  for (int i = tid; i < G * kDecD; i += 256) {
+    const int hh = i / kDecD, d = i - hh * kDecD;
+    part[hh * (kDecD + 2) + 2 + d] = (s_acc[0][hh][d] + s_acc[1][hh][d]) + (s_acc[2][hh][d] + s_acc[3][hh][d]);
+  }
+}
+
+__global__ __launch_bounds__(128) void decode_combine_kernel(DecodeAttnArgs a) {
+  const int bhq = blockIdx.x;
+  const int b = bhq / a.Hq, hq = bhq - (bhq / a.Hq) * a.Hq;
+  const int g = hq / a.G, hh = hq - g * a.G;
+  const int bg = b * a.Hkv + g;
+  int plen = a.lengths[bg];
+  plen = plen < 0 ? 0 : (plen > a.capacity ? (int)a.capacity : plen);
+  const int total = plen + a.exact_len;
+  const int ns = (total + kDecSlice - 1) / kDecSlice;
+  const float* base = a.part + (int64_t)bg * a.nslice * a.G * (kDecD + 2) + hh * (kDecD + 2);
+  const int64_t sstride = (int64_t)a.G * (kDecD + 2);
+  float M = -INFINITY;
+  for (int s = 0; s < ns; ++s) M = __builtin_fmaxf(M, base[s * sstride]);
+  float L = 0.0f, acc = 0.0f;
+  const int d = threadIdx.x;
+  for (int s = 0; s < ns; ++s) {
+    const float ms = base[s * sstride];
+    if (ms == -INFINITY) continue;
+    const float f = __expf(ms - M);
+    L += base[s * sstride + 1] * f;
+    acc += base[s * sstride + 2 + d] * f;
+  }
+  a.out[b * a.so_b + hq * a.so_h + d] = __builtin_bit_cast(uint16_t, (__bf16)(acc / L));
+}
+
+}  // namespace da
+
+using namespace da;
+
+extern "C" int da_decode_update(const void* new_k, const void* new_v, int dtype, int64_t B,
+                                int64_t Hkv, int64_t D, int64_t sn_b, int64_t sn_h, void* k_exact,
+                                void* v_exact, int64_t sx_b, int64_t sx_h, int64_t sx_s,
+                                void* k_packed, void* v_packed, int64_t sp_b, int64_t sp_h,
+                                int64_t sp_s, int32_t* counts, int32_t* timestamps, int64_t sc_b,
+                                int64_t sc_h, int32_t* lengths, int64_t capacity,
+                                int64_t exact_seq_len, int64_t total_seq_len, int64_t window,
+                                float threshold, int use_cosine, void* stream) {
+  DA_REQUIRE(new_k && new_v && k_exact && v_exact && k_packed && v_packed && counts && timestamps && lengths,
+             "da_decode_update: null pointer");
+  if (dtype != DA_BF16) return set_error(DA_ERR_UNSUPPORTED, "da_decode_update: only bf16 is supported");
+  DA_REQUIRE(B > 0 && Hkv > 0 && window > 0 && capacity > 0, "da_decode_update: empty shape");
+  if (D > 128 || (D & 1)) return set_error(DA_ERR_UNSUPPORTED, "da_decode_update: head_dim must be even and <= 128");
+  DA_REQUIRE(exact_seq_len >= 0 && total_seq_len >= 0, "da_decode_update: negative lengths");
+  DA_REQUIRE(((sn_b | sn_h | sx_b | sx_h | sx_s | sp_b | sp_h | sp_s) & 1) == 0,
+             "da_decode_update: rows must be 4-byte aligned");
+  DecodeUpdateArgs a = {};
+  a.new_k = (const uint16_t*)new_k; a.new_v = (const uint16_t*)new_v; a.sn_b = sn_b; a.sn_h = sn_h;
+  a.kx = (uint16_t*)k_exact; a.vx = (uint16_t*)v_exact; a.sx_b = sx_b; a.sx_h = sx_h; a.sx_s = sx_s;
+  a.kp = (uint16_t*)k_packed; a.vp = (uint16_t*)v_packed; a.sp_b = sp_b; a.sp_h = sp_h; a.sp_s = sp_s;
+  a.counts = counts; a.ts = timestamps; a.sc_b = sc_b; a.sc_h = sc_h; a.lengths = lengths;
+  a.capacity = capacity; a.exact_len = exact_seq_len; a.total_len = total_seq_len; a.window = window;
+  a.B = (int)B; a.H = (int)Hkv; a.D = (int)D; a.thr = threshold;
+  const unsigned blocks = (unsigned)((B * Hkv + 3) / 4);
+  if (use_cosine)
+    hipLaunchKernelGGL(decode_update_kernel<true>, dim3(blocks), dim3(256), 0, (hipStream_t)stream, a);
+  else
+    hipLaunchKernelGGL(decode_update_kernel<false>, dim3(blocks), dim3(256), 0, (hipStream_t)stream, a);
+  return check_launch("da_decode_update");
+}
+
+extern "C" int64_t da_decode_workspace_size(int64_t B, int64_t Hq, int64_t capacity, int64_t window) {
+  const int64_t nslice = (capacity + window + kDecSlice - 1) / kDecSlice;
+  return B * Hq * nslice * (kDecD + 2) * (int64_t)sizeof(float);
+}
+
+extern "C" int da_decode_attention(const void* q, int dtype, int64_t B, int64_t Hq, int64_t Hkv,
+                                   int64_t D, int64_t sq_b, int64_t sq_h, const void* k_packed,
+                                   const void* v_packed, int64_t sp_b, int64_t sp_h, int64_t sp_s,
+                                   const int32_t* counts, int64_t sc_b, int64_t sc_h,
+                                   const int32_t* lengths, int64_t capacity, const void* k_exact,
+                                   const void* v_exact, int64_t sx_b, int64_t sx_h, int64_t sx_s,
+                                   int64_t window, int64_t exact_len, float scale, void* out,
+                                   int64_t so_b, int64_t so_h, void* workspace,
+                                   int64_t workspace_bytes, void* stream) {
+  DA_REQUIRE(q && k_packed && v_packed && counts && lengths && k_exact && v_exact && out,
+             "da_decode_attention: null pointer");
+  if (dtype != DA_BF16) return set_error(DA_ERR_UNSUPPORTED, "da_decode_attention: only bf16 is supported");
+  if (D != kDecD) return set_error(DA_ERR_UNSUPPORTED, "da_decode_attention: head_dim must be 128");
+  DA_REQUIRE(B > 0 && Hq > 0 && Hkv > 0 && Hq % Hkv == 0, "da_decode_attention: bad head counts");
+  if (Hq / Hkv > kDecMaxG) return set_error(DA_ERR_UNSUPPORTED, "da_decode_attention: GQA group above %d", kDecMaxG);
+  DA_REQUIRE(window > 0 && exact_len >= 0 && exact_len <= window && capacity > 0,
+             "da_decode_attention: bad cache lengths");
+  DA_REQUIRE(((sp_b | sp_h | sp_s | sx_b | sx_h | sx_s) & 7) == 0 && (((uintptr_t)k_packed | (uintptr_t)k_exact) & 15) == 0,
+             "da_decode_attention: key rows must be 16-byte aligned");
+  const int64_t need = da_decode_workspace_size(B, Hq, capacity, window);
+  if (!workspace || workspace_bytes < need)
+    return set_error(DA_ERR_WORKSPACE, "da_decode_attention: workspace of %lld bytes required", (long long)need);
+  DecodeAttnArgs a = {};
+  a.q = (const uint16_t*)q; a.sq_b = sq_b; a.sq_h = sq_h;
+  a.kp = (const uint16_t*)k_packed; a.vp = (const uint16_t*)v_packed; a.sp_b = sp_b; a.sp_h = sp_h; a.sp_s = sp_s;
+  a.counts = counts; a.sc_b = sc_b; a.sc_h = sc_h; a.lengths = lengths; a.capacity = capacity;
+  a.kx = (const uint16_t*)k_exact; a.vx = (const uint16_t*)v_exact; a.sx_b = sx_b; a.sx_h = sx_h; a.sx_s = sx_s;
+  a.exact_len = (int)exact_len; a.scale = scale; a.out = (uint16_t*)out; a.so_b = so_b; a.so_h = so_h;
+  a.part = (float*)workspace;
+  a.nslice = (int)((capacity + window + kDecSlice - 1) / kDecSlice);
+  a.B = (int)B; a.Hq = (int)Hq; a.Hkv = (int)Hkv; a.G = (int)(Hq / Hkv);
+  hipStream_t st = (hipStream_t)stream;
+  hipLaunchKernelGGL(decode_attn_kernel, dim3((unsigned)(B * Hkv), (unsigned)a.nslice), dim3(256), 0, st, a);
+  int rc = check_launch("da_decode_attention");
+  if (rc) return rc;
+  hipLaunchKernelGGL(decode_combine_kernel, dim3((unsigned)(B * Hq)), dim3(128), 0, st, a);
+  return check_launch("da_decode_attention(combine)");
+}

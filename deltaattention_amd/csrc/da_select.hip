@@ -21,26 +21,6 @@
 
 namespace da {
 
-__device__ __forceinline__ float wave_tree_sum(float t) {
-#pragma clang fp contract(off)
-  t = t + dpp_f32<kDppXor1>(t);
-  t = t + dpp_f32<kDppXor2>(t);
-  t = t + dpp_f32<kDppHalfMirror>(t);
-  t = t + dpp_f32<kDppMirror>(t);
-  const float r0 = readlane_f32(t, 0);
-  const float r1 = readlane_f32(t, 16);
-  const float r2 = readlane_f32(t, 32);
-  const float r3 = readlane_f32(t, 48);
-  return (r0 + r1) + (r2 + r3);
-}
-
-__device__ __forceinline__ float pair_dot(float x0, float x1, float y0, float y1) {
-#pragma clang fp contract(off)
-  const float p0 = x0 * y0;
-  const float p1 = x1 * y1;
-  return p0 + p1;
-}
-
 __device__ __forceinline__ void store_keep_bits(int32_t* keep_row, int64_t base, int64_t end,
                                                 uint64_t bits, int lane) {
   const int64_t r = base + lane;

@@ -128,6 +128,48 @@ int da_dense_prefill(const void* q, const void* k, const void* v, void* out, int
                      const int64_t* strides, int causal, float scale, void* stream);
 
 /*
+ * Decode step of the compressed cache.  Replaces fused_hybrid_decode_update_kernel
+ * (deltaDecoding.py:9-104) as launched by HybridCompressedCache.update (:181-211).
+ *
+ * new_k, new_v: [B, Hkv, 1, D] bf16 (strides sn_b, sn_h).
+ * k_exact, v_exact: ring [B, Hkv, W, D] (strides sx_*); k_packed, v_packed:
+ *   [B, Hkv, capacity, D] (strides sp_*); counts, timestamps: [B, Hkv, capacity]
+ *   int32 (strides sc_b, sc_h, packed axis contiguous); lengths: [B * Hkv] int32.
+ * exact_seq_len, total_seq_len: the cache's host trackers before this token.
+ * threshold: tau^2 (Euclidean, merge iff dist^2 <= tau^2) or tau (cosine, merge iff
+ *   cos >= tau).  When the ring is full the evicted token merges into the last packed
+ *   anchor or is appended (count 1, timestamp total - W); the new token then takes
+ *   ring slot exact_seq_len % W.  The caller keeps capacity > length (the reference's
+ *   host tracker, :185-187).
+ */
+int da_decode_update(const void* new_k, const void* new_v, int dtype, int64_t B, int64_t Hkv,
+                     int64_t D, int64_t sn_b, int64_t sn_h, void* k_exact, void* v_exact,
+                     int64_t sx_b, int64_t sx_h, int64_t sx_s, void* k_packed, void* v_packed,
+                     int64_t sp_b, int64_t sp_h, int64_t sp_s, int32_t* counts,
+                     int32_t* timestamps, int64_t sc_b, int64_t sc_h, int32_t* lengths,
+                     int64_t capacity, int64_t exact_seq_len, int64_t total_seq_len,
+                     int64_t window, float threshold, int use_cosine, void* stream);
+
+/*
+ * q_len = 1 attention over the compressed cache.  Replaces fused_hybrid_decode_kernel
+ * (deltaDecoding.py:236-362) and its wrapper (modeling_llama.py:453-518).
+ *
+ * q: [B, Hq, D] bf16 (strides sq_b, sq_h); query head h reads kv head h / (Hq / Hkv).
+ * Scores over the packed anchors [0, lengths[b*Hkv + g]) get + log(count); then the
+ * ring slots [0, exact_len) (exact_len = min(exact_seq_len, W)).  out: [B, Hq, D]
+ * (strides so_b, so_h).  D must be 128, Hq / Hkv <= 8.
+ */
+int64_t da_decode_workspace_size(int64_t B, int64_t Hq, int64_t capacity, int64_t window);
+int da_decode_attention(const void* q, int dtype, int64_t B, int64_t Hq, int64_t Hkv, int64_t D,
+                        int64_t sq_b, int64_t sq_h, const void* k_packed, const void* v_packed,
+                        int64_t sp_b, int64_t sp_h, int64_t sp_s, const int32_t* counts,
+                        int64_t sc_b, int64_t sc_h, const int32_t* lengths, int64_t capacity,
+                        const void* k_exact, const void* v_exact, int64_t sx_b, int64_t sx_h,
+                        int64_t sx_s, int64_t window, int64_t exact_len, float scale, void* out,
+                        int64_t so_b, int64_t so_h, void* workspace, int64_t workspace_bytes,
+                        void* stream);
+
+/*
  * strides for da_hybrid_prefill / da_dense_prefill: int64[3 * 8] element strides
  * (batch, head, sequence) of, in order: q, k, v, k_packed, v_packed, out,
  * timestamps (sequence stride must be 1), counts (sequence stride must be 1).

@@ -21,7 +21,8 @@ def declared_symbols():
 def test_header_declares_the_expected_entry_points():
     assert declared_symbols() == sorted([
         "da_last_error", "da_version", "da_select", "da_pack_workspace_size", "da_pack",
-        "da_hybrid_workspace_size", "da_hybrid_prefill", "da_dense_prefill"])
+        "da_hybrid_workspace_size", "da_hybrid_prefill", "da_dense_prefill",
+        "da_decode_update", "da_decode_workspace_size", "da_decode_attention"])
 
 
 def test_library_exports_every_declared_symbol():

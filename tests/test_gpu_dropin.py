@@ -1,0 +1,215 @@
+"""The reference-named modules, called the way modeling_llama.py calls them, and the
+decode path against the oracle's state machine."""
+import numpy as np
+import pytest
+import torch
+
+from conftest import announce
+from oracle import delta_oracle as O
+from oracle import select_oracle_c as OC
+
+pytestmark = pytest.mark.gpu
+
+MAX_ABS, MEAN_ABS = 2e-2, 1e-3
+
+
+def _inputs(B, Hq, Hkv, N, seed):
+    from deltaattention_amd import synth
+    return synth.make_layer_inputs(B, Hq, Hkv, N, 128, seed=seed, rope_base=10000.0)
+
+
+def _close(got, want, what):
+    got = np.asarray(got, dtype=np.float32)
+    err = np.abs(got - np.asarray(want, dtype=np.float32))
+    print(f"{what}: max-abs {err.max():.3e} mean-abs {err.mean():.3e}", flush=True)
+    assert np.isfinite(got).all()
+    assert err.max() <= MAX_ABS and err.mean() <= MEAN_ABS, (what, err.max(), err.mean())
+
+
+def _expand(t, G):
+    """repeat_kv (modeling_llama.py:223-232)."""
+    B, H, N = t.shape[:3]
+    return t[:, :, None].expand(B, H, G, *t.shape[2:]).reshape(B, H * G, *t.shape[2:])
+
+
+def test_flash_wrappers(gpu):
+    from deltaattention_amd.flashAttention import _attn_fwd_flat, triton_flash_attention
+    q, k, v = _inputs(1, 8, 2, 600, 1)
+    qg, kg, vg = q.to(gpu), k.to(gpu), v.to(gpu)
+    announce("triton_flash_attention GQA + expanded, _attn_fwd_flat launch")
+    a = triton_flash_attention(qg, kg, vg)
+    b = triton_flash_attention(qg, _expand(kg, 4), _expand(vg, 4))
+    out = torch.empty_like(qg)
+    ke, ve = _expand(kg, 4).contiguous(), _expand(vg, 4).contiguous()
+    _attn_fwd_flat[(5, 8, 1)](qg, ke, ve, 128 ** -0.5, out, *qg.stride(), *ke.stride(), *ve.stride(),
+                              *out.stride(), 1, 8, 600, HEAD_DIM=128, BLOCK_M=128, BLOCK_N=128,
+                              IS_CAUSAL=True, num_warps=8, num_stages=3)
+    ref = O.dense_attention(q.float().numpy(), k.float().numpy(), v.float().numpy())
+    for t, name in ((a, "gqa"), (b, "expanded"), (out, "kernel object")):
+        _close(t.float().cpu().numpy(), ref, f"flash {name}")
+
+
+def test_select_and_pack_kernel_objects(gpu):
+    """chunked_eval_kernel / parallel_scatter_pack_kv_kernel launched as in
+    modeling_llama.py:634-685."""
+    from deltaattention_amd.tritonModules import chunked_eval_kernel, parallel_scatter_pack_kv_kernel
+    q, k, v = _inputs(1, 4, 2, 1100, 2)
+    kg, vg = k.to(gpu), v.to(gpu)
+    bsz, H, q_len, D = kg.shape
+    chunk_size, num_chunks = 512, 3
+    keep_mask = torch.zeros((bsz, H, q_len), dtype=torch.int32, device=gpu)
+    chunk_counts = torch.zeros((bsz, H, num_chunks), dtype=torch.int32, device=gpu)
+    announce("chunked_eval_kernel object")
+    chunked_eval_kernel[(bsz * H, num_chunks)](
+        kg, keep_mask, chunk_counts, 9.0 ** 2, *kg.stride(), *keep_mask.stride(),
+        *chunk_counts.stride(), q_len, D, chunk_size, num_heads=H, BLOCK_D=128, USE_COSINE=False)
+    ok, occ = OC.select_delta(k.float().numpy(), 9.0, 512)
+    assert (keep_mask.cpu().numpy() == ok).all() and (chunk_counts.cpu().numpy() == occ).all()
+    index_map = (torch.cumsum(keep_mask, dim=-1) - 1).to(torch.int32)
+    P = int(chunk_counts.sum(-1).max().item())
+    k_packed = torch.zeros((bsz, H, P, D), device=gpu, dtype=kg.dtype)
+    v_packed = torch.zeros_like(k_packed)
+    ts = torch.zeros((bsz, H, P), device=gpu, dtype=torch.int32)
+    announce("parallel_scatter_pack_kv_kernel object")
+    parallel_scatter_pack_kv_kernel[(bsz * H, (q_len + 63) // 64)](
+        kg, vg, k_packed, v_packed, ts, keep_mask, index_map, *kg.stride(), *vg.stride(),
+        *k_packed.stride(), *v_packed.stride(), *ts.stride(), *keep_mask.stride(),
+        *index_map.stride(), q_len, D, H, BLOCK_S=64, BLOCK_D=128)
+    ref = O.pack(k.float().numpy(), v.float().numpy(), ok)
+    assert (ts.cpu().numpy() == ref["timestamps"]).all()
+    assert torch.equal(k_packed.float().cpu(), torch.from_numpy(ref["k_packed"]))
+    assert torch.equal(v_packed.float().cpu(), torch.from_numpy(ref["v_packed"]))
+
+
+@pytest.mark.parametrize("variant", ["hybrid", "sanity", "pure_phase1"])
+def test_hybrid_kernel_objects_on_expanded_inputs(gpu, variant):
+    """hybrid kernels launched as modeling_llama.py:334-353 on repeat_kv-expanded tensors
+    equal the GQA-native path and the oracle."""
+    from deltaattention_amd import deltaFlashAttention as dfa
+    from deltaattention_amd import ops
+    q, k, v = _inputs(1, 8, 2, 1300, 3)
+    qg, kg, vg = q.to(gpu), k.to(gpu), v.to(gpu)
+    keep, _ = ops.select(kg, 9.0, 512)
+    pk = ops.pack(keep, kg, vg).trimmed()
+    G = 4
+    ke, ve = _expand(kg, G).contiguous(), _expand(vg, G).contiguous()
+    kpe, vpe = _expand(pk.k_packed, G).contiguous(), _expand(pk.v_packed, G).contiguous()
+    tse = _expand(pk.timestamps, G).contiguous()
+    cne = _expand(pk.counts, G).contiguous().float()
+    out = torch.empty_like(qg)
+    kern = {"hybrid": dfa.hybrid_compressed_flash_kernel,
+            "sanity": dfa.hybrid_compressed_flash_kernel_sanity,
+            "pure_phase1": dfa.pure_phase1_flash_kernel}[variant]
+    announce(f"{variant} kernel object, expanded inputs")
+    kern[(11, 8, 1)](qg, ke, ve, kpe, vpe, tse, cne, out, *qg.stride(), *ke.stride(), *ve.stride(),
+                     *kpe.stride(), *vpe.stride(), *tse.stride(), *cne.stride(), *out.stride(),
+                     128 ** -0.5, 1300, 1300, kpe.shape[2], 128, 8, 128,
+                     BLOCK_M=128, BLOCK_N=128, BLOCK_D=128, num_warps=8, num_stages=1)
+    native = ops.hybrid_prefill(qg, kg, vg, pk.k_packed, pk.v_packed, pk.timestamps, pk.counts,
+                                window=128, variant=variant)
+    assert torch.allclose(out.float(), native.float(), atol=1e-2, rtol=0)
+    kf, vf = k.float().numpy(), v.float().numpy()
+    p = O.pack(kf, vf, keep.cpu().numpy())
+    ref = O.hybrid_attention(q.float().numpy(), kf, vf, p["k_packed"], p["v_packed"],
+                             p["timestamps"], p["counts"], 128, variant=variant)
+    _close(out.float().cpu().numpy(), ref, f"{variant} object")
+
+
+@pytest.mark.parametrize("mode", ["delta", "periodic"])
+def test_delta_prefill_attention_glue(gpu, mode):
+    """PATH 1 (modeling_llama.py:600-749) with the globVR knobs of eval_speedup.set_row_delta."""
+    from deltaattention_amd import attention, globVR
+    q, k, v = _inputs(1, 8, 2, 1500, 4)
+    saved = dict(vars(globVR))
+    try:
+        globVR.packing_mode = mode
+        globVR.row_delta_threshold = 9.0
+        globVR.row_similarity_metric = "euclidian"
+        globVR.chunk_size = 512
+        globVR.target_keep_rate = 0.3
+        globVR.dense_window_size = 128
+        globVR.time_internal = False
+        announce(f"delta_prefill_attention mode={mode}")
+        out = attention.delta_prefill_attention(q.to(gpu), k.to(gpu), v.to(gpu))
+        kf, vf = k.float().numpy(), v.float().numpy()
+        keep = OC.select_delta(kf, 9.0, 512)[0] if mode == "delta" else O.select_periodic(1, 2, 1500, 0.3)
+        p = O.pack(kf, vf, keep)
+        ref = O.hybrid_attention(q.float().numpy(), kf, vf, p["k_packed"], p["v_packed"],
+                                 p["timestamps"], p["counts"], 128)
+        _close(out.float().cpu().numpy(), ref, f"glue {mode}")
+        assert 0.0 < globVR.spars < 1.0
+    finally:
+        for name, val in saved.items():
+            setattr(globVR, name, val)
+
+
+def _oracle_cache_from_prefill(p, k, v, W, cap):
+    B, H, N, D = k.shape
+    P = p["P"]
+    st = O_decode_state(B, H, D, cap, W)
+    st["k_packed"][:, :, :P] = p["k_packed"]
+    st["v_packed"][:, :, :P] = p["v_packed"]
+    st["counts"][:, :, :P] = p["counts"]
+    st["timestamps"][:, :, :P] = p["timestamps"]
+    st["lengths"][:] = P
+    e = min(N, W)
+    st["k_exact"][:, :, :e] = k[:, :, -e:]
+    st["v_exact"][:, :, :e] = v[:, :, -e:]
+    st["exact_len"], st["total_len"] = e, N
+    return st
+
+
+def O_decode_state(B, H, D, cap, W):
+    return {"k_packed": np.zeros((B, H, cap, D), np.float32), "v_packed": np.zeros((B, H, cap, D), np.float32),
+            "counts": np.zeros((B, H, cap), np.int32), "timestamps": np.zeros((B, H, cap), np.int32),
+            "lengths": np.zeros(B * H, np.int32), "k_exact": np.zeros((B, H, W, D), np.float32),
+            "v_exact": np.zeros((B, H, W, D), np.float32), "exact_len": 0, "total_len": 0, "window": W}
+
+
+@pytest.mark.parametrize("metric,tau", [("euclidean", 9.5), ("cosine", 0.9)])
+def test_decode_cache_matches_oracle(gpu, metric, tau):
+    """Prefill hand-off then 80 decode steps: cache state bit-exact and attention within
+    tolerance against the oracle (deltaDecoding.py:9-362, modeling_llama.py:453-518)."""
+    from types import SimpleNamespace
+    from deltaattention_amd import attention, globVR, synth
+    from deltaattention_amd.deltaDecoding import HybridCompressedCache, decode_attention
+    B, Hq, Hkv, N, W, steps = 1, 8, 2, 700, 50, 80
+    q, k, v = _inputs(B, Hq, Hkv, N + steps, 5)
+    cfg = SimpleNamespace(hidden_size=Hq * 128, num_attention_heads=Hq, num_key_value_heads=Hkv,
+                          num_hidden_layers=1, head_dim=128)
+    saved = dict(vars(globVR))
+    try:
+        globVR.packing_mode, globVR.chunk_size = "delta", 512
+        globVR.row_delta_threshold, globVR.row_similarity_metric = tau, metric
+        globVR.time_internal = False
+        cache = HybridCompressedCache(cfg, B, dtype=torch.bfloat16, exact_window_size=W,
+                                      initial_capacity=64)
+        qg, kg, vg = q.to(gpu), k.to(gpu), v.to(gpu)
+        announce(f"decode {metric}: prefill hand-off")
+        attention.delta_prefill_attention(qg[:, :, :N], kg[:, :, :N], vg[:, :, :N], 0, cache)
+        kf, vf = k.float().numpy(), v.float().numpy()
+        keep, _ = OC.select_delta(kf[:, :, :N], tau, 512, 0, metric)
+        p = O.pack(kf[:, :, :N], vf[:, :, :N], keep)
+        st = _oracle_cache_from_prefill(p, kf[:, :, :N], vf[:, :, :N], W, cache.capacity + 4096)
+        outs = []
+        for t in range(steps):
+            if t == 0:
+                announce(f"decode {metric}: {steps} update+attention steps")
+            cache.update(kg[:, :, N + t:N + t + 1], vg[:, :, N + t:N + t + 1], 0)
+            outs.append(decode_attention(qg[:, :, N + t:N + t + 1], cache, 0))
+            O.decode_update(st, kf[:, :, N + t:N + t + 1], vf[:, :, N + t:N + t + 1], tau, metric)
+            if t in (0, steps - 1):
+                ref = O.decode_attention(q.float().numpy()[:, :, N + t], st)
+                _close(outs[-1][:, :, 0].float().cpu().numpy(), ref, f"decode attn step {t}")
+        n = int(cache.packed_lengths[0].max().item())
+        assert (cache.packed_lengths[0].cpu().numpy() == st["lengths"]).all()
+        assert (cache.packed_counts[0, :, :, :n].cpu().numpy() == st["counts"][:, :, :n]).all()
+        assert (cache.packed_timestamps[0, :, :, :n].cpu().numpy() == st["timestamps"][:, :, :n]).all()
+        assert torch.equal(cache.k_packed[0, :, :, :n].float().cpu(), torch.from_numpy(st["k_packed"][:, :, :n]))
+        assert torch.equal(cache.k_exact[0].float().cpu(), torch.from_numpy(st["k_exact"]))
+        assert cache.get_seq_length(0) == N + steps
+        merged = int(st["counts"].sum()) - N
+        print(f"decode {metric}: evicted {steps} tokens, packed length {n}, merged-in {merged}")
+    finally:
+        for name, val in saved.items():
+            setattr(globVR, name, val)
