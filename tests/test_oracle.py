@@ -346,3 +346,19 @@ def test_decode_attention_log_count_identity():
         s = keys @ q[0, h] * D ** -0.5
         e = np.exp(s - s.max())
         assert np.abs(out[0, h] - e @ vals / e.sum()).max() < 1e-5
+
+
+def test_decode_update_cosine_on_a_circle():
+    """Cosine merge (deltaDecoding.py:67-72): evicted keys rotate by theta per token, so
+    cos to the last packed key is cos((t - a) theta); with tau between cos(2 theta) and
+    cos(3 theta) every third evicted token is appended."""
+    W, T, D, theta = 3, 40, 8, 0.2
+    st = _decode_state(1, 1, D, 64, W)
+    tau = 0.5 * (np.cos(2 * theta) + np.cos(3 * theta))
+    for t in range(T):
+        kk = np.zeros((1, 1, 1, D), np.float32)
+        kk[..., 0], kk[..., 1] = np.cos(t * theta), np.sin(t * theta)
+        O.decode_update(st, kk, kk, tau, "cosine")
+    n = int(st["lengths"][0])
+    assert st["timestamps"][0, 0, :n].tolist() == list(range(0, T - W, 3))
+    assert st["counts"][0, 0, :n].sum() == T - W
