@@ -182,7 +182,8 @@ template <int VARIANT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void attn_kernel(AttnArgs a) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
-  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar)
   const int hl = lane >> 5;   // which half of the wave
   const int ql = lane & 31;   // query column of this lane
 
@@ -414,6 +415,388 @@ void attn_kernel(AttnArgs a) {
   }
 }
 
+// ====================================================================================
+// Ping-pong kernel for GQA groups that are a multiple of 4 (the Llama-3 hot path).
+//
+// A workgroup is 8 waves, two per SIMD.  Waves 0-3 (group A) own query rows
+// R0..R0+31 and waves 4-7 (group B) rows R0+32..R0+63, each wave one query head of a
+// GQA group of 4, so all 8 waves read the same K/V tiles.  Work is cut into sections
+// separated by workgroup barriers; in every section one group runs its matrix work
+// (P.V of the previous tile and Q.K of the current one: 32 MFMAs) while the other
+// runs its softmax (VALU), and the roles swap each section.  Group B runs one section
+// behind group A, so the two waves sharing a SIMD always have complementary work and
+// the MFMA pipe and the VALU co-execute.
+//
+// K tiles are staged one section pair ahead of V tiles: K(t+1) and V(t) are loaded in
+// even sections and written to LDS in odd ones (threads 256-511 stage K with the
+// per-key counts / timestamps, threads 0-255 stage V^T).  Two K and two V stages
+// (66.5 KiB) suffice because every stage is rewritten only after both groups read it.
+//
+// The running maximum is updated lazily: only when a tile's maximum exceeds it by
+// more than 2^8 in probability (8 in log2 units) are O and l rescaled, so p stays
+// below 256 and the rescale (64 multiplies) is rare.  The result is unchanged; only
+// the rounding reference point of bf16(p) moves.
+// ====================================================================================
+// Masks of tile scores.  Dense keys: causal (key <= row) and key < Nk.  Pure Phase 1:
+// key valid iff it is a live anchor with timestamp <= row (tl holds INT_MAX otherwise).
+__device__ __forceinline__ void mask_dense(f32x16* s, int key0, int row, int hl, int Nk, bool causal) {
+#pragma unroll
+  for (int kb2 = 0; kb2 < 2; ++kb2)
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int key = key0 + kb2 * 32 + 8 * (r >> 2) + 4 * hl + (r & 3);
+      const bool ok = key < Nk && (!causal || key <= row);
+      if (!ok) s[kb2][r] = -INFINITY;
+    }
+}
+__device__ __forceinline__ void mask_pure(f32x16* s, const int* tl, int row, int hl) {
+#pragma unroll
+  for (int kb2 = 0; kb2 < 2; ++kb2)
+#pragma unroll
+    for (int r4 = 0; r4 < 4; ++r4) {
+      const int4 t4 = *(const int4*)(tl + kb2 * 32 + 8 * r4 + 4 * hl);
+      if (!(t4.x <= row)) s[kb2][4 * r4 + 0] = -INFINITY;
+      if (!(t4.y <= row)) s[kb2][4 * r4 + 1] = -INFINITY;
+      if (!(t4.z <= row)) s[kb2][4 * r4 + 2] = -INFINITY;
+      if (!(t4.w <= row)) s[kb2][4 * r4 + 3] = -INFINITY;
+    }
+}
+
+// Scheduling pattern for a block of 16 LDS operand reads feeding 16 MFMAs: four reads
+// are issued ahead, then reads and MFMAs alternate, so an MFMA rarely waits for LDS.
+__device__ __forceinline__ void pipe_mfma_reads() {
+  __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);  // DS read x4
+#pragma unroll
+  for (int i = 0; i < 12; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+  }
+  __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);  // MFMA x4
+}
+
+// Third dword of a raw buffer resource on gfx9 (32-bit data format, no swizzle).
+constexpr int kBufferDword3 = 0x00020000;
+
+// A wave-uniform pointer moved into scalar registers.
+__device__ __forceinline__ const void* uniform_ptr(const void* p) {
+  const uint64_t v = (uint64_t)p;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  return (const void*)(((uint64_t)hi << 32) | lo);
+}
+
+constexpr int kPPK = kKBytes + kTileN * 8;   // K tile + float counts[64] + int ts[64]
+constexpr int kPPV = kVBytes;
+constexpr int kPPLds = 2 * kPPK + 2 * kPPV;
+constexpr int kPPCnt = kKBytes;
+constexpr int kPPTs = kKBytes + kTileN * 4;
+constexpr float kLazyLog2 = 8.0f;
+
+template <int VARIANT>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void attn_pp_kernel(AttnArgs a) {
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  char* const kst0 = smem;
+  char* const vst0 = smem + 2 * kPPK;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wid = tid >> 6;  // uniform per wave; kept as a VGPR value (lower register pressure)
+  const int grp = wid >> 2, hw = wid & 3;
+  const int hl = lane >> 5, ql = lane & 31;
+
+  // ---- workgroup -> (unit, row group): XCD-aware, longest rows first ----
+  const int wg = blockIdx.x;
+  int unit, rg;
+  if ((a.units & 7) == 0) {
+    const int xcd = wg & 7, idx = wg >> 3, upx = a.units >> 3;
+    unit = xcd * upx + idx % upx;
+    rg = a.n_row_groups - 1 - idx / upx;
+  } else {
+    unit = wg % a.units;
+    rg = a.n_row_groups - 1 - wg / a.units;
+  }
+  const int hunits = a.G >> 2;
+  const int bg = unit / hunits;
+  const int hu = unit - bg * hunits;
+  const int b = bg / a.Hkv, g = bg - (bg / a.Hkv) * a.Hkv;
+  const int h = g * a.G + hu * 4 + hw;
+  const int R0 = rg * 64;
+  const int r0w = R0 + grp * 32;
+  const int wg_end = R0 + 64;
+  const int start_m = (R0 / kBlock) * kBlock;
+  const int row = r0w + ql;
+
+  // ---- schedule (identical to attn_kernel) ----
+  int P = a.P_host;
+  if (a.P_dev) P = min(*a.P_dev, a.P_host);
+  int n1 = 0, ds = 0;
+  int kend = a.causal ? min(a.Nk, wg_end) : a.Nk;
+  if (VARIANT == kHybrid || VARIANT == kSanity) {
+    const int nblk = (P + kBlock - 1) / kBlock;
+    const int32_t* bmax = a.sched + (int64_t)bg * 2 * a.nblk_cap;
+    const int32_t* pmax = bmax + a.nblk_cap;
+    const int thr = start_m - a.window;
+    int lo = 0, hi = nblk;
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      if (pmax[mid] < thr) lo = mid + 1; else hi = mid;
+    }
+    const int last = lo > 0 ? bmax[lo - 1] : -1;
+    ds = max(0, ((last + 1) / kBlock) * kBlock);
+    if (VARIANT == kHybrid) n1 = lo * (kBlock / kTileN);
+    kend = min(a.Nk, wg_end);
+  } else if (VARIANT == kPure) {
+    n1 = (P + kTileN - 1) / kTileN;
+    kend = 0;
+  }
+  const int n2 = kend > ds ? (kend - ds + kTileN - 1) / kTileN : 0;
+  const int T = n1 + n2;
+
+  const uint16_t* kp_base = a.kp + (int64_t)b * a.skp_b + (int64_t)g * a.skp_h;
+  const uint16_t* vp_base = a.vp + (int64_t)b * a.svp_b + (int64_t)g * a.svp_h;
+  const uint16_t* k_base = a.k + (int64_t)b * a.sk_b + (int64_t)g * a.sk_h;
+  const uint16_t* v_base = a.v + (int64_t)b * a.sv_b + (int64_t)g * a.sv_h;
+  const int32_t* ts_row = a.ts ? a.ts + (int64_t)b * a.sts_b + (int64_t)g * a.sts_h : nullptr;
+  const char* cnt_row = a.cnt ? (const char*)a.cnt + ((int64_t)b * a.scnt_b + (int64_t)g * a.scnt_h) * 4 : nullptr;
+  constexpr bool kPureV = VARIANT == kPure;
+  constexpr bool kWeights = VARIANT == kHybrid || VARIANT == kPure;
+
+  auto key0_of = [&](int t) { return t < n1 ? t * kTileN : ds + (t - n1) * kTileN; };
+  auto skipped = [&](int t) { return t >= n1 && a.causal && key0_of(t) > r0w + 31; };
+
+  // ---- staging: waves 4-7 stage K (+ counts, timestamps), waves 0-3 stage V ----
+  // Rows are fetched with buffer loads whose resource covers exactly the tile's valid
+  // keys, so rows past the end of the keys read as zero without any select, and the
+  // tile base lives in scalar registers (no 64-bit per-lane address arithmetic).  The
+  // tile index is clamped; staging slots past the last tile are loaded and written too,
+  // the schedule below never reads them and the LDS stages they land in are free then.
+  const bool kthr = wid >= 4;
+  const int tq = tid & 255;
+  const int s_chunk = kthr ? (tq & 15) : (tq >> 4);  // 16-byte chunk of the row
+  const int s_grp = kthr ? (tq >> 4) : (tq & 15);    // group of 4 keys
+  const char* sb1 = (const char*)uniform_ptr(kthr ? kp_base : vp_base);  // Phase-1 source
+  const char* sb2 = (const char*)uniform_ptr(kthr ? k_base : v_base);    // Phase-2 source
+  const int sn1b = __builtin_amdgcn_readfirstlane((int)(2 * (kthr ? a.skp_n : a.svp_n)));  // bytes
+  const int sn2b = __builtin_amdgcn_readfirstlane((int)(2 * (kthr ? a.sk_n : a.sv_n)));
+  struct SRegs {
+    u32x4 x[4];
+    int ts;
+    int craw;  // count word as loaded (float or int32 bits)
+    bool cvalid;
+  };
+  auto stage_load = [&](SRegs& R, int t_raw) {
+    const int t = min(t_raw, T - 1);
+    const bool ph1 = t < n1;
+    const int key0 = key0_of(t);
+    const int limit = ph1 ? P : a.Nk;
+    const int snb = ph1 ? sn1b : sn2b;
+    const void* base = uniform_ptr((ph1 ? sb1 : sb2) + (int64_t)key0 * snb);
+    const int nrows = max(0, min(limit - key0, kTileN));
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<void*>(base), (short)0, __builtin_amdgcn_readfirstlane(nrows * snb), kBufferDword3);
+    const int voff = s_grp * 4 * snb + s_chunk * 16;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      R.x[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, voff + j * snb, 0, 0));
+    if (kWeights) {
+      // raw words only; conversion and validity are applied in stage_store
+      const int key = key0 + (tq & 63);
+      const int kc = max(min(key, P - 1), 0);
+      R.cvalid = ph1 && key < P;
+      R.craw = P > 0 ? ((const int32_t*)cnt_row)[kc] : 0;
+      if (kPureV) R.ts = P > 0 ? ts_row[kc] : INT_MAX;
+    }
+  };
+  auto stage_store = [&](const SRegs& R, int t) {
+    if (kthr) {
+      char* st = kst0 + (t & 1) * kPPK;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) *(u32x4*)(st + k_lds_off(s_grp * 4 + j, s_chunk)) = R.x[j];
+      if (kWeights && tq < kTileN) {
+        const float cv0 = a.cnt_is_float ? __int_as_float(R.craw) : (float)R.craw;
+        const float cv = R.cvalid ? (a.no_count ? 1.0f : cv0) : 0.0f;
+        ((float*)(st + kPPCnt))[tq] = cv;
+        if (kPureV) ((int*)(st + kPPTs))[tq] = cv > 0.0f ? R.ts : INT_MAX;
+      }
+    } else {
+      char* st = vst0 + (t & 1) * kPPV - kKBytes;  // vt_lds_* offsets include kKBytes
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const uint32_t x0 = R.x[0][w], x1 = R.x[1][w], x2 = R.x[2][w], x3 = R.x[3][w];
+        const int d0 = s_chunk * 8 + 2 * w;
+        u32x2 lo, hi;
+        lo[0] = __builtin_amdgcn_perm(x1, x0, 0x05040100u);
+        lo[1] = __builtin_amdgcn_perm(x3, x2, 0x05040100u);
+        hi[0] = __builtin_amdgcn_perm(x1, x0, 0x07060302u);
+        hi[1] = __builtin_amdgcn_perm(x3, x2, 0x07060302u);
+        *(u32x2*)(st + vt_lds_group(d0, s_grp)) = lo;
+        *(u32x2*)(st + vt_lds_group(d0 + 1, s_grp)) = hi;
+      }
+    }
+  };
+
+  // ---- per-lane LDS offsets (stage-relative) ----
+  int k_off[kD / 16];
+#pragma unroll
+  for (int tt = 0; tt < kD / 16; ++tt) k_off[tt] = k_lds_off(ql, 2 * tt + hl);  // + 8192 * kb2
+  int v_off[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) v_off[u] = vt_lds_chunk(ql, 2 * u + hl) - kKBytes;  // + 4096 * db
+
+  // ---- Q^T in registers ----
+  bf16x8 qreg[kD / 16];
+  {
+    const uint16_t* qrow = a.q + (int64_t)b * a.sq_b + (int64_t)h * a.sq_h + (int64_t)row * a.sq_n;
+#pragma unroll
+    for (int t = 0; t < kD / 16; ++t) {
+      u32x4 w = (row < a.Nq) ? *(const u32x4*)(qrow + 16 * t + 8 * hl) : u32x4{0, 0, 0, 0};
+      qreg[t] = __builtin_bit_cast(bf16x8, w);
+    }
+    // Redefine Q^T here so the loop does not see it as an outstanding load: otherwise
+    // every S = K Q^T block waits for all memory loads, including the staging loads
+    // meant to land two sections later.
+#pragma unroll
+    for (int t = 0; t < kD / 16; ++t) asm volatile("" : "+v"(qreg[t]));
+  }
+
+  f32x16 o[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) o[i] = f32x16{};
+  f32x16 s[2];
+  u32x4 pw[4];
+  float m_used = -INFINITY, l_i = 0.0f;
+  const float c = a.scale_log2;
+
+  // K(t + 1) is written to LDS by waves 4-7 at the end of section 2t, V(t) by waves
+  // 0-3 at the end of section 2t + 1: always by the group in its softmax section, and
+  // each stage is free by then (K(t - 1) was last read in section 2t - 1, V(t - 2) in
+  // section 2t - 1).  The loads of the next tile are issued right after each store, so
+  // every load has two sections to land.
+  SRegs sr;
+  sr.ts = 0;
+  sr.craw = 0;
+  sr.cvalid = false;
+  if (T > 0) {
+    if (kthr) {
+      stage_load(sr, 0);
+      stage_store(sr, 0);
+    }
+    stage_load(sr, kthr ? 1 : 0);
+  }
+  lds_barrier();
+
+  const int nsec = T > 0 ? 2 * T + 2 : 0;
+  for (int sec = 0; sec < nsec; ++sec) {
+    const int tl = sec >> 1;
+    const int sw = sec - grp;
+    if (sw >= 0) {
+      const int t = sw >> 1;
+      if ((sw & 1) == 0) {
+        // ---- matrix section: O^T += V^T P^T for tile t-1, then S^T = K Q^T for tile t ----
+        if (t >= 1 && !skipped(t - 1)) {
+          const char* vst = vst0 + ((t - 1) & 1) * kPPV;
+#pragma unroll
+          for (int u = 0; u < 4; ++u) {
+            const bf16x8 pbv = __builtin_bit_cast(bf16x8, pw[u]);
+#pragma unroll
+            for (int db = 0; db < 4; ++db) {
+              const u32x4 vw = *(const u32x4*)(vst + v_off[u] + db * 4096);
+              o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, vw), pbv,
+                                                               o[db], 0, 0, 0);
+            }
+          }
+          pipe_mfma_reads();
+        }
+        if (t < T && !skipped(t)) {
+          const char* kst = kst0 + (t & 1) * kPPK;
+#pragma unroll
+          for (int kb2 = 0; kb2 < 2; ++kb2) {
+            s[kb2] = f32x16{};
+#pragma unroll
+            for (int tt = 0; tt < kD / 16; ++tt) {
+              const u32x4 w = *(const u32x4*)(kst + k_off[tt] + kb2 * 8192);
+              s[kb2] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, w),
+                                                                qreg[tt], s[kb2], 0, 0, 0);
+            }
+          }
+          pipe_mfma_reads();
+        }
+      } else if (t < T && !skipped(t)) {
+        // ---- softmax section for tile t ----
+        const char* kst = kst0 + (t & 1) * kPPK;
+        const int key0 = key0_of(t);
+        if (kPureV) {
+          mask_pure(s, (const int*)(kst + kPPTs), row, hl);
+        } else if (t >= n1) {
+          if ((a.causal && key0 + kTileN - 1 > r0w) || key0 + kTileN > a.Nk)
+            mask_dense(s, key0, row, hl, a.Nk, a.causal);
+        }
+        float mx = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = __builtin_fmaxf(mx, __builtin_fmaxf(s[0][r], s[1][r]));
+        mx = __builtin_fmaxf(mx, swap_halves(mx));
+        const bool upd = (mx - m_used) * c > kLazyLog2;
+        if (__ballot(upd)) {
+          const float m_new = upd ? mx : m_used;
+          const float alpha = exp2_fast((m_used - m_new) * c);
+#pragma unroll
+          for (int db = 0; db < 4; ++db)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
+          l_i *= alpha;
+          m_used = m_new;
+        }
+        const float neg = (m_used == -INFINITY) ? 0.0f : -m_used * c;
+        const bool weighted = kWeights && t < n1;
+        const float* cl = (const float*)(kst + kPPCnt);
+        float psum = 0.0f;
+#pragma unroll
+        for (int kb2 = 0; kb2 < 2; ++kb2) {
+#pragma unroll
+          for (int r4 = 0; r4 < 4; ++r4) {
+            float p[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) p[e] = exp2_fast(__builtin_fmaf(s[kb2][4 * r4 + e], c, neg));
+            if (weighted) {
+              const f32x4 w4 = *(const f32x4*)(cl + kb2 * 32 + 8 * r4 + 4 * hl);
+#pragma unroll
+              for (int e = 0; e < 4; ++e) p[e] *= w4[e];
+            }
+            psum += (p[0] + p[1]) + (p[2] + p[3]);
+            pw[2 * kb2 + (r4 >> 1)][(r4 & 1) * 2 + 0] = pack_bf16x2(p[0], p[1]);
+            pw[2 * kb2 + (r4 >> 1)][(r4 & 1) * 2 + 1] = pack_bf16x2(p[2], p[3]);
+          }
+        }
+        l_i += psum;
+      }
+    }
+    if (kthr == ((sec & 1) == 0)) {
+      stage_store(sr, kthr ? tl + 1 : tl);
+      stage_load(sr, kthr ? tl + 2 : tl + 1);
+    }
+    lds_barrier();
+  }
+
+  // ---- finalize ----
+  const float l_tot = l_i + swap_halves(l_i);
+  float inv;
+  if (VARIANT == kPure)
+    inv = l_tot > 0.0f ? 1.0f / l_tot : 1.0f;  // deltaFlashAttention.py:353-354
+  else
+    inv = 1.0f / l_tot;
+  if (row < a.Nq) {
+    uint16_t* orow = a.out + (int64_t)b * a.so_b + (int64_t)h * a.so_h + (int64_t)row * a.so_n;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        u32x2 w;
+        w[0] = pack_bf16x2(o[db][4 * j + 0] * inv, o[db][4 * j + 1] * inv);
+        w[1] = pack_bf16x2(o[db][4 * j + 2] * inv, o[db][4 * j + 3] * inv);
+        *(u32x2*)(orow + db * 32 + 8 * j + 4 * hl) = w;
+      }
+  }
+}
+
 // Per (batch, kv head): maxima of packed blocks of 128 timestamps (lanes at or
 // beyond P read seq_len_k + 1, deltaFlashAttention.py:70) and their prefix maxima.
 __global__ __launch_bounds__(256) void hybrid_schedule_kernel(const int32_t* __restrict__ ts,
@@ -424,7 +807,8 @@ __global__ __launch_bounds__(256) void hybrid_schedule_kernel(const int32_t* __r
                                                               int32_t* __restrict__ sched) {
   __shared__ int32_t s_bmax[4096];
   __shared__ int32_t s_wave[4];
-  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar)
   const int bg = blockIdx.x;
   const int b = bg / Hkv, g = bg - (bg / Hkv) * Hkv;
   int P = P_host;
@@ -477,6 +861,42 @@ static int allow_lds(size_t bytes) {
   return DA_OK;
 }
 
+template <int V>
+static int allow_lds_pp(size_t bytes) {
+  static int done = 0;
+  if (!done) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_pp_kernel<V>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+    if (e != hipSuccess) return set_error(DA_ERR_HIP, "hipFuncSetAttribute: %s", hipGetErrorString(e));
+    done = 1;
+  }
+  return DA_OK;
+}
+
+// GQA groups that are a multiple of 4 run the ping-pong kernel (64 rows x 4 heads per
+// workgroup of 8 waves); other groups run attn_kernel.
+static int launch_attn_pp(int variant, AttnArgs& a, hipStream_t st) {
+  a.rows_per_wg = 64;
+  a.n_row_groups = (a.Nq + 63) / 64;
+  const size_t lds = kPPLds;
+  const unsigned grid = (unsigned)((int64_t)a.n_row_groups * a.units);
+  int rc = DA_OK;
+  switch (variant) {
+    case kHybrid: rc = allow_lds_pp<kHybrid>(lds); break;
+    case kSanity: rc = allow_lds_pp<kSanity>(lds); break;
+    case kPure: rc = allow_lds_pp<kPure>(lds); break;
+    default: rc = allow_lds_pp<kDense>(lds); break;
+  }
+  if (rc) return rc;
+  switch (variant) {
+    case kHybrid: hipLaunchKernelGGL(attn_pp_kernel<kHybrid>, dim3(grid), dim3(512), lds, st, a); break;
+    case kSanity: hipLaunchKernelGGL(attn_pp_kernel<kSanity>, dim3(grid), dim3(512), lds, st, a); break;
+    case kPure: hipLaunchKernelGGL(attn_pp_kernel<kPure>, dim3(grid), dim3(512), lds, st, a); break;
+    default: hipLaunchKernelGGL(attn_pp_kernel<kDense>, dim3(grid), dim3(512), lds, st, a); break;
+  }
+  return check_launch("attention kernel (ping-pong)");
+}
+
 static int launch_attn(int variant, AttnArgs& a, hipStream_t st) {
   const size_t lds = 2 * kStageBytes;
   const unsigned grid = (unsigned)((int64_t)a.n_row_groups * a.units);
@@ -488,6 +908,7 @@ static int launch_attn(int variant, AttnArgs& a, hipStream_t st) {
     default: rc = allow_lds<kDense>(lds); break;
   }
   if (rc) return rc;
+  if (a.hpw == 4) return launch_attn_pp(variant, a, st);
   switch (variant) {
     case kHybrid:
       hipLaunchKernelGGL(attn_kernel<kHybrid>, dim3(grid), dim3(256), lds, st, a);
@@ -519,6 +940,9 @@ static int fill_common(AttnArgs& a, const void* q, const void* k, const void* v,
   for (int i = 0; i < 18; ++i)
     DA_REQUIRE((st[i] & 7) == 0, "%s: strides must be multiples of 8 elements (stride %d = %lld)", who, i, (long long)st[i]);
   DA_REQUIRE(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out), "%s: tensors must be 16-byte aligned", who);
+  for (int i : {DA_STRIDE_K + 2, DA_STRIDE_V + 2})
+    DA_REQUIRE(st[i] >= kD && st[i] < (1ll << 24),
+               "%s: key/value sequence strides must be in [head_dim, 2^24) (stride %d = %lld)", who, i, (long long)st[i]);
   a.q = (const uint16_t*)q; a.k = (const uint16_t*)k; a.v = (const uint16_t*)v; a.out = (uint16_t*)out;
   a.sq_b = st[DA_STRIDE_Q]; a.sq_h = st[DA_STRIDE_Q + 1]; a.sq_n = st[DA_STRIDE_Q + 2];
   a.sk_b = st[DA_STRIDE_K]; a.sk_h = st[DA_STRIDE_K + 1]; a.sk_n = st[DA_STRIDE_K + 2];
@@ -564,6 +988,9 @@ extern "C" int da_hybrid_prefill(const void* q, const void* k, const void* v, co
   DA_REQUIRE(num_packed > 0 && num_packed <= 4096 * kBlock, "da_hybrid_prefill: num_packed must be in [1, %d]", 4096 * kBlock);
   DA_REQUIRE(window >= 0 && window < (1ll << 30), "da_hybrid_prefill: window must be >= 0");
   DA_REQUIRE(aligned16(k_packed) && aligned16(v_packed), "da_hybrid_prefill: packed tensors must be 16-byte aligned");
+  for (int i : {DA_STRIDE_KP + 2, DA_STRIDE_VP + 2})
+    DA_REQUIRE(strides[i] >= kD && strides[i] < (1ll << 24),
+               "da_hybrid_prefill: packed sequence strides must be in [head_dim, 2^24) (stride %d = %lld)", i, (long long)strides[i]);
   DA_REQUIRE(strides[DA_STRIDE_TS + 2] == 1 && strides[DA_STRIDE_CNT + 2] == 1,
              "da_hybrid_prefill: timestamps and counts must be contiguous along the packed axis");
   if (!workspace || workspace_bytes < da_hybrid_workspace_size(B, Hkv, num_packed))

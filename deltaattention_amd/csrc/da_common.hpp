@@ -67,6 +67,14 @@ __device__ __forceinline__ float readlane_f32(float v, int lane) {
   return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
 }
 
+// Workgroup barrier that orders LDS accesses only: unlike __syncthreads() it does not
+// wait for outstanding global loads, so prefetches stay in flight across it.
+__device__ __forceinline__ void lds_barrier() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup", "local");
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup", "local");
+}
+
 // Fixed-order fp32 sum over a wave where lane l holds the pair sum of head-dimension
 // slots 2l and 2l+1 (level 1 of a perfect pairwise tree over 128 slots): DPP lane^1,
 // lane^2, 8-lane mirror and 16-lane mirror give levels 2-5, then (r0 + r1) + (r2 + r3)

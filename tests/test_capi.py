@@ -78,9 +78,16 @@ def test_attention_rejects_bad_shapes():
                                  f, 0, 0, fake, 1 << 20, None) == -1
     assert lib.da_hybrid_prefill(*args, 3, fake, 1, 1, 4, 2, 64, 64, 128, st, 10, None, 0,
                                  f, 7, 0, fake, 1 << 20, None) == -1
-    st2 = _native.strides_array([0] * 18 + [0, 0, 1, 0, 0, 1])
+    # (batch, head, sequence) strides of q, k, v, k_packed, v_packed, out, timestamps, counts
+    rows = [8192, 8192, 128]
+    st2 = _native.strides_array(rows * 6 + [0, 0, 1, 0, 0, 1])
     assert lib.da_hybrid_prefill(*args, 3, fake, 1, 1, 4, 2, 64, 64, 128, st2, 10, None, 0,
                                  f, 0, 0, None, 0, None) == -4
+    # key/value rows that overlap (sequence stride below head_dim) are refused
+    st3 = _native.strides_array(rows * 3 + [8192, 8192, 64] + rows * 2 + [0, 0, 1, 0, 0, 1])
+    assert lib.da_hybrid_prefill(*args, 3, fake, 1, 1, 4, 2, 64, 64, 128, st3, 10, None, 0,
+                                 f, 0, 0, fake, 1 << 20, None) == -1
+    assert b"sequence strides" in lib.da_last_error()
 
 
 def test_workspace_sizes():
