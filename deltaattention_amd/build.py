@@ -25,6 +25,9 @@ HIPCC_FLAGS = [
     "-O3", "-std=c++17", "-fPIC", f"--offload-arch={ARCH}",
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-fno-honor-nans",
+    # MFMA accumulators in VGPRs: the softmax reads S with VALU instructions, and the
+    # AGPR form would copy every S element through v_accvgpr_read
+    "-mllvm", "-amdgpu-mfma-vgpr-form",
     "-Wall", "-Wno-unused-result", "-Wno-unused-function",
 ]
 

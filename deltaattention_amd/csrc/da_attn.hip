@@ -39,6 +39,11 @@
 // c = scale * log2(e) -- the same values as exp(s*scale - m*scale).  In Phase 1
 // p is multiplied by the anchor count in fp32 and then rounded to bf16 for the
 // P.V product while l accumulates the fp32 weights (deltaFlashAttention.py:86-98).
+#include <cstdlib>
+#include <cstring>
+#include <type_traits>
+#include <utility>
+
 #include "da_common.hpp"
 
 namespace da {
@@ -485,9 +490,76 @@ __device__ __forceinline__ const void* uniform_ptr(const void* p) {
   return (const void*)(((uint64_t)hi << 32) | lo);
 }
 
+// Workgroup barrier after the wave's own LDS reads and writes are done, leaving
+// loads to LDS (buffer_load ... lds) in flight.  A fence for LDS would wait for those
+// too (vmcnt(0)): the loads issued in this window are only read after the next
+// barrier, and their wait is explicit.  The asm is a compiler memory barrier.
+__device__ __forceinline__ void barrier_keep_loads() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef short i16x8 __attribute__((ext_vector_type(8)));
+typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+
+// LDS byte address of a pointer into the kernel's LDS.
+__device__ __forceinline__ uint32_t lds_addr(const void* p) {
+  return (uint32_t)(uintptr_t)(const __attribute__((address_space(3))) char*)p;
+}
+// ds_read_b64_tr_b16 at addr + OFF: in each group of 16 lanes, lane i receives element
+// i % 4 of the 8 bytes read by lanes 4e + i / 4, e = 0..3 (a 4 x 4 transpose of 16-bit
+// elements per group of four lanes).  Issued as asm: the caller waits with lgkm_wait.
+template <int OFF>
+__device__ __forceinline__ i16x4 ds_read_tr16(uint32_t addr) {
+  i16x4 v;
+  asm volatile("ds_read_b64_tr_b16 %0, %1 offset:%2" : "=v"(v) : "v"(addr), "i"(OFF));
+  return v;
+}
+// s_waitcnt lgkmcnt(N) that the uses of a and b cannot move above.
+template <int N>
+__device__ __forceinline__ void lgkm_wait(i16x4& a, i16x4& b) {
+  asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(a), "+v"(b) : "i"(N));
+}
+template <typename F, int... I>
+__device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
+  (f(std::integral_constant<int, I>{}), ...);
+}
+// f(integral_constant<int, i>) for i = 0 .. N-1, in order
+template <int N, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  static_for_impl(f, std::make_integer_sequence<int, N>{});
+}
+
+// Max / sum of x over lanes l and l ^ 32, without LDS (v_permlane32_swap); the order
+// of the returned pair does not matter for either.
+__device__ __forceinline__ float halves_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __builtin_fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float halves_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// s_waitcnt immediate (gfx9 encoding) that waits for vmcnt <= n only.
+constexpr int vmcnt_only(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
+
+// As pipe_mfma_reads, for P.V blocks whose operand takes two transpose reads.
+__device__ __forceinline__ void pipe_mfma_reads_tr() {
+  __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);  // DS read x8
+#pragma unroll
+  for (int i = 0; i < 12; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // DS read x2
+  }
+  __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);  // MFMA x4
+}
+
 constexpr int kPPK = kKBytes + kTileN * 8;   // K tile + float counts[64] + int ts[64]
 constexpr int kPPV = kVBytes;
 constexpr int kPPLds = 2 * kPPK + 2 * kPPV;
+constexpr int kDmaMetaSlot = kTileN * 8;  // float weights[64], int timestamps[64]
+constexpr int kDmaLds = 3 * kKBytes + 3 * kVBytes + 4 * kDmaMetaSlot;
 constexpr int kPPCnt = kKBytes;
 constexpr int kPPTs = kKBytes + kTileN * 4;
 constexpr float kLazyLog2 = 8.0f;
@@ -797,6 +869,866 @@ void attn_pp_kernel(AttnArgs a) {
   }
 }
 
+template <int VARIANT>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void attn_dma_kernel(AttnArgs a) {
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  char* const kst0 = smem;
+  char* const vst0 = smem + 3 * kKBytes;
+  char* const meta0 = smem + 3 * kKBytes + 3 * kVBytes;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wid = tid >> 6;  // uniform per wave; kept as a VGPR value (lower register pressure)
+  const int grp = wid >> 2, hw = wid & 3;
+  const int hl = lane >> 5, ql = lane & 31;
+
+  // ---- workgroup -> (unit, row group): XCD-aware, longest rows first ----
+  const int wg = blockIdx.x;
+  int unit, rg;
+  if ((a.units & 7) == 0) {
+    const int xcd = wg & 7, idx = wg >> 3, upx = a.units >> 3;
+    unit = xcd * upx + idx % upx;
+    rg = a.n_row_groups - 1 - idx / upx;
+  } else {
+    unit = wg % a.units;
+    rg = a.n_row_groups - 1 - wg / a.units;
+  }
+  const int hunits = a.G >> 2;
+  const int bg = unit / hunits;
+  const int hu = unit - bg * hunits;
+  const int b = bg / a.Hkv, g = bg - (bg / a.Hkv) * a.Hkv;
+  const int h = g * a.G + hu * 4 + hw;
+  const int R0 = rg * 64;
+  const int r0w = R0 + grp * 32;
+  const int wg_end = R0 + 64;
+  const int start_m = (R0 / kBlock) * kBlock;
+  const int row = r0w + ql;
+
+  // ---- schedule (identical to attn_kernel) ----
+  int P = a.P_host;
+  if (a.P_dev) P = min(*a.P_dev, a.P_host);
+  int n1 = 0, ds = 0;
+  int kend = a.causal ? min(a.Nk, wg_end) : a.Nk;
+  if (VARIANT == kHybrid || VARIANT == kSanity) {
+    const int nblk = (P + kBlock - 1) / kBlock;
+    const int32_t* bmax = a.sched + (int64_t)bg * 2 * a.nblk_cap;
+    const int32_t* pmax = bmax + a.nblk_cap;
+    const int thr = start_m - a.window;
+    int lo = 0, hi = nblk;
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      if (pmax[mid] < thr) lo = mid + 1; else hi = mid;
+    }
+    const int last = lo > 0 ? bmax[lo - 1] : -1;
+    ds = max(0, ((last + 1) / kBlock) * kBlock);
+    if (VARIANT == kHybrid) n1 = lo * (kBlock / kTileN);
+    kend = min(a.Nk, wg_end);
+  } else if (VARIANT == kPure) {
+    n1 = (P + kTileN - 1) / kTileN;
+    kend = 0;
+  }
+  const int n2 = kend > ds ? (kend - ds + kTileN - 1) / kTileN : 0;
+  const int T = n1 + n2;
+
+  const uint16_t* kp_base = a.kp + (int64_t)b * a.skp_b + (int64_t)g * a.skp_h;
+  const uint16_t* vp_base = a.vp + (int64_t)b * a.svp_b + (int64_t)g * a.svp_h;
+  const uint16_t* k_base = a.k + (int64_t)b * a.sk_b + (int64_t)g * a.sk_h;
+  const uint16_t* v_base = a.v + (int64_t)b * a.sv_b + (int64_t)g * a.sv_h;
+  const int32_t* ts_row = a.ts ? a.ts + (int64_t)b * a.sts_b + (int64_t)g * a.sts_h : nullptr;
+  const char* cnt_row = a.cnt ? (const char*)a.cnt + ((int64_t)b * a.scnt_b + (int64_t)g * a.scnt_h) * 4 : nullptr;
+  constexpr bool kPureV = VARIANT == kPure;
+  constexpr bool kWeights = VARIANT == kHybrid || VARIANT == kPure;
+
+  auto key0_of = [&](int t) { return t < n1 ? t * kTileN : ds + (t - n1) * kTileN; };
+  auto skipped = [&](int t) { return t >= n1 && a.causal && key0_of(t) > r0w + 31; };
+
+  // ---- staging: loads straight into LDS (buffer_load ... lds), three stages each
+  // for K and V and a ring of four slots for the tiles' weights.  Wave w loads the
+  // 4-row chunks 2w and 2w + 1 of both tiles: lane l writes 16 bytes at chunk base +
+  // 16 l, i.e. row 4c + l / 16 at position l % 16, so it fetches the source chunk that
+  // the swizzled layout keeps there.  The buffer resource covers exactly the tile's
+  // valid keys: rows past the end arrive as zeros.  Each wave issues the same loads in
+  // every window, so the s_waitcnt vmcnt(n) at the end of a window, n = the loads of
+  // this window, waits exactly for those of the window before. ----
+  const int wid_s = __builtin_amdgcn_readfirstlane(wid);
+  const char* kb1 = (const char*)uniform_ptr(kp_base);
+  const char* kb2 = (const char*)uniform_ptr(k_base);
+  const char* vb1 = (const char*)uniform_ptr(vp_base);
+  const char* vb2 = (const char*)uniform_ptr(v_base);
+  const int skpb = __builtin_amdgcn_readfirstlane((int)(2 * a.skp_n));
+  const int skb = __builtin_amdgcn_readfirstlane((int)(2 * a.sk_n));
+  const int svpb = __builtin_amdgcn_readfirstlane((int)(2 * a.svp_n));
+  const int svb = __builtin_amdgcn_readfirstlane((int)(2 * a.sv_n));
+  auto dma_rows = [&](bool isK, int t_raw) {
+    const int t = min(t_raw, T - 1);
+    const bool ph1 = t < n1;
+    const int key0 = key0_of(t);
+    const int limit = ph1 ? P : a.Nk;
+    const int snb = isK ? (ph1 ? skpb : skb) : (ph1 ? svpb : svb);
+    const char* src = isK ? (ph1 ? kb1 : kb2) : (ph1 ? vb1 : vb2);
+    const void* base = uniform_ptr(src + (int64_t)key0 * snb);
+    const int nrows = max(0, min(limit - key0, kTileN));
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<void*>(base), (short)0, __builtin_amdgcn_readfirstlane(nrows * snb), kBufferDword3);
+    char* dst = isK ? kst0 + (t_raw % 3) * kKBytes : vst0 + (t_raw % 3) * kVBytes;
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      const int rc = 2 * wid_s + j;
+      const int rowt = rc * 4 + (lane >> 4);
+      const int pos = lane & 15;
+      const int chunk = pos ^ (isK ? (rowt & 15) : 4 * (rowt & 3));
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)(dst + rc * 1024), 16,
+                                               rowt * snb + chunk * 16, 0, 0, 0);
+    }
+  };
+  // raw weights (and timestamps) of the tile's 64 keys, into slot t % 4 of their ring
+  auto meta_of = [&](int t) { return meta0 + (t & 3) * kDmaMetaSlot; };
+  auto dma_meta = [&](int t_raw) {
+    if (!kWeights) return;
+    const int t = min(t_raw, T - 1);
+    const int key0 = key0_of(t);
+    const int nrows = t < n1 ? max(0, min(P - key0, kTileN)) : 0;
+    char* dst = meta_of(t_raw) - kPPCnt;
+    const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<void*>(uniform_ptr(cnt_row + (int64_t)key0 * 4)), (short)0,
+        __builtin_amdgcn_readfirstlane(nrows * 4), kBufferDword3);
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rc, (__attribute__((address_space(3))) void*)(dst + kPPCnt), 4,
+                                             lane * 4, 0, 0, 0);
+    if (kPureV) {
+      const __amdgpu_buffer_rsrc_t rt = __builtin_amdgcn_make_buffer_rsrc(
+          const_cast<void*>(uniform_ptr(ts_row + key0)), (short)0, __builtin_amdgcn_readfirstlane(nrows * 4),
+          kBufferDword3);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rt, (__attribute__((address_space(3))) void*)(dst + kPPTs), 4,
+                                               lane * 4, 0, 0, 0);
+    }
+  };
+  auto dma_issue = [&](int tk, int tv) {
+    dma_rows(true, tk);
+    dma_rows(false, tv);
+    if (wid_s == 0) dma_meta(tk);
+  };
+  // weights and timestamps of tile t in place: zero weight (and INT_MAX timestamp)
+  // for keys that are not packed keys of this tile, the count as fp32 otherwise
+  auto convert_meta = [&](int t) {
+    if (!kWeights) return;
+    char* ks = meta_of(t) - kPPCnt;
+    const int key = key0_of(t) + lane;
+    const bool valid = t < n1 && key < P;
+    const int raw = ((const int*)(ks + kPPCnt))[lane];
+    const float cv0 = a.cnt_is_float ? __int_as_float(raw) : (float)raw;
+    const float cv = valid ? (a.no_count ? 1.0f : cv0) : 0.0f;
+    ((float*)(ks + kPPCnt))[lane] = cv;
+    if (kPureV) {
+      const int tsv = ((const int*)(ks + kPPTs))[lane];
+      ((int*)(ks + kPPTs))[lane] = cv > 0.0f ? tsv : INT_MAX;
+    }
+  };
+
+  // ---- per-lane LDS offsets (stage-relative) ----
+  int k_off[kD / 16];
+#pragma unroll
+  for (int tt = 0; tt < kD / 16; ++tt) k_off[tt] = k_lds_off(ql, 2 * tt + hl);  // + 8192 * kb2
+  // V stays row-major (16-byte chunk c of key row r at position c ^ 4 (r & 3)); the
+  // A operand V^T of a P.V MFMA comes from two ds_read_b64_tr_b16: in each group of 16
+  // lanes, lane 4e + q points at keys row + e, head dims 4q .. 4q + 3, and lane i
+  // receives head dim i of the 4 rows.  v_off[db] covers keys 16u + 4 (lane / 32) + 0..3
+  // (+ 4096 u; + 2048 for keys 8 further) and head dims 32 db + 16 ((lane / 16) & 1) + ..
+  int v_off[4];
+  {
+    const int gq = lane >> 4, sq = lane & 15, q = sq >> 2;
+    const int base = (4 * (gq >> 1) + q) * 256 + ((2 * (gq & 1) + ((sq & 3) >> 1)) << 4) + 8 * (sq & 1);
+#pragma unroll
+    for (int db = 0; db < 4; ++db) v_off[db] = base + 64 * (db ^ q);
+  }
+
+  // ---- Q^T in registers ----
+  bf16x8 qreg[kD / 16];
+  {
+    const uint16_t* qrow = a.q + (int64_t)b * a.sq_b + (int64_t)h * a.sq_h + (int64_t)row * a.sq_n;
+#pragma unroll
+    for (int t = 0; t < kD / 16; ++t) {
+      u32x4 w = (row < a.Nq) ? *(const u32x4*)(qrow + 16 * t + 8 * hl) : u32x4{0, 0, 0, 0};
+      qreg[t] = __builtin_bit_cast(bf16x8, w);
+    }
+    // Redefine Q^T here so the loop does not see it as an outstanding load: otherwise
+    // every S = K Q^T block waits for all memory loads, including the staging loads
+    // meant to land two sections later.
+#pragma unroll
+    for (int t = 0; t < kD / 16; ++t) asm volatile("" : "+v"(qreg[t]));
+  }
+
+  f32x16 o[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) o[i] = f32x16{};
+  f32x16 s[2];
+  u32x4 pw[4];
+  float m_used = -INFINITY, l_i = 0.0f;
+  const float c = a.scale_log2;
+  const float lazy_thr = kLazyLog2 / c;
+
+  // Sections 2k and 2k + 1 form window k; the workgroup synchronises only at the end
+  // of a window (within one, each group works on its own registers and on stages that
+  // no load touches).  Window k issues the loads of K(k+2) (with its weights) and of
+  // V(k+1) at its start and waits at its end for those of window k - 1.  K(t) is read
+  // in window t, V(t) in window t + 1 and the weights of tile t in windows t and t + 1;
+  // the loads that overwrite stage t % 3 (ring slot t % 4) come in window t + 1 (t + 2,
+  // t + 2), after the barrier.  Wave 0 loads the weights and converts them in place at
+  // the end of the window after its own wait.
+  if (T > 0) {
+    dma_rows(true, 0);
+    if (wid_s == 0) dma_meta(0);
+    dma_issue(1, 0);
+    __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
+    if (wid_s == 0) {
+      convert_meta(0);
+      convert_meta(1);
+    }
+    lds_barrier();
+  }
+
+  const int nsec = T > 0 ? 2 * T + 2 : 0;
+  for (int sec = 0; sec < nsec; ++sec) {
+    const int tl = sec >> 1;
+    const int sw = sec - grp;
+    // window tl loads K(tl + 2) and V(tl + 1) in its first section, in the middle of
+    // the section's work so that the loads of the eight waves do not queue up together
+    bool issued = (sec & 1) != 0;
+    auto issue_once = [&]() {
+      if (!issued) {
+        dma_issue(tl + 2, tl + 1);
+        issued = true;
+      }
+    };
+    if (sw >= 0) {
+      const int t = sw >> 1;
+      if ((sw & 1) == 0) {
+        // ---- matrix section: O^T += V^T P^T for tile t-1, then S^T = K Q^T for tile t ----
+        // Raised issue priority: the matrix pipe is the bottleneck, the softmax wave on
+        // the same SIMD takes the remaining issue slots.
+        __builtin_amdgcn_s_setprio(1);
+        if (t >= 1 && !skipped(t - 1)) {
+          // The V^T operands come from transpose reads issued by hand (the compiler
+          // would make each wait for every load to LDS in flight), four MFMAs ahead,
+          // with the matching lgkmcnt waits: LDS reads complete in order.
+          const uint32_t vb = lds_addr(vst0) + ((t - 1) % 3) * kVBytes;
+          uint32_t va[4];
+#pragma unroll
+          for (int db = 0; db < 4; ++db) va[db] = vb + v_off[db];
+          i16x4 vlo[16], vhi[16];
+          static_for<4>([&](auto I) {
+            constexpr int j = decltype(I)::value;
+            vlo[j] = ds_read_tr16<(j >> 2) * 4096>(va[j & 3]);
+            vhi[j] = ds_read_tr16<(j >> 2) * 4096 + 2048>(va[j & 3]);
+          });
+          static_for<16>([&](auto I) {
+            constexpr int i = decltype(I)::value;
+            constexpr int after = 2 * ((i + 3 < 15 ? i + 3 : 15) - i);  // reads issued after those of MFMA i
+            lgkm_wait<after>(vlo[i], vhi[i]);
+            const i16x8 vw = __builtin_shufflevector(vlo[i], vhi[i], 0, 1, 2, 3, 4, 5, 6, 7);
+            o[i & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, vw),
+                                                                __builtin_bit_cast(bf16x8, pw[i >> 2]),
+                                                                o[i & 3], 0, 0, 0);
+            if constexpr (i + 4 < 16) {
+              constexpr int j = i + 4;
+              vlo[j] = ds_read_tr16<(j >> 2) * 4096>(va[j & 3]);
+              vhi[j] = ds_read_tr16<(j >> 2) * 4096 + 2048>(va[j & 3]);
+            }
+          });
+        }
+        issue_once();
+        if (t < T && !skipped(t)) {
+          const char* kst = kst0 + (t % 3) * kKBytes;
+#pragma unroll
+          for (int kb2 = 0; kb2 < 2; ++kb2) {
+            s[kb2] = f32x16{};
+#pragma unroll
+            for (int tt = 0; tt < kD / 16; ++tt) {
+              const u32x4 w = *(const u32x4*)(kst + k_off[tt] + kb2 * 8192);
+              s[kb2] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, w),
+                                                                qreg[tt], s[kb2], 0, 0, 0);
+            }
+          }
+          pipe_mfma_reads();
+        }
+        __builtin_amdgcn_s_setprio(0);
+      } else if (t < T && !skipped(t)) {
+        // ---- softmax section for tile t ----
+        const char* kst = meta_of(t) - kPPCnt;  // weights / timestamps at kPPCnt / kPPTs
+        const int key0 = key0_of(t);
+        if (kPureV) {
+          mask_pure(s, (const int*)(kst + kPPTs), row, hl);
+        } else if (t >= n1) {
+          if ((a.causal && key0 + kTileN - 1 > r0w) || key0 + kTileN > a.Nk)
+            mask_dense(s, key0, row, hl, a.Nk, a.causal);
+        }
+        float mx = -INFINITY;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) mx = __builtin_fmaxf(mx, __builtin_fmaxf(s[0][r], s[1][r]));
+        mx = halves_max(mx);
+        const bool upd = mx > m_used + lazy_thr;  // no NaN when m_used = -inf
+        issue_once();
+        if (__ballot(upd)) {
+          const float m_new = upd ? mx : m_used;
+          const float alpha = exp2_fast((m_used - m_new) * c);
+#pragma unroll
+          for (int db = 0; db < 4; ++db)
+#pragma unroll
+            for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
+          l_i *= alpha;
+          m_used = m_new;
+        }
+        const float neg = (m_used == -INFINITY) ? 0.0f : -m_used * c;
+        const bool weighted = kWeights && t < n1;
+        const float* cl = (const float*)(kst + kPPCnt);
+        float psum = 0.0f;
+#pragma unroll
+        for (int kb2 = 0; kb2 < 2; ++kb2) {
+#pragma unroll
+          for (int r4 = 0; r4 < 4; ++r4) {
+            float p[4];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) p[e] = exp2_fast(__builtin_fmaf(s[kb2][4 * r4 + e], c, neg));
+            if (weighted) {
+              const f32x4 w4 = *(const f32x4*)(cl + kb2 * 32 + 8 * r4 + 4 * hl);
+#pragma unroll
+              for (int e = 0; e < 4; ++e) p[e] *= w4[e];
+            }
+            psum += (p[0] + p[1]) + (p[2] + p[3]);
+            pw[2 * kb2 + (r4 >> 1)][(r4 & 1) * 2 + 0] = pack_bf16x2(p[0], p[1]);
+            pw[2 * kb2 + (r4 >> 1)][(r4 & 1) * 2 + 1] = pack_bf16x2(p[2], p[3]);
+          }
+        }
+        l_i += psum;
+      }
+    }
+    issue_once();
+    if (sec & 1) {
+      // the loads of window tl - 1 are done when at most this window's are pending
+      if (wid_s == 0) {
+        __builtin_amdgcn_s_waitcnt(vmcnt_only(4 + (kWeights ? 1 : 0) + (kPureV ? 1 : 0)));
+        if (tl >= 1) convert_meta(tl + 1);  // weights of tile tl + 1 (tiles 0, 1: prologue)
+      } else {
+        __builtin_amdgcn_s_waitcnt(vmcnt_only(4));
+      }
+      barrier_keep_loads();
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(vmcnt_only(0));  // no load may land in LDS after the exit
+
+  // ---- finalize ----
+  const float l_tot = halves_sum(l_i);
+  float inv;
+  if (VARIANT == kPure)
+    inv = l_tot > 0.0f ? 1.0f / l_tot : 1.0f;  // deltaFlashAttention.py:353-354
+  else
+    inv = 1.0f / l_tot;
+  if (row < a.Nq) {
+    uint16_t* orow = a.out + (int64_t)b * a.so_b + (int64_t)h * a.so_h + (int64_t)row * a.so_n;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        u32x2 w;
+        w[0] = pack_bf16x2(o[db][4 * j + 0] * inv, o[db][4 * j + 1] * inv);
+        w[1] = pack_bf16x2(o[db][4 * j + 2] * inv, o[db][4 * j + 3] * inv);
+        *(u32x2*)(orow + db * 32 + 8 * j + 4 * hl) = w;
+      }
+  }
+}
+
+// ---------------------------------------------------------------------------------
+// Intra-wave pipelined kernel for GQA groups that are a multiple of 4.  A workgroup is
+// four waves, one per SIMD with up to 512 registers each; wave w computes query head
+// 4 * hu + w for the 32 rows R0 .. R0 + 31, and the four waves share the staged K and
+// V^T tiles.  Step t (one 64-key tile) has two phases of 16 slots; a slot is one MFMA
+// plus a fixed slice of VALU / LDS / memory work that does not depend on it, so one
+// wave keeps its matrix pipe and its VALU busy together (sched_barrier between slots):
+//   phase 1: S(t+1) = K(t+1) Q^T    (16 MFMA) || P of keys 0-31 of tile t, staging
+//   phase 2: O += V(t-1)^T P(t-1)^T (16 MFMA) || P of keys 32-63 of tile t, running
+//            max of S(t+1)
+// The running max runs one tile ahead of the exponentials and P.V one tile behind
+// them.  The factor the max of tile t asks of O is applied in step t + 1 between the
+// phases, after P.V of tile t - 1 and before that of tile t.
+// Staging: at the start of step t every thread writes its registers of K(t+2) and V(t)
+// to LDS and issues the loads of K(t+3) and V(t+1) into the same registers, so each
+// load has about one step to land; one barrier per step.
+// ---------------------------------------------------------------------------------
+
+// LDS: K stages (2 x 16 KiB), V^T stages (2 x 16 KiB), then a ring of 3 slots of
+// per-key weights (float[64]) and timestamps (int[64]): the slot of tile t is written
+// with K(t) in step t - 2 and read by the softmax of tile t in step t.
+constexpr int kIWV = 2 * kKBytes;
+constexpr int kIWMeta = 2 * kKBytes + 2 * kVBytes;
+constexpr int kIWMetaSlot = kTileN * 8;
+constexpr int kIWLds = kIWMeta + 3 * kIWMetaSlot;
+
+
+// Instruction order for one phase of attn_iw_kernel (16 MFMAs fed by 16 LDS operand
+// reads, plus VALU work that does not depend on them): the operand reads run four
+// ahead and NV VALU instructions follow every MFMA, so the VALU issues while the
+// matrix pipe works.  With STAGING the phase also carries 12 LDS writes and 8 buffer
+// loads, spread over the second half.
+template <int NV, bool STAGING>
+__device__ __forceinline__ void sched_phase() {
+  __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);  // DS read x4
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+    __builtin_amdgcn_sched_group_barrier(0x002, NV, 0);  // VALU
+    if (i < 12) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+    if (STAGING && i >= 4) {
+      __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // DS write
+      if (i & 1) __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);  // VMEM read
+    }
+  }
+}
+
+template <int VARIANT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
+void attn_iw_kernel(AttnArgs a) {
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  char* const kst0 = smem;
+  char* const vst0 = smem + kIWV;
+  char* const meta0 = smem + kIWMeta;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int hw = tid >> 6;
+  const int hl = lane >> 5, ql = lane & 31;
+  constexpr bool kPureV = VARIANT == kPure;
+  constexpr bool kWeights = VARIANT == kHybrid || VARIANT == kPure;
+
+  // ---- workgroup -> (unit, row group): XCD-aware, longest rows first ----
+  const int wg = blockIdx.x;
+  int unit, rg;
+  if ((a.units & 7) == 0) {
+    const int xcd = wg & 7, idx = wg >> 3, upx = a.units >> 3;
+    unit = xcd * upx + idx % upx;
+    rg = a.n_row_groups - 1 - idx / upx;
+  } else {
+    unit = wg % a.units;
+    rg = a.n_row_groups - 1 - wg / a.units;
+  }
+  const int hunits = a.G >> 2;
+  const int bg = unit / hunits;
+  const int hu = unit - bg * hunits;
+  const int b = bg / a.Hkv, g = bg - (bg / a.Hkv) * a.Hkv;
+  const int h = g * a.G + hu * 4 + hw;
+  const int R0 = rg * 32;
+  const int wg_end = R0 + 32;
+  const int start_m = (R0 / kBlock) * kBlock;
+  const int row = R0 + ql;
+
+  // ---- schedule (deltaFlashAttention.py:56-100, as in attn_kernel) ----
+  int P = a.P_host;
+  if (a.P_dev) P = min(*a.P_dev, a.P_host);
+  int n1 = 0, ds = 0;
+  int kend = a.causal ? min(a.Nk, wg_end) : a.Nk;
+  if (VARIANT == kHybrid || VARIANT == kSanity) {
+    const int nblk = (P + kBlock - 1) / kBlock;
+    const int32_t* bmax = a.sched + (int64_t)bg * 2 * a.nblk_cap;
+    const int32_t* pmax = bmax + a.nblk_cap;
+    const int thr = start_m - a.window;
+    int lo = 0, hi = nblk;
+    while (lo < hi) {
+      const int mid = (lo + hi) >> 1;
+      if (pmax[mid] < thr) lo = mid + 1; else hi = mid;
+    }
+    const int last = lo > 0 ? bmax[lo - 1] : -1;
+    ds = max(0, ((last + 1) / kBlock) * kBlock);
+    if (VARIANT == kHybrid) n1 = lo * (kBlock / kTileN);
+    kend = min(a.Nk, wg_end);
+  } else if (VARIANT == kPure) {
+    n1 = (P + kTileN - 1) / kTileN;
+    kend = 0;
+  }
+  n1 = __builtin_amdgcn_readfirstlane(n1);
+  ds = __builtin_amdgcn_readfirstlane(ds);
+  P = __builtin_amdgcn_readfirstlane(P);
+  const int n2 = kend > ds ? (kend - ds + kTileN - 1) / kTileN : 0;
+  const int T = __builtin_amdgcn_readfirstlane(n1 + n2);
+
+  const uint16_t* kp_base = a.kp + (int64_t)b * a.skp_b + (int64_t)g * a.skp_h;
+  const uint16_t* vp_base = a.vp + (int64_t)b * a.svp_b + (int64_t)g * a.svp_h;
+  const uint16_t* k_base = a.k + (int64_t)b * a.sk_b + (int64_t)g * a.sk_h;
+  const uint16_t* v_base = a.v + (int64_t)b * a.sv_b + (int64_t)g * a.sv_h;
+  const int32_t* ts_row = a.ts ? a.ts + (int64_t)b * a.sts_b + (int64_t)g * a.sts_h : nullptr;
+  const char* cnt_row = a.cnt ? (const char*)a.cnt + ((int64_t)b * a.scnt_b + (int64_t)g * a.scnt_h) * 4 : nullptr;
+
+  auto key0_of = [&](int t) { return t < n1 ? t * kTileN : ds + (t - n1) * kTileN; };
+  // tiles whose dense keys need the causal / length mask (every tile for pure Phase 1)
+  auto needs_mask = [&](int t) {
+    if (kPureV) return true;
+    if (t < n1) return false;
+    const int key0 = key0_of(t);
+    return (a.causal && key0 + kTileN - 1 > R0) || key0 + kTileN > a.Nk;
+  };
+
+  // ---- staging: every thread stages 4 rows of K (16-byte chunk s_kc of keys
+  // 4 s_kg .. 4 s_kg + 3) and 4 rows of V (chunk s_vc of keys 4 s_vg ..), the latter
+  // transposed into V^T.  Buffer loads whose resource covers exactly the tile's valid
+  // keys read rows past the end as zero. ----
+  const int s_kc = tid & 15, s_kg = tid >> 4;
+  const int s_vc = tid >> 4, s_vg = tid & 15;
+  const char* kb1 = (const char*)uniform_ptr(kp_base);
+  const char* kb2 = (const char*)uniform_ptr(k_base);
+  const char* vb1 = (const char*)uniform_ptr(vp_base);
+  const char* vb2 = (const char*)uniform_ptr(v_base);
+  const int skp = (int)(2 * a.skp_n), sk = (int)(2 * a.sk_n);
+  const int svp = (int)(2 * a.svp_n), sv = (int)(2 * a.sv_n);
+  struct SRegs {
+    u32x4 k[4];
+    u32x4 v[4];
+    int ts;
+    int craw;
+    int cstate;  // 0: past the packed keys (weight 0), 1: packed key, 2: dense key (weight 1)
+  };
+  auto load_rows = [&](u32x4* x, const char* b1, const char* b2, int sb1, int sb2, int t, int grp4, int chunk) {
+    const bool ph1 = t < n1;
+    const int key0 = key0_of(t);
+    const int limit = ph1 ? P : a.Nk;
+    const int snb = ph1 ? sb1 : sb2;
+    const void* base = uniform_ptr((ph1 ? b1 : b2) + (int64_t)key0 * snb);
+    const int nrows = max(0, min(limit - key0, kTileN));
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<void*>(base), (short)0, __builtin_amdgcn_readfirstlane(nrows * snb), kBufferDword3);
+    const int voff = grp4 * 4 * snb + chunk * 16;
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      x[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, voff + j * snb, 0, 0));
+  };
+  auto stage_load_k = [&](SRegs& R, int tk) {
+    tk = min(tk, T - 1);
+    load_rows(R.k, kb1, kb2, skp, sk, tk, s_kg, s_kc);
+    if (kWeights) {
+      const int key = key0_of(tk) + (tid & 63);
+      const int kc = max(min(key, P - 1), 0);  // P >= 1 (checked on the host)
+      R.cstate = tk < n1 ? (key < P ? 1 : 0) : 2;
+      R.craw = ((const int32_t*)cnt_row)[kc];
+      if (kPureV) R.ts = ts_row[kc];
+    }
+  };
+  auto stage_load_v = [&](SRegs& R, int tv) {
+    load_rows(R.v, vb1, vb2, svp, sv, min(tv, T - 1), s_vg, s_vc);
+  };
+  auto meta_of = [&](int t) { return meta0 + (t % 3) * kIWMetaSlot; };
+  // K row j of this thread (and, with row 0, the key's weight and timestamp)
+  auto store_k_row = [&](const SRegs& R, int tk, int j) {
+    char* ks = kst0 + (tk & 1) * kKBytes;
+    *(u32x4*)(ks + k_lds_off(s_kg * 4 + j, s_kc)) = R.k[j];
+    if (kWeights && j == 0) {
+      // four threads write each key's entry, all with the same value (no branch)
+      const float cv0 = a.cnt_is_float ? __int_as_float(R.craw) : (float)R.craw;
+      const float cv = R.cstate == 2 ? 1.0f : R.cstate == 1 ? (a.no_count ? 1.0f : cv0) : 0.0f;
+      char* ms = meta_of(tk);
+      ((float*)ms)[tid & 63] = cv;
+      if (kPureV) ((int*)(ms + kTileN * 4))[tid & 63] = cv > 0.0f ? R.ts : INT_MAX;
+    }
+  };
+  auto store_k = [&](const SRegs& R, int tk) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) store_k_row(R, tk, j);
+  };
+  // head dimensions s_vc * 8 + 2w, + 1 of the 4 staged V rows, as V^T
+  auto store_v_part = [&](const SRegs& R, int tv, int w) {
+    char* vs = vst0 + (tv & 1) * kVBytes - kKBytes;  // vt_lds_* offsets include kKBytes
+    const uint32_t x0 = R.v[0][w], x1 = R.v[1][w], x2 = R.v[2][w], x3 = R.v[3][w];
+    const int d0 = s_vc * 8 + 2 * w;
+    u32x2 lo, hi;
+    lo[0] = __builtin_amdgcn_perm(x1, x0, 0x05040100u);
+    lo[1] = __builtin_amdgcn_perm(x3, x2, 0x05040100u);
+    hi[0] = __builtin_amdgcn_perm(x1, x0, 0x07060302u);
+    hi[1] = __builtin_amdgcn_perm(x3, x2, 0x07060302u);
+    *(u32x2*)(vs + vt_lds_group(d0, s_vg)) = lo;
+    *(u32x2*)(vs + vt_lds_group(d0 + 1, s_vg)) = hi;
+  };
+  auto store_v = [&](const SRegs& R, int tv) {
+#pragma unroll
+    for (int w = 0; w < 4; ++w) store_v_part(R, tv, w);
+  };
+
+  // ---- per-lane LDS offsets (stage-relative) ----
+  int k_off[kD / 16];
+#pragma unroll
+  for (int tt = 0; tt < kD / 16; ++tt) k_off[tt] = k_lds_off(ql, 2 * tt + hl);  // + 8192 * kb
+  int v_off[4];
+#pragma unroll
+  for (int u = 0; u < 4; ++u) v_off[u] = vt_lds_chunk(ql, 2 * u + hl) - kKBytes;  // + 4096 * db
+
+  // ---- Q^T in registers ----
+  bf16x8 qreg[kD / 16];
+  {
+    const uint16_t* qrow = a.q + (int64_t)b * a.sq_b + (int64_t)h * a.sq_h + (int64_t)row * a.sq_n;
+#pragma unroll
+    for (int t = 0; t < kD / 16; ++t) {
+      const u32x4 w = row < a.Nq ? *(const u32x4*)(qrow + 16 * t + 8 * hl) : u32x4{0, 0, 0, 0};
+      qreg[t] = __builtin_bit_cast(bf16x8, w);
+    }
+    // Q^T lives in AGPRs (the MFMA reads its B operand from there; the VGPRs are
+    // needed by the softmax), and the redefinition also keeps the loop from counting
+    // Q as an outstanding load.
+#pragma unroll
+    for (int t = 0; t < kD / 16; ++t) asm volatile("" : "+a"(qreg[t]));
+  }
+
+  f32x16 o[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) o[i] = f32x16{};
+  float m = -INFINITY, l = 0.0f;
+  float neg = 0.0f;  // -m * c
+  const float c = a.scale_log2;
+  const float lazy_thr = kLazyLog2 / c;
+
+  // ---- building blocks ----
+  auto qk = [&](int t, f32x16 (&s)[2]) {
+    const char* kst = kst0 + (t & 1) * kKBytes;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+#pragma unroll
+      for (int tt = 0; tt < kD / 16; ++tt) {
+        const bf16x8 w = __builtin_bit_cast(bf16x8, *(const u32x4*)(kst + k_off[tt] + kb * 8192));
+        s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(w, qreg[tt], tt == 0 ? f32x16{} : s[kb], 0, 0, 0);
+      }
+    }
+  };
+  auto pv = [&](int t, const u32x4 (&pw)[4]) {
+    const char* vst = vst0 + (t & 1) * kVBytes;
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+#pragma unroll
+      for (int db = 0; db < 4; ++db) {
+        const bf16x8 w = __builtin_bit_cast(bf16x8, *(const u32x4*)(vst + v_off[u] + db * 4096));
+        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(w, __builtin_bit_cast(bf16x8, pw[u]), o[db], 0, 0, 0);
+      }
+    }
+  };
+  auto mask = [&](int t, f32x16 (&s)[2]) {
+    if (kPureV)
+      mask_pure(s, (const int*)(meta_of(t) + kTileN * 4), row, hl);
+    else
+      mask_dense(s, key0_of(t), row, hl, a.Nk, a.causal);
+  };
+  // Max of S values 4g .. 4g + 3 of both key halves.
+  auto max_part = [&](const f32x16 (&s)[2], int g) {
+    return __builtin_fmaxf(
+        __builtin_fmaxf(__builtin_fmaxf(s[0][4 * g], s[0][4 * g + 1]), __builtin_fmaxf(s[0][4 * g + 2], s[0][4 * g + 3])),
+        __builtin_fmaxf(__builtin_fmaxf(s[1][4 * g], s[1][4 * g + 1]), __builtin_fmaxf(s[1][4 * g + 2], s[1][4 * g + 3])));
+  };
+  // Running max of the next tile with lazy rescale (the max moves only when it grows
+  // by more than 2^kLazyLog2); returns the factor for l and O.
+  auto update_max = [&](float mx) {
+    const bool upd = mx > m + lazy_thr;  // no NaN when m = -inf
+    const float m_new = upd ? mx : m;
+    const float al = upd ? exp2_fast((m - m_new) * c) : 1.0f;
+    m = m_new;
+    neg = (m == -INFINITY) ? 0.0f : -m * c;
+    return al;
+  };
+  // P of S values 2j, 2j + 1 of key half kb (MFMA B layout), weighted, summed, in
+  // three stages: A (scale and shift), B (exp2), C (weight, sum, pack).  Slot i of a
+  // phase runs A of pair i, B of pair i - 1 and C of pair i - 2, so the instructions of
+  // one slot do not wait for each other and the MFMA after them issues on time.
+  struct Pipe {
+    float x[2][2];  // after A, by pair parity
+    float p[2][2];  // after B
+  };
+  auto exp_slot = [&](int t, const f32x16& s, u32x4* pw2, int kb, int i, Pipe& pp_, float& psum) {
+    if (i >= 2 && i - 2 < 8) {
+      const int j = i - 2, r4 = j >> 1, half = j & 1;
+      float p0 = pp_.p[j & 1][0], p1 = pp_.p[j & 1][1];
+      if (kWeights) {
+        const f32x2 w2 = *(const f32x2*)((const float*)meta_of(t) + kb * 32 + 8 * r4 + 4 * hl + 2 * half);
+        p0 *= w2[0];
+        p1 *= w2[1];
+      }
+      psum += p0 + p1;
+      uint32_t pk = pack_bf16x2(p0, p1);
+      asm volatile("" : "+v"(pk));  // computed in its slot, not sunk to the MFMA that reads it
+      pw2[r4 >> 1][(r4 & 1) * 2 + half] = pk;
+    }
+    if (i >= 1 && i - 1 < 8) {
+      const int j = i - 1;
+      pp_.p[j & 1][0] = exp2_fast(pp_.x[j & 1][0]);
+      pp_.p[j & 1][1] = exp2_fast(pp_.x[j & 1][1]);
+    }
+    if (i < 8) {
+      pp_.x[i & 1][0] = __builtin_fmaf(s[2 * i], c, neg);
+      pp_.x[i & 1][1] = __builtin_fmaf(s[2 * i + 1], c, neg);
+    }
+  };
+  auto rescale = [&](float f) {
+    if (__ballot(f != 1.0f)) {
+#pragma unroll
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int r = 0; r < 16; ++r) o[db][r] *= f;
+    }
+  };
+
+  SRegs r;
+  r.ts = 0;
+  r.craw = 0;
+  r.cstate = 0;
+  float q0 = 1.0f, q1 = 1.0f;  // factors for O before P.V of tiles t - 1 and t
+
+  // Phase 1 of step t: 16 slots, each one MFMA of S(t+1) = K(t+1) Q^T (if QK) plus
+  // a fixed slice of other work -- P of keys 0-31 of tile t and (if ST) the LDS writes
+  // of K(t+2) and V(t) followed by the loads of K(t+3) and V(t+1).  The K operands are
+  // read four slots ahead and sched_barrier keeps the slots in this order.
+  auto phase1 = [&](auto QK, auto ST, int t, const f32x16 (&sc)[2], f32x16 (&sn)[2], u32x4 (&pc)[4]) {
+    constexpr bool kQK = decltype(QK)::value, kST = decltype(ST)::value;
+    const char* kst = kst0 + ((t + 1) & 1) * kKBytes;
+    u32x4 fr[16];
+    if (kQK) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) fr[i] = *(const u32x4*)(kst + k_off[i >> 1] + (i & 1) * 8192);
+    }
+    float psum = 0.0f;
+    Pipe pipe;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      if (kQK) {
+        if (i + 4 < 16) fr[i + 4] = *(const u32x4*)(kst + k_off[(i + 4) >> 1] + ((i + 4) & 1) * 8192);
+        const int kb = i & 1, tt = i >> 1;
+        sn[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, fr[i]), qreg[tt],
+                                                          tt == 0 ? f32x16{} : sn[kb], 0, 0, 0);
+      }
+      if (i < 10) exp_slot(t, sc[0], pc, 0, i, pipe, psum);
+      if (kST) {
+        // LDS writes of the staged rows first, then the loads of the next ones, so
+        // each load has a whole step to land before its registers are written out
+        if (i < 4) {
+          store_k_row(r, t + 2, i);
+          store_v_part(r, t, i);
+        }
+        if (i == 4) stage_load_k(r, t + 3);
+        if (i == 5) stage_load_v(r, t + 1);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    l += psum;
+  };
+  // Phase 2 of step t: 16 slots, each one MFMA of O += V(t-1)^T P(t-1)^T (if PV) plus
+  // a slice of P of keys 32-63 of tile t, then (if NX) the running max of S(t+1).
+  auto phase2 = [&](auto PV, auto NX, int t, const f32x16 (&sc)[2], const u32x4 (&pp)[4], u32x4 (&pc)[4],
+                    const f32x16 (&sn)[2]) {
+    constexpr bool kPV = decltype(PV)::value, kNX = decltype(NX)::value;
+    const char* vst = vst0 + ((t - 1) & 1) * kVBytes;
+    u32x4 fr[16];
+    if (kPV) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) fr[i] = *(const u32x4*)(vst + v_off[i >> 2] + (i & 3) * 4096);
+    }
+    float psum = 0.0f;
+    float mp[4];
+    float mx = 0.0f;
+    Pipe pipe;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      if (kPV) {
+        if (i + 4 < 16) fr[i + 4] = *(const u32x4*)(vst + v_off[(i + 4) >> 2] + ((i + 4) & 3) * 4096);
+        const int u = i >> 2, db = i & 3;
+        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, fr[i]),
+                                                         __builtin_bit_cast(bf16x8, pp[u]), o[db], 0, 0, 0);
+      }
+      if (i < 10) exp_slot(t, sc[1], pc + 2, 1, i, pipe, psum);
+      if (kNX) {
+        if (i >= 6 && i < 10) mp[i - 6] = max_part(sn, i - 6);
+        if (i == 10) mx = halves_max(__builtin_fmaxf(__builtin_fmaxf(mp[0], mp[1]), __builtin_fmaxf(mp[2], mp[3])));
+        if (i == 11) {
+          l += psum;
+          psum = 0.0f;
+          q1 = update_max(mx);
+          l *= q1;
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    l += psum;
+  };
+
+  f32x16 sX[2], sY[2];
+  u32x4 pX[4], pY[4];
+  using Yes = std::integral_constant<bool, true>;
+  using No = std::integral_constant<bool, false>;
+
+  if (T > 0) {
+    // ---- prologue: K(0), K(1) in LDS; K(2), V(0) in the staging registers; S(0)
+    // and its running max ----
+    stage_load_k(r, 0);
+    store_k(r, 0);
+    stage_load_k(r, 1);
+    store_k(r, 1);
+    stage_load_k(r, 2);
+    stage_load_v(r, 0);
+    lds_barrier();
+    qk(0, sX);
+    lds_barrier();  // K(0) read by every wave before step 0 overwrites its stage
+    if (needs_mask(0)) mask(0, sX);
+    q1 = update_max(halves_max(__builtin_fmaxf(__builtin_fmaxf(max_part(sX, 0), max_part(sX, 1)),
+                                               __builtin_fmaxf(max_part(sX, 2), max_part(sX, 3)))));
+    l *= q1;
+
+    // ---- step t (tiles 0 .. T-2): S(t) in sc, S(t+1) to sn, P(t-1) in pp, P(t) to pc ----
+    auto step = [&](auto PV, int t, f32x16 (&sc)[2], f32x16 (&sn)[2], const u32x4 (&pp)[4], u32x4 (&pc)[4]) {
+      phase1(Yes{}, Yes{}, t, sc, sn, pc);
+      if (needs_mask(t + 1)) mask(t + 1, sn);
+      rescale(q0);  // O holds P.V up to tile t-2; P(t-1) is relative to the max of tile t-1
+      q0 = q1;
+      phase2(PV, Yes{}, t, sc, pp, pc, sn);
+      lds_barrier();
+    };
+    int t = 0;
+    if (T > 2) {
+      step(No{}, 0, sX, sY, pY, pX);
+      step(Yes{}, 1, sY, sX, pX, pY);
+      for (t = 2; t + 2 < T; t += 2) {
+        step(Yes{}, t, sX, sY, pY, pX);
+        step(Yes{}, t + 1, sY, sX, pX, pY);
+      }
+    }
+    // ---- the last tile t = T - 1: V(t) still sits in the staging registers ----
+    auto last = [&](auto PV, int t, const f32x16 (&sc)[2], const u32x4 (&pp)[4], u32x4 (&pc)[4]) {
+      store_v(r, t);
+      phase1(No{}, No{}, t, sc, sX, pc);
+      rescale(q0);
+      q0 = q1;
+      phase2(PV, No{}, t, sc, pp, pc, sc);
+      rescale(q0);
+      lds_barrier();  // V(t) from every thread
+      pv(t, pc);
+    };
+    if (t + 1 < T) {
+      if (t == 0)
+        step(No{}, t, sX, sY, pY, pX);
+      else
+        step(Yes{}, t, sX, sY, pY, pX);
+      last(Yes{}, t + 1, sY, pX, pY);
+    } else if (t == 0) {
+      last(No{}, t, sX, pY, pX);
+    } else {
+      last(Yes{}, t, sX, pY, pX);
+    }
+  }
+
+  // ---- finalize ----
+  const float l_tot = halves_sum(l);
+  float inv;
+  if (VARIANT == kPure)
+    inv = l_tot > 0.0f ? 1.0f / l_tot : 1.0f;  // deltaFlashAttention.py:353-354
+  else
+    inv = 1.0f / l_tot;
+  if (row < a.Nq) {
+    uint16_t* orow = a.out + (int64_t)b * a.so_b + (int64_t)h * a.so_h + (int64_t)row * a.so_n;
+#pragma unroll
+    for (int db = 0; db < 4; ++db)
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        u32x2 w;
+        w[0] = pack_bf16x2(o[db][4 * j + 0] * inv, o[db][4 * j + 1] * inv);
+        w[1] = pack_bf16x2(o[db][4 * j + 2] * inv, o[db][4 * j + 3] * inv);
+        *(u32x2*)(orow + db * 32 + 8 * j + 4 * hl) = w;
+      }
+  }
+}
+
 // Per (batch, kv head): maxima of packed blocks of 128 timestamps (lanes at or
 // beyond P read seq_len_k + 1, deltaFlashAttention.py:70) and their prefix maxima.
 __global__ __launch_bounds__(256) void hybrid_schedule_kernel(const int32_t* __restrict__ ts,
@@ -873,8 +1805,87 @@ static int allow_lds_pp(size_t bytes) {
   return DA_OK;
 }
 
+template <int V>
+static int allow_lds_iw(size_t bytes) {
+  static int done = 0;
+  if (!done) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_iw_kernel<V>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+    if (e != hipSuccess) return set_error(DA_ERR_HIP, "hipFuncSetAttribute: %s", hipGetErrorString(e));
+    done = 1;
+  }
+  return DA_OK;
+}
+
+static int launch_attn_iw(int variant, AttnArgs& a, hipStream_t st) {
+  a.rows_per_wg = 32;
+  a.n_row_groups = (a.Nq + 31) / 32;
+  const size_t lds = kIWLds;
+  const unsigned grid = (unsigned)((int64_t)a.n_row_groups * a.units);
+  int rc = DA_OK;
+  switch (variant) {
+    case kHybrid: rc = allow_lds_iw<kHybrid>(lds); break;
+    case kSanity: rc = allow_lds_iw<kSanity>(lds); break;
+    case kPure: rc = allow_lds_iw<kPure>(lds); break;
+    default: rc = allow_lds_iw<kDense>(lds); break;
+  }
+  if (rc) return rc;
+  switch (variant) {
+    case kHybrid: hipLaunchKernelGGL(attn_iw_kernel<kHybrid>, dim3(grid), dim3(256), lds, st, a); break;
+    case kSanity: hipLaunchKernelGGL(attn_iw_kernel<kSanity>, dim3(grid), dim3(256), lds, st, a); break;
+    case kPure: hipLaunchKernelGGL(attn_iw_kernel<kPure>, dim3(grid), dim3(256), lds, st, a); break;
+    default: hipLaunchKernelGGL(attn_iw_kernel<kDense>, dim3(grid), dim3(256), lds, st, a); break;
+  }
+  return check_launch("attention kernel (intra-wave)");
+}
+
+template <int V>
+static int allow_lds_dma(size_t bytes) {
+  static int done = 0;
+  if (!done) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_dma_kernel<V>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
+    if (e != hipSuccess) return set_error(DA_ERR_HIP, "hipFuncSetAttribute: %s", hipGetErrorString(e));
+    done = 1;
+  }
+  return DA_OK;
+}
+
+static int launch_attn_dma(int variant, AttnArgs& a, hipStream_t st) {
+  a.rows_per_wg = 64;
+  a.n_row_groups = (a.Nq + 63) / 64;
+  const size_t lds = kDmaLds;
+  const unsigned grid = (unsigned)((int64_t)a.n_row_groups * a.units);
+  int rc = DA_OK;
+  switch (variant) {
+    case kHybrid: rc = allow_lds_dma<kHybrid>(lds); break;
+    case kSanity: rc = allow_lds_dma<kSanity>(lds); break;
+    case kPure: rc = allow_lds_dma<kPure>(lds); break;
+    default: rc = allow_lds_dma<kDense>(lds); break;
+  }
+  if (rc) return rc;
+  switch (variant) {
+    case kHybrid: hipLaunchKernelGGL(attn_dma_kernel<kHybrid>, dim3(grid), dim3(512), lds, st, a); break;
+    case kSanity: hipLaunchKernelGGL(attn_dma_kernel<kSanity>, dim3(grid), dim3(512), lds, st, a); break;
+    case kPure: hipLaunchKernelGGL(attn_dma_kernel<kPure>, dim3(grid), dim3(512), lds, st, a); break;
+    default: hipLaunchKernelGGL(attn_dma_kernel<kDense>, dim3(grid), dim3(512), lds, st, a); break;
+  }
+  return check_launch("attention kernel (ping-pong, direct LDS loads)");
+}
+
+// Kernel choice for GQA groups that are a multiple of 4: DELTAATTN_ATTN_KERNEL=pp|iw|dma
+// (default dma).  Other groups run attn_kernel.
+static int attn_kernel_choice() {
+  static int v = -1;
+  if (v < 0) {
+    const char* e = getenv("DELTAATTN_ATTN_KERNEL");
+    v = (e && strcmp(e, "pp") == 0) ? 0 : (e && strcmp(e, "iw") == 0) ? 1 : 2;
+  }
+  return v;
+}
+
 // GQA groups that are a multiple of 4 run the ping-pong kernel (64 rows x 4 heads per
-// workgroup of 8 waves); other groups run attn_kernel.
+// workgroup of 8 waves) or the intra-wave kernel; other groups run attn_kernel.
 static int launch_attn_pp(int variant, AttnArgs& a, hipStream_t st) {
   a.rows_per_wg = 64;
   a.n_row_groups = (a.Nq + 63) / 64;
@@ -908,7 +1919,13 @@ static int launch_attn(int variant, AttnArgs& a, hipStream_t st) {
     default: rc = allow_lds<kDense>(lds); break;
   }
   if (rc) return rc;
-  if (a.hpw == 4) return launch_attn_pp(variant, a, st);
+  if (a.hpw == 4) {
+    switch (attn_kernel_choice()) {
+      case 0: return launch_attn_pp(variant, a, st);
+      case 1: return launch_attn_iw(variant, a, st);
+      default: return launch_attn_dma(variant, a, st);
+    }
+  }
   switch (variant) {
     case kHybrid:
       hipLaunchKernelGGL(attn_kernel<kHybrid>, dim3(grid), dim3(256), lds, st, a);
