@@ -303,14 +303,13 @@ void attn_kernel(AttnArgs a) {
     const bool skip = !ph1 && a.causal && key0 > r0w + 31;
     if (!skip) {
       // ---- S^T = K Q^T for two 32-key blocks ----
-      f32x16 s[2];
+      // the two key blocks alternate so that consecutive MFMAs do not depend on each other
+      f32x16 s[2] = {f32x16{}, f32x16{}};
 #pragma unroll
-      for (int kb2 = 0; kb2 < 2; ++kb2) {
-        s[kb2] = f32x16{};
-        const int krow = kb2 * 32 + ql;
+      for (int tt = 0; tt < kD / 16; ++tt) {
 #pragma unroll
-        for (int tt = 0; tt < kD / 16; ++tt) {
-          const u32x4 w = *(const u32x4*)(stage + k_lds_off(krow, 2 * tt + hl));
+        for (int kb2 = 0; kb2 < 2; ++kb2) {
+          const u32x4 w = *(const u32x4*)(stage + k_lds_off(kb2 * 32 + ql, 2 * tt + hl));
           s[kb2] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, w), qreg[tt],
                                                             s[kb2], 0, 0, 0);
         }
@@ -425,17 +424,16 @@ void attn_kernel(AttnArgs a) {
 //
 // A workgroup is 8 waves, two per SIMD.  Waves 0-3 (group A) own query rows
 // R0..R0+31 and waves 4-7 (group B) rows R0+32..R0+63, each wave one query head of a
-// GQA group of 4, so all 8 waves read the same K/V tiles.  Work is cut into sections
-// separated by workgroup barriers; in every section one group runs its matrix work
-// (P.V of the previous tile and Q.K of the current one: 32 MFMAs) while the other
-// runs its softmax (VALU), and the roles swap each section.  Group B runs one section
-// behind group A, so the two waves sharing a SIMD always have complementary work and
-// the MFMA pipe and the VALU co-execute.
+// GQA group of 4, so all 8 waves read the same K/V tiles.  In every section one group
+// runs its matrix work (P.V of the previous tile and Q.K of the current one: 32 MFMAs,
+// at raised issue priority) while the other runs its softmax (VALU), and the roles
+// swap each section: group B runs one section behind group A, so the two waves that
+// share a SIMD always have complementary work and the MFMA pipe and the VALU
+// co-execute.  Two sections form a window; the workgroup synchronises once per window.
 //
-// K tiles are staged one section pair ahead of V tiles: K(t+1) and V(t) are loaded in
-// even sections and written to LDS in odd ones (threads 256-511 stage K with the
-// per-key counts / timestamps, threads 0-255 stage V^T).  Two K and two V stages
-// (66.5 KiB) suffice because every stage is rewritten only after both groups read it.
+// K and V tiles go straight from memory to LDS (buffer_load ... lds), three stages
+// each, issued two windows ahead of their use; V is kept row-major and read as V^T
+// with ds_read_b64_tr_b16.  No tile passes through registers.
 //
 // The running maximum is updated lazily: only when a tile's maximum exceeds it by
 // more than 2^8 in probability (8 in log2 units) are O and l rescaled, so p stays
@@ -467,18 +465,6 @@ __device__ __forceinline__ void mask_pure(f32x16* s, const int* tl, int row, int
     }
 }
 
-// Scheduling pattern for a block of 16 LDS operand reads feeding 16 MFMAs: four reads
-// are issued ahead, then reads and MFMAs alternate, so an MFMA rarely waits for LDS.
-__device__ __forceinline__ void pipe_mfma_reads() {
-  __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);  // DS read x4
-#pragma unroll
-  for (int i = 0; i < 12; ++i) {
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
-  }
-  __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);  // MFMA x4
-}
-
 // Third dword of a raw buffer resource on gfx9 (32-bit data format, no swizzle).
 constexpr int kBufferDword3 = 0x00020000;
 
@@ -500,7 +486,6 @@ __device__ __forceinline__ void barrier_keep_loads() {
 
 typedef short i16x4 __attribute__((ext_vector_type(4)));
 typedef short i16x8 __attribute__((ext_vector_type(8)));
-typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
 // LDS byte address of a pointer into the kernel's LDS.
 __device__ __forceinline__ uint32_t lds_addr(const void* p) {
@@ -541,25 +526,27 @@ __device__ __forceinline__ float halves_sum(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// MFMAs of a P.V block whose V^T operand reads run this many MFMAs ahead.
+constexpr int kTrAhead = 6;
+
+// Scheduling pattern for a block of 16 LDS operand reads feeding 16 MFMAs: eight reads
+// are issued ahead, then reads and MFMAs alternate, so an MFMA rarely waits for LDS.
+__device__ __forceinline__ void pipe_mfma_reads_deep() {
+  __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);  // DS read x8
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
+    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
+  }
+  __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);  // MFMA x8
+}
+
 // s_waitcnt immediate (gfx9 encoding) that waits for vmcnt <= n only.
 constexpr int vmcnt_only(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 
-// As pipe_mfma_reads, for P.V blocks whose operand takes two transpose reads.
-__device__ __forceinline__ void pipe_mfma_reads_tr() {
-  __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);  // DS read x8
-#pragma unroll
-  for (int i = 0; i < 12; ++i) {
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-    __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);  // DS read x2
-  }
-  __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);  // MFMA x4
-}
-
-constexpr int kPPK = kKBytes + kTileN * 8;   // K tile + float counts[64] + int ts[64]
-constexpr int kPPV = kVBytes;
-constexpr int kPPLds = 2 * kPPK + 2 * kPPV;
-constexpr int kDmaMetaSlot = kTileN * 8;  // float weights[64], int timestamps[64]
-constexpr int kDmaLds = 3 * kKBytes + 3 * kVBytes + 4 * kDmaMetaSlot;
+constexpr int kPPMetaSlot = kTileN * 8;  // float weights[64], int timestamps[64]
+constexpr int kPPLds = 3 * kKBytes + 3 * kVBytes + 4 * kPPMetaSlot;
+// offsets of the weights and timestamps relative to (slot - kPPCnt), as in a K stage
 constexpr int kPPCnt = kKBytes;
 constexpr int kPPTs = kKBytes + kTileN * 4;
 constexpr float kLazyLog2 = 8.0f;
@@ -567,311 +554,6 @@ constexpr float kLazyLog2 = 8.0f;
 template <int VARIANT>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void attn_pp_kernel(AttnArgs a) {
-  extern __shared__ __attribute__((aligned(16))) char smem[];
-  char* const kst0 = smem;
-  char* const vst0 = smem + 2 * kPPK;
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wid = tid >> 6;  // uniform per wave; kept as a VGPR value (lower register pressure)
-  const int grp = wid >> 2, hw = wid & 3;
-  const int hl = lane >> 5, ql = lane & 31;
-
-  // ---- workgroup -> (unit, row group): XCD-aware, longest rows first ----
-  const int wg = blockIdx.x;
-  int unit, rg;
-  if ((a.units & 7) == 0) {
-    const int xcd = wg & 7, idx = wg >> 3, upx = a.units >> 3;
-    unit = xcd * upx + idx % upx;
-    rg = a.n_row_groups - 1 - idx / upx;
-  } else {
-    unit = wg % a.units;
-    rg = a.n_row_groups - 1 - wg / a.units;
-  }
-  const int hunits = a.G >> 2;
-  const int bg = unit / hunits;
-  const int hu = unit - bg * hunits;
-  const int b = bg / a.Hkv, g = bg - (bg / a.Hkv) * a.Hkv;
-  const int h = g * a.G + hu * 4 + hw;
-  const int R0 = rg * 64;
-  const int r0w = R0 + grp * 32;
-  const int wg_end = R0 + 64;
-  const int start_m = (R0 / kBlock) * kBlock;
-  const int row = r0w + ql;
-
-  // ---- schedule (identical to attn_kernel) ----
-  int P = a.P_host;
-  if (a.P_dev) P = min(*a.P_dev, a.P_host);
-  int n1 = 0, ds = 0;
-  int kend = a.causal ? min(a.Nk, wg_end) : a.Nk;
-  if (VARIANT == kHybrid || VARIANT == kSanity) {
-    const int nblk = (P + kBlock - 1) / kBlock;
-    const int32_t* bmax = a.sched + (int64_t)bg * 2 * a.nblk_cap;
-    const int32_t* pmax = bmax + a.nblk_cap;
-    const int thr = start_m - a.window;
-    int lo = 0, hi = nblk;
-    while (lo < hi) {
-      const int mid = (lo + hi) >> 1;
-      if (pmax[mid] < thr) lo = mid + 1; else hi = mid;
-    }
-    const int last = lo > 0 ? bmax[lo - 1] : -1;
-    ds = max(0, ((last + 1) / kBlock) * kBlock);
-    if (VARIANT == kHybrid) n1 = lo * (kBlock / kTileN);
-    kend = min(a.Nk, wg_end);
-  } else if (VARIANT == kPure) {
-    n1 = (P + kTileN - 1) / kTileN;
-    kend = 0;
-  }
-  const int n2 = kend > ds ? (kend - ds + kTileN - 1) / kTileN : 0;
-  const int T = n1 + n2;
-
-  const uint16_t* kp_base = a.kp + (int64_t)b * a.skp_b + (int64_t)g * a.skp_h;
-  const uint16_t* vp_base = a.vp + (int64_t)b * a.svp_b + (int64_t)g * a.svp_h;
-  const uint16_t* k_base = a.k + (int64_t)b * a.sk_b + (int64_t)g * a.sk_h;
-  const uint16_t* v_base = a.v + (int64_t)b * a.sv_b + (int64_t)g * a.sv_h;
-  const int32_t* ts_row = a.ts ? a.ts + (int64_t)b * a.sts_b + (int64_t)g * a.sts_h : nullptr;
-  const char* cnt_row = a.cnt ? (const char*)a.cnt + ((int64_t)b * a.scnt_b + (int64_t)g * a.scnt_h) * 4 : nullptr;
-  constexpr bool kPureV = VARIANT == kPure;
-  constexpr bool kWeights = VARIANT == kHybrid || VARIANT == kPure;
-
-  auto key0_of = [&](int t) { return t < n1 ? t * kTileN : ds + (t - n1) * kTileN; };
-  auto skipped = [&](int t) { return t >= n1 && a.causal && key0_of(t) > r0w + 31; };
-
-  // ---- staging: waves 4-7 stage K (+ counts, timestamps), waves 0-3 stage V ----
-  // Rows are fetched with buffer loads whose resource covers exactly the tile's valid
-  // keys, so rows past the end of the keys read as zero without any select, and the
-  // tile base lives in scalar registers (no 64-bit per-lane address arithmetic).  The
-  // tile index is clamped; staging slots past the last tile are loaded and written too,
-  // the schedule below never reads them and the LDS stages they land in are free then.
-  const bool kthr = wid >= 4;
-  const int tq = tid & 255;
-  const int s_chunk = kthr ? (tq & 15) : (tq >> 4);  // 16-byte chunk of the row
-  const int s_grp = kthr ? (tq >> 4) : (tq & 15);    // group of 4 keys
-  const char* sb1 = (const char*)uniform_ptr(kthr ? kp_base : vp_base);  // Phase-1 source
-  const char* sb2 = (const char*)uniform_ptr(kthr ? k_base : v_base);    // Phase-2 source
-  const int sn1b = __builtin_amdgcn_readfirstlane((int)(2 * (kthr ? a.skp_n : a.svp_n)));  // bytes
-  const int sn2b = __builtin_amdgcn_readfirstlane((int)(2 * (kthr ? a.sk_n : a.sv_n)));
-  struct SRegs {
-    u32x4 x[4];
-    int ts;
-    int craw;  // count word as loaded (float or int32 bits)
-    bool cvalid;
-  };
-  auto stage_load = [&](SRegs& R, int t_raw) {
-    const int t = min(t_raw, T - 1);
-    const bool ph1 = t < n1;
-    const int key0 = key0_of(t);
-    const int limit = ph1 ? P : a.Nk;
-    const int snb = ph1 ? sn1b : sn2b;
-    const void* base = uniform_ptr((ph1 ? sb1 : sb2) + (int64_t)key0 * snb);
-    const int nrows = max(0, min(limit - key0, kTileN));
-    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<void*>(base), (short)0, __builtin_amdgcn_readfirstlane(nrows * snb), kBufferDword3);
-    const int voff = s_grp * 4 * snb + s_chunk * 16;
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      R.x[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, voff + j * snb, 0, 0));
-    if (kWeights) {
-      // raw words only; conversion and validity are applied in stage_store
-      const int key = key0 + (tq & 63);
-      const int kc = max(min(key, P - 1), 0);
-      R.cvalid = ph1 && key < P;
-      R.craw = P > 0 ? ((const int32_t*)cnt_row)[kc] : 0;
-      if (kPureV) R.ts = P > 0 ? ts_row[kc] : INT_MAX;
-    }
-  };
-  auto stage_store = [&](const SRegs& R, int t) {
-    if (kthr) {
-      char* st = kst0 + (t & 1) * kPPK;
-#pragma unroll
-      for (int j = 0; j < 4; ++j) *(u32x4*)(st + k_lds_off(s_grp * 4 + j, s_chunk)) = R.x[j];
-      if (kWeights && tq < kTileN) {
-        const float cv0 = a.cnt_is_float ? __int_as_float(R.craw) : (float)R.craw;
-        const float cv = R.cvalid ? (a.no_count ? 1.0f : cv0) : 0.0f;
-        ((float*)(st + kPPCnt))[tq] = cv;
-        if (kPureV) ((int*)(st + kPPTs))[tq] = cv > 0.0f ? R.ts : INT_MAX;
-      }
-    } else {
-      char* st = vst0 + (t & 1) * kPPV - kKBytes;  // vt_lds_* offsets include kKBytes
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        const uint32_t x0 = R.x[0][w], x1 = R.x[1][w], x2 = R.x[2][w], x3 = R.x[3][w];
-        const int d0 = s_chunk * 8 + 2 * w;
-        u32x2 lo, hi;
-        lo[0] = __builtin_amdgcn_perm(x1, x0, 0x05040100u);
-        lo[1] = __builtin_amdgcn_perm(x3, x2, 0x05040100u);
-        hi[0] = __builtin_amdgcn_perm(x1, x0, 0x07060302u);
-        hi[1] = __builtin_amdgcn_perm(x3, x2, 0x07060302u);
-        *(u32x2*)(st + vt_lds_group(d0, s_grp)) = lo;
-        *(u32x2*)(st + vt_lds_group(d0 + 1, s_grp)) = hi;
-      }
-    }
-  };
-
-  // ---- per-lane LDS offsets (stage-relative) ----
-  int k_off[kD / 16];
-#pragma unroll
-  for (int tt = 0; tt < kD / 16; ++tt) k_off[tt] = k_lds_off(ql, 2 * tt + hl);  // + 8192 * kb2
-  int v_off[4];
-#pragma unroll
-  for (int u = 0; u < 4; ++u) v_off[u] = vt_lds_chunk(ql, 2 * u + hl) - kKBytes;  // + 4096 * db
-
-  // ---- Q^T in registers ----
-  bf16x8 qreg[kD / 16];
-  {
-    const uint16_t* qrow = a.q + (int64_t)b * a.sq_b + (int64_t)h * a.sq_h + (int64_t)row * a.sq_n;
-#pragma unroll
-    for (int t = 0; t < kD / 16; ++t) {
-      u32x4 w = (row < a.Nq) ? *(const u32x4*)(qrow + 16 * t + 8 * hl) : u32x4{0, 0, 0, 0};
-      qreg[t] = __builtin_bit_cast(bf16x8, w);
-    }
-    // Redefine Q^T here so the loop does not see it as an outstanding load: otherwise
-    // every S = K Q^T block waits for all memory loads, including the staging loads
-    // meant to land two sections later.
-#pragma unroll
-    for (int t = 0; t < kD / 16; ++t) asm volatile("" : "+v"(qreg[t]));
-  }
-
-  f32x16 o[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) o[i] = f32x16{};
-  f32x16 s[2];
-  u32x4 pw[4];
-  float m_used = -INFINITY, l_i = 0.0f;
-  const float c = a.scale_log2;
-
-  // K(t + 1) is written to LDS by waves 4-7 at the end of section 2t, V(t) by waves
-  // 0-3 at the end of section 2t + 1: always by the group in its softmax section, and
-  // each stage is free by then (K(t - 1) was last read in section 2t - 1, V(t - 2) in
-  // section 2t - 1).  The loads of the next tile are issued right after each store, so
-  // every load has two sections to land.
-  SRegs sr;
-  sr.ts = 0;
-  sr.craw = 0;
-  sr.cvalid = false;
-  if (T > 0) {
-    if (kthr) {
-      stage_load(sr, 0);
-      stage_store(sr, 0);
-    }
-    stage_load(sr, kthr ? 1 : 0);
-  }
-  lds_barrier();
-
-  const int nsec = T > 0 ? 2 * T + 2 : 0;
-  for (int sec = 0; sec < nsec; ++sec) {
-    const int tl = sec >> 1;
-    const int sw = sec - grp;
-    if (sw >= 0) {
-      const int t = sw >> 1;
-      if ((sw & 1) == 0) {
-        // ---- matrix section: O^T += V^T P^T for tile t-1, then S^T = K Q^T for tile t ----
-        if (t >= 1 && !skipped(t - 1)) {
-          const char* vst = vst0 + ((t - 1) & 1) * kPPV;
-#pragma unroll
-          for (int u = 0; u < 4; ++u) {
-            const bf16x8 pbv = __builtin_bit_cast(bf16x8, pw[u]);
-#pragma unroll
-            for (int db = 0; db < 4; ++db) {
-              const u32x4 vw = *(const u32x4*)(vst + v_off[u] + db * 4096);
-              o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, vw), pbv,
-                                                               o[db], 0, 0, 0);
-            }
-          }
-          pipe_mfma_reads();
-        }
-        if (t < T && !skipped(t)) {
-          const char* kst = kst0 + (t & 1) * kPPK;
-#pragma unroll
-          for (int kb2 = 0; kb2 < 2; ++kb2) {
-            s[kb2] = f32x16{};
-#pragma unroll
-            for (int tt = 0; tt < kD / 16; ++tt) {
-              const u32x4 w = *(const u32x4*)(kst + k_off[tt] + kb2 * 8192);
-              s[kb2] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, w),
-                                                                qreg[tt], s[kb2], 0, 0, 0);
-            }
-          }
-          pipe_mfma_reads();
-        }
-      } else if (t < T && !skipped(t)) {
-        // ---- softmax section for tile t ----
-        const char* kst = kst0 + (t & 1) * kPPK;
-        const int key0 = key0_of(t);
-        if (kPureV) {
-          mask_pure(s, (const int*)(kst + kPPTs), row, hl);
-        } else if (t >= n1) {
-          if ((a.causal && key0 + kTileN - 1 > r0w) || key0 + kTileN > a.Nk)
-            mask_dense(s, key0, row, hl, a.Nk, a.causal);
-        }
-        float mx = -INFINITY;
-#pragma unroll
-        for (int r = 0; r < 16; ++r) mx = __builtin_fmaxf(mx, __builtin_fmaxf(s[0][r], s[1][r]));
-        mx = __builtin_fmaxf(mx, swap_halves(mx));
-        const bool upd = (mx - m_used) * c > kLazyLog2;
-        if (__ballot(upd)) {
-          const float m_new = upd ? mx : m_used;
-          const float alpha = exp2_fast((m_used - m_new) * c);
-#pragma unroll
-          for (int db = 0; db < 4; ++db)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
-          l_i *= alpha;
-          m_used = m_new;
-        }
-        const float neg = (m_used == -INFINITY) ? 0.0f : -m_used * c;
-        const bool weighted = kWeights && t < n1;
-        const float* cl = (const float*)(kst + kPPCnt);
-        float psum = 0.0f;
-#pragma unroll
-        for (int kb2 = 0; kb2 < 2; ++kb2) {
-#pragma unroll
-          for (int r4 = 0; r4 < 4; ++r4) {
-            float p[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) p[e] = exp2_fast(__builtin_fmaf(s[kb2][4 * r4 + e], c, neg));
-            if (weighted) {
-              const f32x4 w4 = *(const f32x4*)(cl + kb2 * 32 + 8 * r4 + 4 * hl);
-#pragma unroll
-              for (int e = 0; e < 4; ++e) p[e] *= w4[e];
-            }
-            psum += (p[0] + p[1]) + (p[2] + p[3]);
-            pw[2 * kb2 + (r4 >> 1)][(r4 & 1) * 2 + 0] = pack_bf16x2(p[0], p[1]);
-            pw[2 * kb2 + (r4 >> 1)][(r4 & 1) * 2 + 1] = pack_bf16x2(p[2], p[3]);
-          }
-        }
-        l_i += psum;
-      }
-    }
-    if (kthr == ((sec & 1) == 0)) {
-      stage_store(sr, kthr ? tl + 1 : tl);
-      stage_load(sr, kthr ? tl + 2 : tl + 1);
-    }
-    lds_barrier();
-  }
-
-  // ---- finalize ----
-  const float l_tot = l_i + swap_halves(l_i);
-  float inv;
-  if (VARIANT == kPure)
-    inv = l_tot > 0.0f ? 1.0f / l_tot : 1.0f;  // deltaFlashAttention.py:353-354
-  else
-    inv = 1.0f / l_tot;
-  if (row < a.Nq) {
-    uint16_t* orow = a.out + (int64_t)b * a.so_b + (int64_t)h * a.so_h + (int64_t)row * a.so_n;
-#pragma unroll
-    for (int db = 0; db < 4; ++db)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        u32x2 w;
-        w[0] = pack_bf16x2(o[db][4 * j + 0] * inv, o[db][4 * j + 1] * inv);
-        w[1] = pack_bf16x2(o[db][4 * j + 2] * inv, o[db][4 * j + 3] * inv);
-        *(u32x2*)(orow + db * 32 + 8 * j + 4 * hl) = w;
-      }
-  }
-}
-
-template <int VARIANT>
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
-void attn_dma_kernel(AttnArgs a) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
   char* const kst0 = smem;
   char* const vst0 = smem + 3 * kKBytes;
@@ -981,7 +663,7 @@ void attn_dma_kernel(AttnArgs a) {
     }
   };
   // raw weights (and timestamps) of the tile's 64 keys, into slot t % 4 of their ring
-  auto meta_of = [&](int t) { return meta0 + (t & 3) * kDmaMetaSlot; };
+  auto meta_of = [&](int t) { return meta0 + (t & 3) * kPPMetaSlot; };
   auto dma_meta = [&](int t_raw) {
     if (!kWeights) return;
     const int t = min(t_raw, T - 1);
@@ -1114,21 +796,22 @@ void attn_dma_kernel(AttnArgs a) {
 #pragma unroll
           for (int db = 0; db < 4; ++db) va[db] = vb + v_off[db];
           i16x4 vlo[16], vhi[16];
-          static_for<4>([&](auto I) {
+          static_for<kTrAhead>([&](auto I) {
             constexpr int j = decltype(I)::value;
             vlo[j] = ds_read_tr16<(j >> 2) * 4096>(va[j & 3]);
             vhi[j] = ds_read_tr16<(j >> 2) * 4096 + 2048>(va[j & 3]);
           });
           static_for<16>([&](auto I) {
             constexpr int i = decltype(I)::value;
-            constexpr int after = 2 * ((i + 3 < 15 ? i + 3 : 15) - i);  // reads issued after those of MFMA i
+            // reads issued after those of MFMA i
+            constexpr int after = 2 * ((i + kTrAhead - 1 < 15 ? i + kTrAhead - 1 : 15) - i);
             lgkm_wait<after>(vlo[i], vhi[i]);
             const i16x8 vw = __builtin_shufflevector(vlo[i], vhi[i], 0, 1, 2, 3, 4, 5, 6, 7);
             o[i & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, vw),
                                                                 __builtin_bit_cast(bf16x8, pw[i >> 2]),
                                                                 o[i & 3], 0, 0, 0);
-            if constexpr (i + 4 < 16) {
-              constexpr int j = i + 4;
+            if constexpr (i + kTrAhead < 16) {
+              constexpr int j = i + kTrAhead;
               vlo[j] = ds_read_tr16<(j >> 2) * 4096>(va[j & 3]);
               vhi[j] = ds_read_tr16<(j >> 2) * 4096 + 2048>(va[j & 3]);
             }
@@ -1137,17 +820,19 @@ void attn_dma_kernel(AttnArgs a) {
         issue_once();
         if (t < T && !skipped(t)) {
           const char* kst = kst0 + (t % 3) * kKBytes;
+          // the two key blocks alternate so that consecutive MFMAs do not depend on each other
+          s[0] = f32x16{};
+          s[1] = f32x16{};
 #pragma unroll
-          for (int kb2 = 0; kb2 < 2; ++kb2) {
-            s[kb2] = f32x16{};
+          for (int tt = 0; tt < kD / 16; ++tt) {
 #pragma unroll
-            for (int tt = 0; tt < kD / 16; ++tt) {
+            for (int kb2 = 0; kb2 < 2; ++kb2) {
               const u32x4 w = *(const u32x4*)(kst + k_off[tt] + kb2 * 8192);
               s[kb2] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, w),
                                                                 qreg[tt], s[kb2], 0, 0, 0);
             }
           }
-          pipe_mfma_reads();
+          pipe_mfma_reads_deep();
         }
         __builtin_amdgcn_s_setprio(0);
       } else if (t < T && !skipped(t)) {
@@ -1216,500 +901,6 @@ void attn_dma_kernel(AttnArgs a) {
 
   // ---- finalize ----
   const float l_tot = halves_sum(l_i);
-  float inv;
-  if (VARIANT == kPure)
-    inv = l_tot > 0.0f ? 1.0f / l_tot : 1.0f;  // deltaFlashAttention.py:353-354
-  else
-    inv = 1.0f / l_tot;
-  if (row < a.Nq) {
-    uint16_t* orow = a.out + (int64_t)b * a.so_b + (int64_t)h * a.so_h + (int64_t)row * a.so_n;
-#pragma unroll
-    for (int db = 0; db < 4; ++db)
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        u32x2 w;
-        w[0] = pack_bf16x2(o[db][4 * j + 0] * inv, o[db][4 * j + 1] * inv);
-        w[1] = pack_bf16x2(o[db][4 * j + 2] * inv, o[db][4 * j + 3] * inv);
-        *(u32x2*)(orow + db * 32 + 8 * j + 4 * hl) = w;
-      }
-  }
-}
-
-// ---------------------------------------------------------------------------------
-// Intra-wave pipelined kernel for GQA groups that are a multiple of 4.  A workgroup is
-// four waves, one per SIMD with up to 512 registers each; wave w computes query head
-// 4 * hu + w for the 32 rows R0 .. R0 + 31, and the four waves share the staged K and
-// V^T tiles.  Step t (one 64-key tile) has two phases of 16 slots; a slot is one MFMA
-// plus a fixed slice of VALU / LDS / memory work that does not depend on it, so one
-// wave keeps its matrix pipe and its VALU busy together (sched_barrier between slots):
-//   phase 1: S(t+1) = K(t+1) Q^T    (16 MFMA) || P of keys 0-31 of tile t, staging
-//   phase 2: O += V(t-1)^T P(t-1)^T (16 MFMA) || P of keys 32-63 of tile t, running
-//            max of S(t+1)
-// The running max runs one tile ahead of the exponentials and P.V one tile behind
-// them.  The factor the max of tile t asks of O is applied in step t + 1 between the
-// phases, after P.V of tile t - 1 and before that of tile t.
-// Staging: at the start of step t every thread writes its registers of K(t+2) and V(t)
-// to LDS and issues the loads of K(t+3) and V(t+1) into the same registers, so each
-// load has about one step to land; one barrier per step.
-// ---------------------------------------------------------------------------------
-
-// LDS: K stages (2 x 16 KiB), V^T stages (2 x 16 KiB), then a ring of 3 slots of
-// per-key weights (float[64]) and timestamps (int[64]): the slot of tile t is written
-// with K(t) in step t - 2 and read by the softmax of tile t in step t.
-constexpr int kIWV = 2 * kKBytes;
-constexpr int kIWMeta = 2 * kKBytes + 2 * kVBytes;
-constexpr int kIWMetaSlot = kTileN * 8;
-constexpr int kIWLds = kIWMeta + 3 * kIWMetaSlot;
-
-
-// Instruction order for one phase of attn_iw_kernel (16 MFMAs fed by 16 LDS operand
-// reads, plus VALU work that does not depend on them): the operand reads run four
-// ahead and NV VALU instructions follow every MFMA, so the VALU issues while the
-// matrix pipe works.  With STAGING the phase also carries 12 LDS writes and 8 buffer
-// loads, spread over the second half.
-template <int NV, bool STAGING>
-__device__ __forceinline__ void sched_phase() {
-  __builtin_amdgcn_sched_group_barrier(0x100, 4, 0);  // DS read x4
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-    __builtin_amdgcn_sched_group_barrier(0x002, NV, 0);  // VALU
-    if (i < 12) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
-    if (STAGING && i >= 4) {
-      __builtin_amdgcn_sched_group_barrier(0x200, 1, 0);  // DS write
-      if (i & 1) __builtin_amdgcn_sched_group_barrier(0x020, 2, 0);  // VMEM read
-    }
-  }
-}
-
-template <int VARIANT>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 1)))
-void attn_iw_kernel(AttnArgs a) {
-  extern __shared__ __attribute__((aligned(16))) char smem[];
-  char* const kst0 = smem;
-  char* const vst0 = smem + kIWV;
-  char* const meta0 = smem + kIWMeta;
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int hw = tid >> 6;
-  const int hl = lane >> 5, ql = lane & 31;
-  constexpr bool kPureV = VARIANT == kPure;
-  constexpr bool kWeights = VARIANT == kHybrid || VARIANT == kPure;
-
-  // ---- workgroup -> (unit, row group): XCD-aware, longest rows first ----
-  const int wg = blockIdx.x;
-  int unit, rg;
-  if ((a.units & 7) == 0) {
-    const int xcd = wg & 7, idx = wg >> 3, upx = a.units >> 3;
-    unit = xcd * upx + idx % upx;
-    rg = a.n_row_groups - 1 - idx / upx;
-  } else {
-    unit = wg % a.units;
-    rg = a.n_row_groups - 1 - wg / a.units;
-  }
-  const int hunits = a.G >> 2;
-  const int bg = unit / hunits;
-  const int hu = unit - bg * hunits;
-  const int b = bg / a.Hkv, g = bg - (bg / a.Hkv) * a.Hkv;
-  const int h = g * a.G + hu * 4 + hw;
-  const int R0 = rg * 32;
-  const int wg_end = R0 + 32;
-  const int start_m = (R0 / kBlock) * kBlock;
-  const int row = R0 + ql;
-
-  // ---- schedule (deltaFlashAttention.py:56-100, as in attn_kernel) ----
-  int P = a.P_host;
-  if (a.P_dev) P = min(*a.P_dev, a.P_host);
-  int n1 = 0, ds = 0;
-  int kend = a.causal ? min(a.Nk, wg_end) : a.Nk;
-  if (VARIANT == kHybrid || VARIANT == kSanity) {
-    const int nblk = (P + kBlock - 1) / kBlock;
-    const int32_t* bmax = a.sched + (int64_t)bg * 2 * a.nblk_cap;
-    const int32_t* pmax = bmax + a.nblk_cap;
-    const int thr = start_m - a.window;
-    int lo = 0, hi = nblk;
-    while (lo < hi) {
-      const int mid = (lo + hi) >> 1;
-      if (pmax[mid] < thr) lo = mid + 1; else hi = mid;
-    }
-    const int last = lo > 0 ? bmax[lo - 1] : -1;
-    ds = max(0, ((last + 1) / kBlock) * kBlock);
-    if (VARIANT == kHybrid) n1 = lo * (kBlock / kTileN);
-    kend = min(a.Nk, wg_end);
-  } else if (VARIANT == kPure) {
-    n1 = (P + kTileN - 1) / kTileN;
-    kend = 0;
-  }
-  n1 = __builtin_amdgcn_readfirstlane(n1);
-  ds = __builtin_amdgcn_readfirstlane(ds);
-  P = __builtin_amdgcn_readfirstlane(P);
-  const int n2 = kend > ds ? (kend - ds + kTileN - 1) / kTileN : 0;
-  const int T = __builtin_amdgcn_readfirstlane(n1 + n2);
-
-  const uint16_t* kp_base = a.kp + (int64_t)b * a.skp_b + (int64_t)g * a.skp_h;
-  const uint16_t* vp_base = a.vp + (int64_t)b * a.svp_b + (int64_t)g * a.svp_h;
-  const uint16_t* k_base = a.k + (int64_t)b * a.sk_b + (int64_t)g * a.sk_h;
-  const uint16_t* v_base = a.v + (int64_t)b * a.sv_b + (int64_t)g * a.sv_h;
-  const int32_t* ts_row = a.ts ? a.ts + (int64_t)b * a.sts_b + (int64_t)g * a.sts_h : nullptr;
-  const char* cnt_row = a.cnt ? (const char*)a.cnt + ((int64_t)b * a.scnt_b + (int64_t)g * a.scnt_h) * 4 : nullptr;
-
-  auto key0_of = [&](int t) { return t < n1 ? t * kTileN : ds + (t - n1) * kTileN; };
-  // tiles whose dense keys need the causal / length mask (every tile for pure Phase 1)
-  auto needs_mask = [&](int t) {
-    if (kPureV) return true;
-    if (t < n1) return false;
-    const int key0 = key0_of(t);
-    return (a.causal && key0 + kTileN - 1 > R0) || key0 + kTileN > a.Nk;
-  };
-
-  // ---- staging: every thread stages 4 rows of K (16-byte chunk s_kc of keys
-  // 4 s_kg .. 4 s_kg + 3) and 4 rows of V (chunk s_vc of keys 4 s_vg ..), the latter
-  // transposed into V^T.  Buffer loads whose resource covers exactly the tile's valid
-  // keys read rows past the end as zero. ----
-  const int s_kc = tid & 15, s_kg = tid >> 4;
-  const int s_vc = tid >> 4, s_vg = tid & 15;
-  const char* kb1 = (const char*)uniform_ptr(kp_base);
-  const char* kb2 = (const char*)uniform_ptr(k_base);
-  const char* vb1 = (const char*)uniform_ptr(vp_base);
-  const char* vb2 = (const char*)uniform_ptr(v_base);
-  const int skp = (int)(2 * a.skp_n), sk = (int)(2 * a.sk_n);
-  const int svp = (int)(2 * a.svp_n), sv = (int)(2 * a.sv_n);
-  struct SRegs {
-    u32x4 k[4];
-    u32x4 v[4];
-    int ts;
-    int craw;
-    int cstate;  // 0: past the packed keys (weight 0), 1: packed key, 2: dense key (weight 1)
-  };
-  auto load_rows = [&](u32x4* x, const char* b1, const char* b2, int sb1, int sb2, int t, int grp4, int chunk) {
-    const bool ph1 = t < n1;
-    const int key0 = key0_of(t);
-    const int limit = ph1 ? P : a.Nk;
-    const int snb = ph1 ? sb1 : sb2;
-    const void* base = uniform_ptr((ph1 ? b1 : b2) + (int64_t)key0 * snb);
-    const int nrows = max(0, min(limit - key0, kTileN));
-    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<void*>(base), (short)0, __builtin_amdgcn_readfirstlane(nrows * snb), kBufferDword3);
-    const int voff = grp4 * 4 * snb + chunk * 16;
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-      x[j] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, voff + j * snb, 0, 0));
-  };
-  auto stage_load_k = [&](SRegs& R, int tk) {
-    tk = min(tk, T - 1);
-    load_rows(R.k, kb1, kb2, skp, sk, tk, s_kg, s_kc);
-    if (kWeights) {
-      const int key = key0_of(tk) + (tid & 63);
-      const int kc = max(min(key, P - 1), 0);  // P >= 1 (checked on the host)
-      R.cstate = tk < n1 ? (key < P ? 1 : 0) : 2;
-      R.craw = ((const int32_t*)cnt_row)[kc];
-      if (kPureV) R.ts = ts_row[kc];
-    }
-  };
-  auto stage_load_v = [&](SRegs& R, int tv) {
-    load_rows(R.v, vb1, vb2, svp, sv, min(tv, T - 1), s_vg, s_vc);
-  };
-  auto meta_of = [&](int t) { return meta0 + (t % 3) * kIWMetaSlot; };
-  // K row j of this thread (and, with row 0, the key's weight and timestamp)
-  auto store_k_row = [&](const SRegs& R, int tk, int j) {
-    char* ks = kst0 + (tk & 1) * kKBytes;
-    *(u32x4*)(ks + k_lds_off(s_kg * 4 + j, s_kc)) = R.k[j];
-    if (kWeights && j == 0) {
-      // four threads write each key's entry, all with the same value (no branch)
-      const float cv0 = a.cnt_is_float ? __int_as_float(R.craw) : (float)R.craw;
-      const float cv = R.cstate == 2 ? 1.0f : R.cstate == 1 ? (a.no_count ? 1.0f : cv0) : 0.0f;
-      char* ms = meta_of(tk);
-      ((float*)ms)[tid & 63] = cv;
-      if (kPureV) ((int*)(ms + kTileN * 4))[tid & 63] = cv > 0.0f ? R.ts : INT_MAX;
-    }
-  };
-  auto store_k = [&](const SRegs& R, int tk) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j) store_k_row(R, tk, j);
-  };
-  // head dimensions s_vc * 8 + 2w, + 1 of the 4 staged V rows, as V^T
-  auto store_v_part = [&](const SRegs& R, int tv, int w) {
-    char* vs = vst0 + (tv & 1) * kVBytes - kKBytes;  // vt_lds_* offsets include kKBytes
-    const uint32_t x0 = R.v[0][w], x1 = R.v[1][w], x2 = R.v[2][w], x3 = R.v[3][w];
-    const int d0 = s_vc * 8 + 2 * w;
-    u32x2 lo, hi;
-    lo[0] = __builtin_amdgcn_perm(x1, x0, 0x05040100u);
-    lo[1] = __builtin_amdgcn_perm(x3, x2, 0x05040100u);
-    hi[0] = __builtin_amdgcn_perm(x1, x0, 0x07060302u);
-    hi[1] = __builtin_amdgcn_perm(x3, x2, 0x07060302u);
-    *(u32x2*)(vs + vt_lds_group(d0, s_vg)) = lo;
-    *(u32x2*)(vs + vt_lds_group(d0 + 1, s_vg)) = hi;
-  };
-  auto store_v = [&](const SRegs& R, int tv) {
-#pragma unroll
-    for (int w = 0; w < 4; ++w) store_v_part(R, tv, w);
-  };
-
-  // ---- per-lane LDS offsets (stage-relative) ----
-  int k_off[kD / 16];
-#pragma unroll
-  for (int tt = 0; tt < kD / 16; ++tt) k_off[tt] = k_lds_off(ql, 2 * tt + hl);  // + 8192 * kb
-  int v_off[4];
-#pragma unroll
-  for (int u = 0; u < 4; ++u) v_off[u] = vt_lds_chunk(ql, 2 * u + hl) - kKBytes;  // + 4096 * db
-
-  // ---- Q^T in registers ----
-  bf16x8 qreg[kD / 16];
-  {
-    const uint16_t* qrow = a.q + (int64_t)b * a.sq_b + (int64_t)h * a.sq_h + (int64_t)row * a.sq_n;
-#pragma unroll
-    for (int t = 0; t < kD / 16; ++t) {
-      const u32x4 w = row < a.Nq ? *(const u32x4*)(qrow + 16 * t + 8 * hl) : u32x4{0, 0, 0, 0};
-      qreg[t] = __builtin_bit_cast(bf16x8, w);
-    }
-    // Q^T lives in AGPRs (the MFMA reads its B operand from there; the VGPRs are
-    // needed by the softmax), and the redefinition also keeps the loop from counting
-    // Q as an outstanding load.
-#pragma unroll
-    for (int t = 0; t < kD / 16; ++t) asm volatile("" : "+a"(qreg[t]));
-  }
-
-  f32x16 o[4];
-#pragma unroll
-  for (int i = 0; i < 4; ++i) o[i] = f32x16{};
-  float m = -INFINITY, l = 0.0f;
-  float neg = 0.0f;  // -m * c
-  const float c = a.scale_log2;
-  const float lazy_thr = kLazyLog2 / c;
-
-  // ---- building blocks ----
-  auto qk = [&](int t, f32x16 (&s)[2]) {
-    const char* kst = kst0 + (t & 1) * kKBytes;
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-      for (int tt = 0; tt < kD / 16; ++tt) {
-        const bf16x8 w = __builtin_bit_cast(bf16x8, *(const u32x4*)(kst + k_off[tt] + kb * 8192));
-        s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(w, qreg[tt], tt == 0 ? f32x16{} : s[kb], 0, 0, 0);
-      }
-    }
-  };
-  auto pv = [&](int t, const u32x4 (&pw)[4]) {
-    const char* vst = vst0 + (t & 1) * kVBytes;
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-#pragma unroll
-      for (int db = 0; db < 4; ++db) {
-        const bf16x8 w = __builtin_bit_cast(bf16x8, *(const u32x4*)(vst + v_off[u] + db * 4096));
-        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(w, __builtin_bit_cast(bf16x8, pw[u]), o[db], 0, 0, 0);
-      }
-    }
-  };
-  auto mask = [&](int t, f32x16 (&s)[2]) {
-    if (kPureV)
-      mask_pure(s, (const int*)(meta_of(t) + kTileN * 4), row, hl);
-    else
-      mask_dense(s, key0_of(t), row, hl, a.Nk, a.causal);
-  };
-  // Max of S values 4g .. 4g + 3 of both key halves.
-  auto max_part = [&](const f32x16 (&s)[2], int g) {
-    return __builtin_fmaxf(
-        __builtin_fmaxf(__builtin_fmaxf(s[0][4 * g], s[0][4 * g + 1]), __builtin_fmaxf(s[0][4 * g + 2], s[0][4 * g + 3])),
-        __builtin_fmaxf(__builtin_fmaxf(s[1][4 * g], s[1][4 * g + 1]), __builtin_fmaxf(s[1][4 * g + 2], s[1][4 * g + 3])));
-  };
-  // Running max of the next tile with lazy rescale (the max moves only when it grows
-  // by more than 2^kLazyLog2); returns the factor for l and O.
-  auto update_max = [&](float mx) {
-    const bool upd = mx > m + lazy_thr;  // no NaN when m = -inf
-    const float m_new = upd ? mx : m;
-    const float al = upd ? exp2_fast((m - m_new) * c) : 1.0f;
-    m = m_new;
-    neg = (m == -INFINITY) ? 0.0f : -m * c;
-    return al;
-  };
-  // P of S values 2j, 2j + 1 of key half kb (MFMA B layout), weighted, summed, in
-  // three stages: A (scale and shift), B (exp2), C (weight, sum, pack).  Slot i of a
-  // phase runs A of pair i, B of pair i - 1 and C of pair i - 2, so the instructions of
-  // one slot do not wait for each other and the MFMA after them issues on time.
-  struct Pipe {
-    float x[2][2];  // after A, by pair parity
-    float p[2][2];  // after B
-  };
-  auto exp_slot = [&](int t, const f32x16& s, u32x4* pw2, int kb, int i, Pipe& pp_, float& psum) {
-    if (i >= 2 && i - 2 < 8) {
-      const int j = i - 2, r4 = j >> 1, half = j & 1;
-      float p0 = pp_.p[j & 1][0], p1 = pp_.p[j & 1][1];
-      if (kWeights) {
-        const f32x2 w2 = *(const f32x2*)((const float*)meta_of(t) + kb * 32 + 8 * r4 + 4 * hl + 2 * half);
-        p0 *= w2[0];
-        p1 *= w2[1];
-      }
-      psum += p0 + p1;
-      uint32_t pk = pack_bf16x2(p0, p1);
-      asm volatile("" : "+v"(pk));  // computed in its slot, not sunk to the MFMA that reads it
-      pw2[r4 >> 1][(r4 & 1) * 2 + half] = pk;
-    }
-    if (i >= 1 && i - 1 < 8) {
-      const int j = i - 1;
-      pp_.p[j & 1][0] = exp2_fast(pp_.x[j & 1][0]);
-      pp_.p[j & 1][1] = exp2_fast(pp_.x[j & 1][1]);
-    }
-    if (i < 8) {
-      pp_.x[i & 1][0] = __builtin_fmaf(s[2 * i], c, neg);
-      pp_.x[i & 1][1] = __builtin_fmaf(s[2 * i + 1], c, neg);
-    }
-  };
-  auto rescale = [&](float f) {
-    if (__ballot(f != 1.0f)) {
-#pragma unroll
-      for (int db = 0; db < 4; ++db)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) o[db][r] *= f;
-    }
-  };
-
-  SRegs r;
-  r.ts = 0;
-  r.craw = 0;
-  r.cstate = 0;
-  float q0 = 1.0f, q1 = 1.0f;  // factors for O before P.V of tiles t - 1 and t
-
-  // Phase 1 of step t: 16 slots, each one MFMA of S(t+1) = K(t+1) Q^T (if QK) plus
-  // a fixed slice of other work -- P of keys 0-31 of tile t and (if ST) the LDS writes
-  // of K(t+2) and V(t) followed by the loads of K(t+3) and V(t+1).  The K operands are
-  // read four slots ahead and sched_barrier keeps the slots in this order.
-  auto phase1 = [&](auto QK, auto ST, int t, const f32x16 (&sc)[2], f32x16 (&sn)[2], u32x4 (&pc)[4]) {
-    constexpr bool kQK = decltype(QK)::value, kST = decltype(ST)::value;
-    const char* kst = kst0 + ((t + 1) & 1) * kKBytes;
-    u32x4 fr[16];
-    if (kQK) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) fr[i] = *(const u32x4*)(kst + k_off[i >> 1] + (i & 1) * 8192);
-    }
-    float psum = 0.0f;
-    Pipe pipe;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      if (kQK) {
-        if (i + 4 < 16) fr[i + 4] = *(const u32x4*)(kst + k_off[(i + 4) >> 1] + ((i + 4) & 1) * 8192);
-        const int kb = i & 1, tt = i >> 1;
-        sn[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, fr[i]), qreg[tt],
-                                                          tt == 0 ? f32x16{} : sn[kb], 0, 0, 0);
-      }
-      if (i < 10) exp_slot(t, sc[0], pc, 0, i, pipe, psum);
-      if (kST) {
-        // LDS writes of the staged rows first, then the loads of the next ones, so
-        // each load has a whole step to land before its registers are written out
-        if (i < 4) {
-          store_k_row(r, t + 2, i);
-          store_v_part(r, t, i);
-        }
-        if (i == 4) stage_load_k(r, t + 3);
-        if (i == 5) stage_load_v(r, t + 1);
-      }
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    l += psum;
-  };
-  // Phase 2 of step t: 16 slots, each one MFMA of O += V(t-1)^T P(t-1)^T (if PV) plus
-  // a slice of P of keys 32-63 of tile t, then (if NX) the running max of S(t+1).
-  auto phase2 = [&](auto PV, auto NX, int t, const f32x16 (&sc)[2], const u32x4 (&pp)[4], u32x4 (&pc)[4],
-                    const f32x16 (&sn)[2]) {
-    constexpr bool kPV = decltype(PV)::value, kNX = decltype(NX)::value;
-    const char* vst = vst0 + ((t - 1) & 1) * kVBytes;
-    u32x4 fr[16];
-    if (kPV) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) fr[i] = *(const u32x4*)(vst + v_off[i >> 2] + (i & 3) * 4096);
-    }
-    float psum = 0.0f;
-    float mp[4];
-    float mx = 0.0f;
-    Pipe pipe;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      if (kPV) {
-        if (i + 4 < 16) fr[i + 4] = *(const u32x4*)(vst + v_off[(i + 4) >> 2] + ((i + 4) & 3) * 4096);
-        const int u = i >> 2, db = i & 3;
-        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, fr[i]),
-                                                         __builtin_bit_cast(bf16x8, pp[u]), o[db], 0, 0, 0);
-      }
-      if (i < 10) exp_slot(t, sc[1], pc + 2, 1, i, pipe, psum);
-      if (kNX) {
-        if (i >= 6 && i < 10) mp[i - 6] = max_part(sn, i - 6);
-        if (i == 10) mx = halves_max(__builtin_fmaxf(__builtin_fmaxf(mp[0], mp[1]), __builtin_fmaxf(mp[2], mp[3])));
-        if (i == 11) {
-          l += psum;
-          psum = 0.0f;
-          q1 = update_max(mx);
-          l *= q1;
-        }
-      }
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    l += psum;
-  };
-
-  f32x16 sX[2], sY[2];
-  u32x4 pX[4], pY[4];
-  using Yes = std::integral_constant<bool, true>;
-  using No = std::integral_constant<bool, false>;
-
-  if (T > 0) {
-    // ---- prologue: K(0), K(1) in LDS; K(2), V(0) in the staging registers; S(0)
-    // and its running max ----
-    stage_load_k(r, 0);
-    store_k(r, 0);
-    stage_load_k(r, 1);
-    store_k(r, 1);
-    stage_load_k(r, 2);
-    stage_load_v(r, 0);
-    lds_barrier();
-    qk(0, sX);
-    lds_barrier();  // K(0) read by every wave before step 0 overwrites its stage
-    if (needs_mask(0)) mask(0, sX);
-    q1 = update_max(halves_max(__builtin_fmaxf(__builtin_fmaxf(max_part(sX, 0), max_part(sX, 1)),
-                                               __builtin_fmaxf(max_part(sX, 2), max_part(sX, 3)))));
-    l *= q1;
-
-    // ---- step t (tiles 0 .. T-2): S(t) in sc, S(t+1) to sn, P(t-1) in pp, P(t) to pc ----
-    auto step = [&](auto PV, int t, f32x16 (&sc)[2], f32x16 (&sn)[2], const u32x4 (&pp)[4], u32x4 (&pc)[4]) {
-      phase1(Yes{}, Yes{}, t, sc, sn, pc);
-      if (needs_mask(t + 1)) mask(t + 1, sn);
-      rescale(q0);  // O holds P.V up to tile t-2; P(t-1) is relative to the max of tile t-1
-      q0 = q1;
-      phase2(PV, Yes{}, t, sc, pp, pc, sn);
-      lds_barrier();
-    };
-    int t = 0;
-    if (T > 2) {
-      step(No{}, 0, sX, sY, pY, pX);
-      step(Yes{}, 1, sY, sX, pX, pY);
-      for (t = 2; t + 2 < T; t += 2) {
-        step(Yes{}, t, sX, sY, pY, pX);
-        step(Yes{}, t + 1, sY, sX, pX, pY);
-      }
-    }
-    // ---- the last tile t = T - 1: V(t) still sits in the staging registers ----
-    auto last = [&](auto PV, int t, const f32x16 (&sc)[2], const u32x4 (&pp)[4], u32x4 (&pc)[4]) {
-      store_v(r, t);
-      phase1(No{}, No{}, t, sc, sX, pc);
-      rescale(q0);
-      q0 = q1;
-      phase2(PV, No{}, t, sc, pp, pc, sc);
-      rescale(q0);
-      lds_barrier();  // V(t) from every thread
-      pv(t, pc);
-    };
-    if (t + 1 < T) {
-      if (t == 0)
-        step(No{}, t, sX, sY, pY, pX);
-      else
-        step(Yes{}, t, sX, sY, pY, pX);
-      last(Yes{}, t + 1, sY, pX, pY);
-    } else if (t == 0) {
-      last(No{}, t, sX, pY, pX);
-    } else {
-      last(Yes{}, t, sX, pY, pX);
-    }
-  }
-
-  // ---- finalize ----
-  const float l_tot = halves_sum(l);
   float inv;
   if (VARIANT == kPure)
     inv = l_tot > 0.0f ? 1.0f / l_tot : 1.0f;  // deltaFlashAttention.py:353-354
@@ -1805,87 +996,6 @@ static int allow_lds_pp(size_t bytes) {
   return DA_OK;
 }
 
-template <int V>
-static int allow_lds_iw(size_t bytes) {
-  static int done = 0;
-  if (!done) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_iw_kernel<V>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
-    if (e != hipSuccess) return set_error(DA_ERR_HIP, "hipFuncSetAttribute: %s", hipGetErrorString(e));
-    done = 1;
-  }
-  return DA_OK;
-}
-
-static int launch_attn_iw(int variant, AttnArgs& a, hipStream_t st) {
-  a.rows_per_wg = 32;
-  a.n_row_groups = (a.Nq + 31) / 32;
-  const size_t lds = kIWLds;
-  const unsigned grid = (unsigned)((int64_t)a.n_row_groups * a.units);
-  int rc = DA_OK;
-  switch (variant) {
-    case kHybrid: rc = allow_lds_iw<kHybrid>(lds); break;
-    case kSanity: rc = allow_lds_iw<kSanity>(lds); break;
-    case kPure: rc = allow_lds_iw<kPure>(lds); break;
-    default: rc = allow_lds_iw<kDense>(lds); break;
-  }
-  if (rc) return rc;
-  switch (variant) {
-    case kHybrid: hipLaunchKernelGGL(attn_iw_kernel<kHybrid>, dim3(grid), dim3(256), lds, st, a); break;
-    case kSanity: hipLaunchKernelGGL(attn_iw_kernel<kSanity>, dim3(grid), dim3(256), lds, st, a); break;
-    case kPure: hipLaunchKernelGGL(attn_iw_kernel<kPure>, dim3(grid), dim3(256), lds, st, a); break;
-    default: hipLaunchKernelGGL(attn_iw_kernel<kDense>, dim3(grid), dim3(256), lds, st, a); break;
-  }
-  return check_launch("attention kernel (intra-wave)");
-}
-
-template <int V>
-static int allow_lds_dma(size_t bytes) {
-  static int done = 0;
-  if (!done) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_dma_kernel<V>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
-    if (e != hipSuccess) return set_error(DA_ERR_HIP, "hipFuncSetAttribute: %s", hipGetErrorString(e));
-    done = 1;
-  }
-  return DA_OK;
-}
-
-static int launch_attn_dma(int variant, AttnArgs& a, hipStream_t st) {
-  a.rows_per_wg = 64;
-  a.n_row_groups = (a.Nq + 63) / 64;
-  const size_t lds = kDmaLds;
-  const unsigned grid = (unsigned)((int64_t)a.n_row_groups * a.units);
-  int rc = DA_OK;
-  switch (variant) {
-    case kHybrid: rc = allow_lds_dma<kHybrid>(lds); break;
-    case kSanity: rc = allow_lds_dma<kSanity>(lds); break;
-    case kPure: rc = allow_lds_dma<kPure>(lds); break;
-    default: rc = allow_lds_dma<kDense>(lds); break;
-  }
-  if (rc) return rc;
-  switch (variant) {
-    case kHybrid: hipLaunchKernelGGL(attn_dma_kernel<kHybrid>, dim3(grid), dim3(512), lds, st, a); break;
-    case kSanity: hipLaunchKernelGGL(attn_dma_kernel<kSanity>, dim3(grid), dim3(512), lds, st, a); break;
-    case kPure: hipLaunchKernelGGL(attn_dma_kernel<kPure>, dim3(grid), dim3(512), lds, st, a); break;
-    default: hipLaunchKernelGGL(attn_dma_kernel<kDense>, dim3(grid), dim3(512), lds, st, a); break;
-  }
-  return check_launch("attention kernel (ping-pong, direct LDS loads)");
-}
-
-// Kernel choice for GQA groups that are a multiple of 4: DELTAATTN_ATTN_KERNEL=pp|iw|dma
-// (default dma).  Other groups run attn_kernel.
-static int attn_kernel_choice() {
-  static int v = -1;
-  if (v < 0) {
-    const char* e = getenv("DELTAATTN_ATTN_KERNEL");
-    v = (e && strcmp(e, "pp") == 0) ? 0 : (e && strcmp(e, "iw") == 0) ? 1 : 2;
-  }
-  return v;
-}
-
-// GQA groups that are a multiple of 4 run the ping-pong kernel (64 rows x 4 heads per
-// workgroup of 8 waves) or the intra-wave kernel; other groups run attn_kernel.
 static int launch_attn_pp(int variant, AttnArgs& a, hipStream_t st) {
   a.rows_per_wg = 64;
   a.n_row_groups = (a.Nq + 63) / 64;
@@ -1919,13 +1029,7 @@ static int launch_attn(int variant, AttnArgs& a, hipStream_t st) {
     default: rc = allow_lds<kDense>(lds); break;
   }
   if (rc) return rc;
-  if (a.hpw == 4) {
-    switch (attn_kernel_choice()) {
-      case 0: return launch_attn_pp(variant, a, st);
-      case 1: return launch_attn_iw(variant, a, st);
-      default: return launch_attn_dma(variant, a, st);
-    }
-  }
+  if (a.hpw == 4) return launch_attn_pp(variant, a, st);
   switch (variant) {
     case kHybrid:
       hipLaunchKernelGGL(attn_kernel<kHybrid>, dim3(grid), dim3(256), lds, st, a);
