@@ -38,7 +38,9 @@ def parse_args():
     ap.add_argument("--seq", type=int, default=0, help="override the sequence length")
     ap.add_argument("--window", type=int, default=128)
     ap.add_argument("--seed", type=int, default=0)
-    ap.add_argument("--only", choices=("delta", "hybrid", "dense", "compress"), default=None)
+    ap.add_argument("--only", choices=("delta", "hybrid", "dense", "compress", "copy"), default=None,
+                    help="run one part for K steps (copy: a 1 GiB device copy, the reference for "
+                         "calibrating the FETCH_SIZE / WRITE_SIZE counters)")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-sample-blocks", type=int, default=24,
                     help="query blocks (all heads) the CPU baseline runs")
@@ -91,6 +93,20 @@ def cpu_baseline(q, k, v, tau, window, alg_total, sample_blocks):
                        f"({1e3 * t_compress:.0f} ms) + hybrid attention for {len(blocks)} of {nqb} "
                        f"query blocks x {Hq} heads ({t_sample:.1f} s), extrapolated by the "
                        f"algorithmic-FLOP ratio; BLAS threads={cores}, host {platform.processor() or platform.machine()}")}
+
+
+def traffic_bytes(args, N, r_real):
+    """HBM bytes per launch of the hybrid attention kernel, from the committed rocprofv3
+    FETCH_SIZE / WRITE_SIZE runs (profiles/attn_pp_hybrid_config1_traffic.txt); None for
+    a workload those runs do not cover."""
+    if args.config != 1 or N != 32768 or abs(r_real - 4.0) > 0.05 or args.window != 128:
+        return None
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic_config1.json")
+    try:
+        with open(path) as f:
+            return int(json.load(f)["bytes_per_launch"])
+    except (OSError, ValueError, KeyError):
+        return None
 
 
 def main():
@@ -151,8 +167,17 @@ def main():
         kk, _ = ops.select(k, tau, 512)
         ops.pack(kk, k, v, out=packed)
 
+    copy_src = copy_dst = None
+    if args.only == "copy":
+        copy_src = torch.ones(1 << 29, dtype=torch.int16, device=dev)  # 1 GiB
+        copy_dst = torch.empty_like(copy_src)
+
+    def copy_only():
+        copy_dst.copy_(copy_src)
+
     if args.only:
-        fn = {"delta": step, "hybrid": hybrid_only, "dense": dense_only, "compress": compress_only}[args.only]
+        fn = {"delta": step, "hybrid": hybrid_only, "dense": dense_only, "compress": compress_only,
+              "copy": copy_only}[args.only]
         for _ in range(args.warmup):
             fn()
         ms = time_loop(fn, args.steps)
@@ -214,8 +239,8 @@ def main():
         "realised_ratio": round(r_real, 3),
         "roofline": {"bound": "mfma", "achieved": round(hyb_tflops, 2), "peak": BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(hyb_tflops / BF16_PEAK_TFLOPS, 4),
-                     "traffic": None,
-                     "kernel": "attn_kernel<hybrid> (da_hybrid_prefill)",
+                     "traffic": traffic_bytes(args, N, r_real),
+                     "kernel": "attn_pp_kernel<hybrid> (da_hybrid_prefill)",
                      "algorithmic_flops": fl["algorithmic"]},
     }
     if not args.no_cpu_baseline:
