@@ -33,7 +33,15 @@ def parse_args():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=10)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", type=int, default=1, choices=(1, 2))
+    ap.add_argument("--config", type=int, default=1, choices=(1, 2, 3),
+                    help="1: one layer at 32K; 2: one layer at 128K; 3: full 32-layer "
+                         "Llama-3-8B prefill of 65536 tokens (tokens/s, attention share)")
+    ap.add_argument("--e2e-mode", choices=("periodic", "delta"), default="periodic",
+                    help="config 3 anchor selection: periodic with period r (the control "
+                         "mapping; random-init keys are nearly independent, so delta keeps "
+                         "almost everything) or delta with --tau")
+    ap.add_argument("--tau", type=float, default=15.0)
+    ap.add_argument("--e2e-layers", type=int, default=32)
     ap.add_argument("--ratio", type=float, default=4.0)
     ap.add_argument("--seq", type=int, default=0, help="override the sequence length")
     ap.add_argument("--window", type=int, default=128)
@@ -45,6 +53,10 @@ def parse_args():
     ap.add_argument("--cpu-sample-blocks", type=int, default=24,
                     help="query blocks (all heads) the CPU baseline runs")
     return ap.parse_args()
+
+
+def parse_args_defaults():
+    return {"steps": 10, "warmup": 3}
 
 
 def log(msg):
@@ -109,6 +121,72 @@ def traffic_bytes(args, N, r_real):
         return None
 
 
+def run_config3(args):
+    """Config 3: 32-layer Llama-3-8B prefill of one 65536-token sequence, random bf16
+    weights ~ N(0, 0.02), uniform token ids; PATH 1 (delta) and PATH 2 (dense) through
+    the same model (modeling swap, llama_swap).  Prints one JSON line."""
+    import torch
+    from deltaattention_amd import globVR, llama_swap
+    dev = torch.device("cuda:0")
+    N = args.seq or 65536
+    cfg = llama_swap.llama3_8b_config(llama_swap.DELTA, num_layers=args.e2e_layers)
+    log(f"config 3: {args.e2e_layers} layers, N={N}, building the model ...")
+    model = llama_swap.random_llama(cfg, dev, seed=args.seed)
+    g = torch.Generator().manual_seed(args.seed)
+    ids = torch.randint(0, cfg.vocab_size, (1, N), generator=g).to(dev)
+    if args.e2e_mode == "periodic":
+        globVR.packing_mode = "periodic"
+        globVR.target_keep_rate = 1.0 / args.ratio
+    else:
+        globVR.packing_mode = "delta"
+        globVR.row_delta_threshold = args.tau
+        globVR.chunk_size = 512
+    globVR.dense_window_size = args.window
+    res = {}
+    for name in (llama_swap.DELTA, llama_swap.DENSE):
+        llama_swap.set_implementation(model, name)
+        with torch.no_grad():
+            for _ in range(args.warmup):
+                model(ids, use_cache=False)
+            torch.cuda.synchronize()
+            times, att = [], []
+            for _ in range(args.steps):
+                llama_swap.reset_attention_time()
+                torch.cuda.synchronize()
+                t0 = time.perf_counter()
+                model(ids, use_cache=False)
+                torch.cuda.synchronize()
+                times.append(time.perf_counter() - t0)
+                att.append(llama_swap.attention_time_ms())
+        ms = 1e3 * sum(times) / len(times)
+        res[name] = (ms, sum(att) / len(att))
+        log(f"{name}: {ms:.1f} ms per prefill, attention {res[name][1]:.1f} ms")
+    ms_delta, att_delta = res[llama_swap.DELTA]
+    ms_dense, att_dense = res[llama_swap.DENSE]
+    rec = {
+        "metric": "prefill tokens/s, full Llama-3-8B (32 layers), delta attention",
+        "value": round(N / (ms_delta * 1e-3), 1),
+        "unit": "tokens/s",
+        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms_delta, 2), "higher_is_better": True, "scaling": "weak",
+        "vs_baseline": None, "dtype": "bf16",
+        "data": (f"synthetic: random bf16 weights N(0,0.02), {N} uniform token ids, seed "
+                 f"{args.seed}; anchors {args.e2e_mode} "
+                 + (f"period {args.ratio:g}" if args.e2e_mode == "periodic" else f"tau {args.tau:g}")
+                 + f", W={args.window}; logits over all positions"),
+        "config": {"workload": f"config3: {args.e2e_layers}-layer Llama-3-8B prefill, N={N}",
+                   "seq_len": N, "global_batch": 1, "parallelism": "none (1 GPU)"},
+        "attention_share_delta": round(att_delta / ms_delta, 4),
+        "attention_ms_delta": round(att_delta, 2),
+        "dense_tokens_per_s": round(N / (ms_dense * 1e-3), 1),
+        "dense_ms_per_step": round(ms_dense, 2),
+        "attention_share_dense": round(att_dense / ms_dense, 4),
+        "attention_ms_dense": round(att_dense, 2),
+        "speedup_vs_dense": round(ms_dense / ms_delta, 3),
+    }
+    print(json.dumps(rec), flush=True)
+
+
 def main():
     args = parse_args()
     if args.gpus != 1:
@@ -116,6 +194,13 @@ def main():
                                    "part of it (the path shards by KV head, see DESIGN.md)",
                           "n_gpus": args.gpus}))
         sys.exit(2)
+    if args.config == 3:
+        if args.steps == parse_args_defaults()["steps"]:
+            args.steps = 2
+        if args.warmup == parse_args_defaults()["warmup"]:
+            args.warmup = 1
+        run_config3(args)
+        return
     import numpy as np
     import torch
     from deltaattention_amd import metrics, ops, synth

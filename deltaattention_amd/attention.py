@@ -90,8 +90,12 @@ def keep_mask(key_states: torch.Tensor):
 def delta_prefill_attention(query_states: torch.Tensor, key_states: torch.Tensor,
                             value_states: torch.Tensor, layer_idx: int = 0,
                             past_key_value=None, scaling: Optional[float] = None,
-                            track_sparsity: bool = True) -> torch.Tensor:
-    """PATH 1 attention: q [B, Hq, N, D], post-RoPE k/v [B, Hkv, N, D] -> [B, Hq, N, D]."""
+                            track_sparsity: bool = True,
+                            out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """PATH 1 attention: q [B, Hq, N, D], post-RoPE k/v [B, Hkv, N, D] -> [B, Hq, N, D].
+
+    ``out``, if given, is a [B, Hq, N, D] view (any strides with a contiguous head dim)
+    the kernel writes into."""
     q_len = key_states.shape[2]
     ev = timing.start_event()
     keep, active = keep_mask(key_states)
@@ -114,7 +118,7 @@ def delta_prefill_attention(query_states: torch.Tensor, key_states: torch.Tensor
                              packed.v_packed, packed.timestamps, packed.counts, window=window,
                              scale=scaling, variant=variant,
                              no_count=variant != "sanity" and bool(getattr(globVR, "no_count", False)),
-                             num_packed_dev=packed.num_packed)
+                             num_packed_dev=packed.num_packed, out=out)
     timing.stop_event("time_delta_mm_pattern", ev)
     if past_key_value is not None and hasattr(past_key_value, "initialize_from_prefill"):
         p = packed.trimmed()                                        # :762-773
@@ -126,9 +130,10 @@ def delta_prefill_attention(query_states: torch.Tensor, key_states: torch.Tensor
     return out
 
 
-def dense_prefill_attention(query_states, key_states, value_states, scaling=None):
+def dense_prefill_attention(query_states, key_states, value_states, scaling=None, out=None):
     """PATH 2 (modeling_llama.py:778-803): dense causal flash prefill, GQA-native."""
     ev = timing.start_event()
-    out = ops.dense_prefill(query_states, key_states, value_states, causal=True, scale=scaling)
+    out = ops.dense_prefill(query_states, key_states, value_states, causal=True, scale=scaling,
+                            out=out)
     timing.stop_event("time_triton_flash_attention", ev)
     return out

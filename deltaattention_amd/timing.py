@@ -14,7 +14,8 @@ from . import globVR
 
 
 def enabled() -> bool:
-    return bool(getattr(globVR, "time_internal", False))
+    """Stage timing is on (globVR.time_internal) and there is a device to time on."""
+    return bool(getattr(globVR, "time_internal", False)) and torch.cuda.is_available()
 
 
 def start_event():

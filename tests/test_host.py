@@ -59,3 +59,23 @@ def test_synth_is_deterministic_and_ar1():
     assert abs(r - 0.9) < 0.03
     q, k, v = synth.make_layer_inputs(1, 4, 2, 256, 128, seed=1)
     assert q.dtype == torch.bfloat16 and k.shape == (1, 2, 256, 128) and q.shape == (1, 4, 256, 128)
+
+
+def test_llama_swap_routes_attention_to_this_build():
+    """The registered transformers attention implementations reach the native ops (on
+    CPU tensors those refuse with 'no CPU path': there is no fallback)."""
+    torch = pytest.importorskip("torch")
+    pytest.importorskip("transformers")
+    from transformers import AttentionInterface
+    from deltaattention_amd import llama_swap
+    llama_swap.register()
+    assert llama_swap.DELTA in AttentionInterface._global_mapping
+    assert llama_swap.DENSE in AttentionInterface._global_mapping
+    for impl in (llama_swap.DELTA, llama_swap.DENSE):
+        cfg = llama_swap.llama3_8b_config(impl, num_layers=1)
+        cfg.vocab_size, cfg.hidden_size, cfg.intermediate_size = 64, 256, 512
+        cfg.num_attention_heads, cfg.num_key_value_heads, cfg.head_dim = 2, 1, 128
+        model = llama_swap.random_llama(cfg, torch.device("cpu"))
+        with pytest.raises(ValueError, match="no CPU path"):
+            with torch.no_grad():
+                model(torch.zeros(1, 8, dtype=torch.long), use_cache=False)
