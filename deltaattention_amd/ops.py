@@ -232,7 +232,7 @@ def delta_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, threshold: 
                   chunk_size: int = 512, divide_to: int = 0, metric: str = "euclidean",
                   window: int = 128, scale: Optional[float] = None, variant: str = "hybrid",
                   no_count: bool = False, keep: Optional[torch.Tensor] = None,
-                  return_packed: bool = False):
+                  return_packed: bool = False, out: Optional[torch.Tensor] = None):
     """select -> pack -> hybrid prefill with P kept on the device (no host sync).
 
     Restates PATH 1 of LlamaAttention.forward (modeling_llama.py:600-749) for the delta
@@ -243,5 +243,59 @@ def delta_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, threshold: 
     packed = pack(keep, k, v)
     out = hybrid_prefill(q, k, v, packed.k_packed, packed.v_packed, packed.timestamps,
                          packed.counts, window=window, scale=scale, variant=variant,
-                         no_count=no_count, num_packed_dev=packed.num_packed)
+                         no_count=no_count, num_packed_dev=packed.num_packed, out=out)
     return (out, packed) if return_packed else out
+
+
+def _seq_bounds(cu_seqlens, total: int):
+    """Host list of (start, end) per sequence from cu_seqlens [B + 1]."""
+    if isinstance(cu_seqlens, torch.Tensor):
+        cu = cu_seqlens.detach().to("cpu", torch.int64).tolist()
+    else:
+        cu = [int(x) for x in cu_seqlens]
+    if len(cu) < 2 or cu[0] != 0 or cu[-1] != total or any(b < a for a, b in zip(cu, cu[1:])):
+        raise ValueError(f"cu_seqlens must rise from 0 to the token count {total}, got {cu}")
+    return list(zip(cu[:-1], cu[1:]))
+
+
+def _bhnd(x: torch.Tensor, s: int, e: int) -> torch.Tensor:
+    """[1, H, n, D] view of tokens s..e-1 of a [T, H, D] tensor (no copy)."""
+    return x[s:e].permute(1, 0, 2).unsqueeze(0)
+
+
+def delta_prefill_varlen(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqlens,
+                         threshold: float, chunk_size: int = 512, divide_to: int = 0,
+                         metric: str = "euclidean", window: int = 128,
+                         scale: Optional[float] = None, variant: str = "hybrid",
+                         no_count: bool = False) -> torch.Tensor:
+    """Delta prefill of a packed ragged batch: q [T, Hq, D], k, v [T, Hkv, D] with the
+    sequences at cu_seqlens (host values, length B + 1) -> out [T, Hq, D].
+
+    The reference has no varlen API; each sequence is exactly a B = 1 delta prefill
+    with its own chunking, anchors, P and schedule.  The sequences go through the same
+    kernels on the stream one after another, reading and writing the packed tensors in
+    place through strided views.
+    """
+    if q.dim() != 3 or k.dim() != 3 or v.dim() != 3:
+        raise ValueError("varlen tensors are [tokens, heads, head_dim]")
+    out = torch.empty_like(q)
+    for s, e in _seq_bounds(cu_seqlens, q.shape[0]):
+        if e == s:
+            continue
+        delta_prefill(_bhnd(q, s, e), _bhnd(k, s, e), _bhnd(v, s, e), threshold, chunk_size,
+                      divide_to, metric, window, scale, variant, no_count, out=_bhnd(out, s, e))
+    return out
+
+
+def dense_prefill_varlen(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqlens,
+                         causal: bool = True, scale: Optional[float] = None) -> torch.Tensor:
+    """Dense flash prefill of a packed ragged batch (the control of delta_prefill_varlen)."""
+    if q.dim() != 3 or k.dim() != 3 or v.dim() != 3:
+        raise ValueError("varlen tensors are [tokens, heads, head_dim]")
+    out = torch.empty_like(q)
+    for s, e in _seq_bounds(cu_seqlens, q.shape[0]):
+        if e == s:
+            continue
+        dense_prefill(_bhnd(q, s, e), _bhnd(k, s, e), _bhnd(v, s, e), causal, scale,
+                      out=_bhnd(out, s, e))
+    return out
