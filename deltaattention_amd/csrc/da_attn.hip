@@ -39,6 +39,7 @@
 // c = scale * log2(e) -- the same values as exp(s*scale - m*scale).  In Phase 1
 // p is multiplied by the anchor count in fp32 and then rounded to bf16 for the
 // P.V product while l accumulates the fp32 weights (deltaFlashAttention.py:86-98).
+#include <algorithm>
 #include <cstdlib>
 #include <cstring>
 #include <type_traits>
@@ -84,6 +85,11 @@ struct AttnArgs {
   int causal;
   const int32_t* sched;  // [B*Hkv][2][nblk_cap]: block maxima, prefix maxima
   int nblk_cap;
+  // prepared by the schedule kernel for attn_pp_kernel, [B*Hkv][wcap] each:
+  const float* wts;    // fp32 weight of packed row i (0 at and beyond P)
+  const int32_t* tsw;  // timestamp of packed row i, INT_MAX where the weight is 0
+  const float* ones;   // 64 weights of 1 (the exact tiles)
+  int wcap;            // nblk_cap * 128
   int hpw;          // query heads per workgroup (4, 2 or 1)
   int rows_per_wg;  // 32 * (4 / hpw)
   int n_row_groups;
@@ -615,8 +621,8 @@ void attn_pp_kernel(AttnArgs a) {
   const uint16_t* vp_base = a.vp + (int64_t)b * a.svp_b + (int64_t)g * a.svp_h;
   const uint16_t* k_base = a.k + (int64_t)b * a.sk_b + (int64_t)g * a.sk_h;
   const uint16_t* v_base = a.v + (int64_t)b * a.sv_b + (int64_t)g * a.sv_h;
-  const int32_t* ts_row = a.ts ? a.ts + (int64_t)b * a.sts_b + (int64_t)g * a.sts_h : nullptr;
-  const char* cnt_row = a.cnt ? (const char*)a.cnt + ((int64_t)b * a.scnt_b + (int64_t)g * a.scnt_h) * 4 : nullptr;
+  const float* w_row = a.wts ? a.wts + (int64_t)bg * a.wcap : nullptr;
+  const int32_t* tsw_row = a.tsw ? a.tsw + (int64_t)bg * a.wcap : nullptr;
   constexpr bool kPureV = VARIANT == kPure;
   constexpr bool kWeights = VARIANT == kHybrid || VARIANT == kPure;
 
@@ -662,22 +668,25 @@ void attn_pp_kernel(AttnArgs a) {
                                                rowt * snb + chunk * 16, 0, 0, 0);
     }
   };
-  // raw weights (and timestamps) of the tile's 64 keys, into slot t % 4 of their ring
+  // weights (and timestamps) of the tile's 64 keys, into slot t % 4 of their ring: a
+  // packed tile reads the prepared fp32 weights (0 for rows at and beyond P), an exact
+  // tile 64 ones, so the softmax multiplies every tile by its weights unconditionally
   auto meta_of = [&](int t) { return meta0 + (t & 3) * kPPMetaSlot; };
   auto dma_meta = [&](int t_raw) {
     if (!kWeights) return;
     const int t = min(t_raw, T - 1);
-    const int key0 = key0_of(t);
-    const int nrows = t < n1 ? max(0, min(P - key0, kTileN)) : 0;
+    const bool ph1 = t < n1;
+    const int key0 = ph1 ? t * kTileN : 0;
+    const int nrows = ph1 ? max(0, min(a.wcap - key0, kTileN)) : kTileN;
     char* dst = meta_of(t_raw) - kPPCnt;
     const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<void*>(uniform_ptr(cnt_row + (int64_t)key0 * 4)), (short)0,
+        const_cast<void*>(uniform_ptr(ph1 ? w_row + key0 : a.ones)), (short)0,
         __builtin_amdgcn_readfirstlane(nrows * 4), kBufferDword3);
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rc, (__attribute__((address_space(3))) void*)(dst + kPPCnt), 4,
                                              lane * 4, 0, 0, 0);
     if (kPureV) {
       const __amdgpu_buffer_rsrc_t rt = __builtin_amdgcn_make_buffer_rsrc(
-          const_cast<void*>(uniform_ptr(ts_row + key0)), (short)0, __builtin_amdgcn_readfirstlane(nrows * 4),
+          const_cast<void*>(uniform_ptr(tsw_row + key0)), (short)0, __builtin_amdgcn_readfirstlane(nrows * 4),
           kBufferDword3);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rt, (__attribute__((address_space(3))) void*)(dst + kPPTs), 4,
                                                lane * 4, 0, 0, 0);
@@ -687,22 +696,6 @@ void attn_pp_kernel(AttnArgs a) {
     dma_rows(true, tk);
     dma_rows(false, tv);
     if (wid_s == 0) dma_meta(tk);
-  };
-  // weights and timestamps of tile t in place: zero weight (and INT_MAX timestamp)
-  // for keys that are not packed keys of this tile, the count as fp32 otherwise
-  auto convert_meta = [&](int t) {
-    if (!kWeights) return;
-    char* ks = meta_of(t) - kPPCnt;
-    const int key = key0_of(t) + lane;
-    const bool valid = t < n1 && key < P;
-    const int raw = ((const int*)(ks + kPPCnt))[lane];
-    const float cv0 = a.cnt_is_float ? __int_as_float(raw) : (float)raw;
-    const float cv = valid ? (a.no_count ? 1.0f : cv0) : 0.0f;
-    ((float*)(ks + kPPCnt))[lane] = cv;
-    if (kPureV) {
-      const int tsv = ((const int*)(ks + kPPTs))[lane];
-      ((int*)(ks + kPPTs))[lane] = cv > 0.0f ? tsv : INT_MAX;
-    }
   };
 
   // ---- per-lane LDS offsets (stage-relative) ----
@@ -753,17 +746,13 @@ void attn_pp_kernel(AttnArgs a) {
   // V(k+1) at its start and waits at its end for those of window k - 1.  K(t) is read
   // in window t, V(t) in window t + 1 and the weights of tile t in windows t and t + 1;
   // the loads that overwrite stage t % 3 (ring slot t % 4) come in window t + 1 (t + 2,
-  // t + 2), after the barrier.  Wave 0 loads the weights and converts them in place at
-  // the end of the window after its own wait.
+  // t + 2), after the barrier.  Wave 0 loads the weights; the barrier after its wait
+  // publishes them.
   if (T > 0) {
     dma_rows(true, 0);
     if (wid_s == 0) dma_meta(0);
     dma_issue(1, 0);
     __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
-    if (wid_s == 0) {
-      convert_meta(0);
-      convert_meta(1);
-    }
     lds_barrier();
   }
 
@@ -839,6 +828,12 @@ void attn_pp_kernel(AttnArgs a) {
         // ---- softmax section for tile t ----
         const char* kst = meta_of(t) - kPPCnt;  // weights / timestamps at kPPCnt / kPPTs
         const int key0 = key0_of(t);
+        f32x4 w4[8];
+        if (kWeights) {
+          const float* cl = (const float*)(kst + kPPCnt);
+#pragma unroll
+          for (int j = 0; j < 8; ++j) w4[j] = *(const f32x4*)(cl + (j >> 2) * 32 + 8 * (j & 3) + 4 * hl);
+        }
         if (kPureV) {
           mask_pure(s, (const int*)(kst + kPPTs), row, hl);
         } else if (t >= n1) {
@@ -862,8 +857,6 @@ void attn_pp_kernel(AttnArgs a) {
           m_used = m_new;
         }
         const float neg = (m_used == -INFINITY) ? 0.0f : -m_used * c;
-        const bool weighted = kWeights && t < n1;
-        const float* cl = (const float*)(kst + kPPCnt);
         float psum = 0.0f;
 #pragma unroll
         for (int kb2 = 0; kb2 < 2; ++kb2) {
@@ -872,10 +865,9 @@ void attn_pp_kernel(AttnArgs a) {
             float p[4];
 #pragma unroll
             for (int e = 0; e < 4; ++e) p[e] = exp2_fast(__builtin_fmaf(s[kb2][4 * r4 + e], c, neg));
-            if (weighted) {
-              const f32x4 w4 = *(const f32x4*)(cl + kb2 * 32 + 8 * r4 + 4 * hl);
+            if (kWeights) {
 #pragma unroll
-              for (int e = 0; e < 4; ++e) p[e] *= w4[e];
+              for (int e = 0; e < 4; ++e) p[e] *= w4[4 * kb2 + r4][e];
             }
             psum += (p[0] + p[1]) + (p[2] + p[3]);
             pw[2 * kb2 + (r4 >> 1)][(r4 & 1) * 2 + 0] = pack_bf16x2(p[0], p[1]);
@@ -888,12 +880,10 @@ void attn_pp_kernel(AttnArgs a) {
     issue_once();
     if (sec & 1) {
       // the loads of window tl - 1 are done when at most this window's are pending
-      if (wid_s == 0) {
+      if (wid_s == 0)
         __builtin_amdgcn_s_waitcnt(vmcnt_only(4 + (kWeights ? 1 : 0) + (kPureV ? 1 : 0)));
-        if (tl >= 1) convert_meta(tl + 1);  // weights of tile tl + 1 (tiles 0, 1: prologue)
-      } else {
+      else
         __builtin_amdgcn_s_waitcnt(vmcnt_only(4));
-      }
       barrier_keep_loads();
     }
   }
@@ -922,12 +912,27 @@ void attn_pp_kernel(AttnArgs a) {
 
 // Per (batch, kv head): maxima of packed blocks of 128 timestamps (lanes at or
 // beyond P read seq_len_k + 1, deltaFlashAttention.py:70) and their prefix maxima.
+// Blocks with blockIdx.y = 0 do that; those with blockIdx.y = 1 + c (when wts is set)
+// write the fp32 weights of packed rows [1024 c, 1024 c + 1024) (the count, 1 with
+// no_count, 0 at and beyond P: modeling_llama.py:321-324 and the masked loads of
+// deltaFlashAttention.py:84-90), with tsw set the timestamps with INT_MAX where the
+// weight is 0, and block (0, 1) writes 64 ones.
+struct SchedPrep {
+  const void* cnt;
+  int64_t scnt_b, scnt_h;
+  int cnt_is_float, no_count;
+  float* wts;
+  int32_t* tsw;
+  float* ones;
+  int wcap;
+};
 __global__ __launch_bounds__(256) void hybrid_schedule_kernel(const int32_t* __restrict__ ts,
                                                               int64_t sts_b, int64_t sts_h,
                                                               int Hkv, int P_host,
                                                               const int32_t* P_dev, int Nk,
                                                               int nblk_cap,
-                                                              int32_t* __restrict__ sched) {
+                                                              int32_t* __restrict__ sched,
+                                                              SchedPrep prep) {
   __shared__ int32_t s_bmax[4096];
   __shared__ int32_t s_wave[4];
   const int tid = threadIdx.x, lane = tid & 63;
@@ -938,6 +943,28 @@ __global__ __launch_bounds__(256) void hybrid_schedule_kernel(const int32_t* __r
   if (P_dev) P = min(*P_dev, P_host);
   const int nblk = (P + kBlock - 1) / kBlock;
   const int32_t* row = ts + (int64_t)b * sts_b + (int64_t)g * sts_h;
+  if (blockIdx.y > 0) {
+    const int32_t* crow = (const int32_t*)prep.cnt + (int64_t)b * prep.scnt_b + (int64_t)g * prep.scnt_h;
+    float* wrow = prep.wts + (int64_t)bg * prep.wcap;
+    int32_t* trow = prep.tsw ? prep.tsw + (int64_t)bg * prep.wcap : nullptr;
+    const int i0 = (blockIdx.y - 1) * 1024 + tid;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int i = i0 + 256 * j;
+      if (i >= prep.wcap) break;
+      float w = 0.0f;
+      int tv = INT_MAX;
+      if (i < P) {
+        const int32_t raw = crow[i];
+        w = prep.no_count ? 1.0f : (prep.cnt_is_float ? __int_as_float(raw) : (float)raw);
+        if (trow && w > 0.0f) tv = row[i];
+      }
+      wrow[i] = w;
+      if (trow) trow[i] = tv;
+    }
+    if (bg == 0 && blockIdx.y == 1 && tid < kTileN) prep.ones[tid] = 1.0f;
+    return;
+  }
   for (int jb = wid; jb < nblk; jb += 4) {
     const int i0 = jb * kBlock + lane, i1 = i0 + 64;
     int m = max(i0 < P ? row[i0] : Nk + 1, i1 < P ? row[i1] : Nk + 1);
@@ -1084,9 +1111,29 @@ static int fill_common(AttnArgs& a, const void* q, const void* k, const void* v,
 
 using namespace da;
 
+// Workspace of da_hybrid_prefill: the schedule ([B*Hkv][2][nblk] int32), then, each at
+// a 256-byte boundary, the weights ([B*Hkv][wcap] fp32), the timestamps of the pure
+// Phase-1 variant ([B*Hkv][wcap] int32) and 64 ones; nblk = ceil(num_packed / 128)
+// (at least 1), wcap = 128 nblk.
+struct HybridWs {
+  int nblk, wcap;
+  int64_t w_off, ts_off, ones_off, total;
+};
+static int64_t round256(int64_t x) { return (x + 255) & ~(int64_t)255; }
+static HybridWs hybrid_ws(int64_t B, int64_t Hkv, int64_t num_packed) {
+  HybridWs w;
+  const int64_t nblk = std::max<int64_t>(1, (num_packed + kBlock - 1) / kBlock);
+  w.nblk = (int)nblk;
+  w.wcap = (int)(nblk * kBlock);
+  w.w_off = round256(B * Hkv * 2 * nblk * (int64_t)sizeof(int32_t));
+  w.ts_off = w.w_off + round256(B * Hkv * w.wcap * (int64_t)sizeof(float));
+  w.ones_off = w.ts_off + round256(B * Hkv * w.wcap * (int64_t)sizeof(int32_t));
+  w.total = w.ones_off + 256;
+  return w;
+}
+
 extern "C" int64_t da_hybrid_workspace_size(int64_t B, int64_t Hkv, int64_t num_packed) {
-  const int64_t nblk = (num_packed + kBlock - 1) / kBlock;
-  return B * Hkv * 2 * (nblk > 0 ? nblk : 1) * (int64_t)sizeof(int32_t);
+  return hybrid_ws(B, Hkv, num_packed).total;
 }
 
 extern "C" int da_hybrid_prefill(const void* q, const void* k, const void* v, const void* k_packed,
@@ -1129,16 +1176,34 @@ extern "C" int da_hybrid_prefill(const void* q, const void* k, const void* v, co
   a.no_count = no_count ? 1 : 0;
   a.cnt_is_float = counts_dtype == DA_F32;
   a.causal = 1;
-  a.nblk_cap = (int)((num_packed + kBlock - 1) / kBlock);
-  a.sched = (const int32_t*)workspace;
+  const HybridWs wl = hybrid_ws(B, Hkv, num_packed);
+  char* ws = (char*)workspace;
+  a.nblk_cap = wl.nblk;
+  a.sched = (const int32_t*)ws;
+  a.wcap = wl.wcap;
+  a.wts = (const float*)(ws + wl.w_off);
+  a.tsw = (const int32_t*)(ws + wl.ts_off);
+  a.ones = (const float*)(ws + wl.ones_off);
   hipStream_t st = (hipStream_t)stream;
-  if (variant != DA_VARIANT_PURE_PHASE1) {
-    hipLaunchKernelGGL(hybrid_schedule_kernel, dim3((unsigned)(B * Hkv)), dim3(256), 0, st,
-                       timestamps, a.sts_b, a.sts_h, (int)Hkv, (int)num_packed, num_packed_dev,
-                       (int)Nk, a.nblk_cap, (int32_t*)workspace);
-    rc = check_launch("da_hybrid_prefill(schedule)");
-    if (rc) return rc;
+  SchedPrep prep = {};
+  if (variant != DA_VARIANT_SANITY) {
+    prep.cnt = counts;
+    prep.scnt_b = a.scnt_b;
+    prep.scnt_h = a.scnt_h;
+    prep.cnt_is_float = a.cnt_is_float;
+    prep.no_count = a.no_count;
+    prep.wts = (float*)(ws + wl.w_off);
+    prep.tsw = variant == DA_VARIANT_PURE_PHASE1 ? (int32_t*)(ws + wl.ts_off) : nullptr;
+    prep.ones = (float*)(ws + wl.ones_off);
+    prep.wcap = wl.wcap;
   }
+  const unsigned prep_chunks = prep.wts ? (unsigned)((wl.wcap + 1023) / 1024) : 0u;
+  hipLaunchKernelGGL(hybrid_schedule_kernel, dim3((unsigned)(B * Hkv), 1 + prep_chunks), dim3(256), 0, st,
+                     timestamps,
+                     a.sts_b, a.sts_h, (int)Hkv, (int)num_packed, num_packed_dev, (int)Nk, a.nblk_cap,
+                     (int32_t*)ws, prep);
+  rc = check_launch("da_hybrid_prefill(schedule)");
+  if (rc) return rc;
   const int kv = variant == DA_VARIANT_HYBRID ? kHybrid : (variant == DA_VARIANT_SANITY ? kSanity : kPure);
   return launch_attn(kv, a, st);
 }

@@ -92,8 +92,19 @@ def test_attention_rejects_bad_shapes():
 
 def test_workspace_sizes():
     lib = _native.lib()
-    assert lib.da_hybrid_workspace_size(1, 8, 8192) == 8 * 2 * 64 * 4
-    assert lib.da_hybrid_workspace_size(2, 8, 1) == 2 * 8 * 2 * 1 * 4
+
+    def r256(x):
+        return (x + 255) // 256 * 256
+
+    def hybrid_ws(B, H, P):
+        nblk = max(1, (P + 127) // 128)
+        wcap = 128 * nblk
+        # schedule, fp32 weights, timestamps, 64 ones (each region 256-byte aligned)
+        return r256(B * H * 2 * nblk * 4) + 2 * r256(B * H * wcap * 4) + 256
+
+    assert lib.da_hybrid_workspace_size(1, 8, 8192) == hybrid_ws(1, 8, 8192)
+    assert lib.da_hybrid_workspace_size(2, 8, 1) == hybrid_ws(2, 8, 1)
+    assert lib.da_hybrid_workspace_size(1, 8, 8192) == 4096 + 2 * 8 * 8192 * 4 + 256
 
 
 def test_ops_refuse_cpu_tensors():
