@@ -86,9 +86,9 @@ struct AttnArgs {
   const int32_t* sched;  // [B*Hkv][2][nblk_cap]: block maxima, prefix maxima
   int nblk_cap;
   // prepared by the schedule kernel for attn_pp_kernel, [B*Hkv][wcap] each:
-  const float* wts;    // fp32 weight of packed row i (0 at and beyond P)
+  const float* wts;    // key bias log2(w_i) / scale_log2 of packed row i (-inf where w_i = 0)
   const int32_t* tsw;  // timestamp of packed row i, INT_MAX where the weight is 0
-  const float* ones;   // 64 weights of 1 (the exact tiles)
+  const float* zeros;  // 64 zero biases (the exact tiles)
   int wcap;            // nblk_cap * 128
   int hpw;          // query heads per workgroup (4, 2 or 1)
   int rows_per_wg;  // 32 * (4 / hpw)
@@ -359,6 +359,7 @@ void attn_kernel(AttnArgs a) {
       // S^T registers 8 * (r4 >> 1) .. +7 of block kb2.
       u32x4 pw[4];
       float psum = 0.0f;
+      const bf16x2 ones2 = {(__bf16)1.0f, (__bf16)1.0f};
       const bool weighted = (VARIANT == kPure) || (VARIANT == kHybrid && ph1);
       const float* cl = (const float*)(stage + kCntOff);
 #pragma unroll
@@ -373,9 +374,12 @@ void attn_kernel(AttnArgs a) {
             p[e] = exp2_fast(__builtin_fmaf(s[kb2][4 * r4 + e], c, neg));
             if (weighted) p[e] *= w4[e];
           }
-          psum += (p[0] + p[1]) + (p[2] + p[3]);
-          pw[2 * kb2 + (r4 >> 1)][(r4 & 1) * 2 + 0] = pack_bf16x2(p[0], p[1]);
-          pw[2 * kb2 + (r4 >> 1)][(r4 & 1) * 2 + 1] = pack_bf16x2(p[2], p[3]);
+          // the row sum adds the bf16 values the P.V MFMAs use
+          const uint32_t w01 = pack_bf16x2(p[0], p[1]), w23 = pack_bf16x2(p[2], p[3]);
+          pw[2 * kb2 + (r4 >> 1)][(r4 & 1) * 2 + 0] = w01;
+          pw[2 * kb2 + (r4 >> 1)][(r4 & 1) * 2 + 1] = w23;
+          psum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w01), ones2, psum, false);
+          psum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w23), ones2, psum, false);
         }
       }
       l_i = l_i * alpha + psum;
@@ -668,9 +672,9 @@ void attn_pp_kernel(AttnArgs a) {
                                                rowt * snb + chunk * 16, 0, 0, 0);
     }
   };
-  // weights (and timestamps) of the tile's 64 keys, into slot t % 4 of their ring: a
-  // packed tile reads the prepared fp32 weights (0 for rows at and beyond P), an exact
-  // tile 64 ones, so the softmax multiplies every tile by its weights unconditionally
+  // key biases (and timestamps) of the tile's 64 keys, into slot t % 4 of their ring: a
+  // packed tile reads the prepared biases (-inf for rows without weight, rows at and
+  // beyond P included), an exact tile 64 zeros; S^T starts at them
   auto meta_of = [&](int t) { return meta0 + (t & 3) * kPPMetaSlot; };
   auto dma_meta = [&](int t_raw) {
     if (!kWeights) return;
@@ -680,7 +684,7 @@ void attn_pp_kernel(AttnArgs a) {
     const int nrows = ph1 ? max(0, min(a.wcap - key0, kTileN)) : kTileN;
     char* dst = meta_of(t_raw) - kPPCnt;
     const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<void*>(uniform_ptr(ph1 ? w_row + key0 : a.ones)), (short)0,
+        const_cast<void*>(uniform_ptr(ph1 ? w_row + key0 : a.zeros)), (short)0,
         __builtin_amdgcn_readfirstlane(nrows * 4), kBufferDword3);
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rc, (__attribute__((address_space(3))) void*)(dst + kPPCnt), 4,
                                              lane * 4, 0, 0, 0);
@@ -776,6 +780,24 @@ void attn_pp_kernel(AttnArgs a) {
         // Raised issue priority: the matrix pipe is the bottleneck, the softmax wave on
         // the same SIMD takes the remaining issue slots.
         __builtin_amdgcn_s_setprio(1);
+        const bool do_qk = t < T && !skipped(t);
+        if (kWeights && do_qk) {
+          // S^T starts at the keys' bias log2(weight) / c (packed tiles; 0 for exact
+          // tiles, -inf for rows that carry no weight), so that exp2(c (s - m)) in the
+          // softmax is already the weighted probability.  Loaded before the P.V block
+          // (S is free by now), outside the Q.K block's read pipeline.
+          const float* lw = (const float*)meta_of(t) + 4 * hl;
+#pragma unroll
+          for (int kb2 = 0; kb2 < 2; ++kb2) {
+            const f32x4 b0 = *(const f32x4*)(lw + kb2 * 32);
+            const f32x4 b1 = *(const f32x4*)(lw + kb2 * 32 + 8);
+            const f32x4 b2 = *(const f32x4*)(lw + kb2 * 32 + 16);
+            const f32x4 b3 = *(const f32x4*)(lw + kb2 * 32 + 24);
+            s[kb2] = __builtin_shufflevector(__builtin_shufflevector(b0, b1, 0, 1, 2, 3, 4, 5, 6, 7),
+                                             __builtin_shufflevector(b2, b3, 0, 1, 2, 3, 4, 5, 6, 7),
+                                             0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15);
+          }
+        }
         if (t >= 1 && !skipped(t - 1)) {
           // The V^T operands come from transpose reads issued by hand (the compiler
           // would make each wait for every load to LDS in flight), four MFMAs ahead,
@@ -807,11 +829,13 @@ void attn_pp_kernel(AttnArgs a) {
           });
         }
         issue_once();
-        if (t < T && !skipped(t)) {
+        if (do_qk) {
           const char* kst = kst0 + (t % 3) * kKBytes;
+          if (!kWeights) {
+            s[0] = f32x16{};
+            s[1] = f32x16{};
+          }
           // the two key blocks alternate so that consecutive MFMAs do not depend on each other
-          s[0] = f32x16{};
-          s[1] = f32x16{};
 #pragma unroll
           for (int tt = 0; tt < kD / 16; ++tt) {
 #pragma unroll
@@ -826,24 +850,22 @@ void attn_pp_kernel(AttnArgs a) {
         __builtin_amdgcn_s_setprio(0);
       } else if (t < T && !skipped(t)) {
         // ---- softmax section for tile t ----
-        const char* kst = meta_of(t) - kPPCnt;  // weights / timestamps at kPPCnt / kPPTs
+        const char* kst = meta_of(t) - kPPCnt;  // timestamps at kPPTs
         const int key0 = key0_of(t);
-        f32x4 w4[8];
-        if (kWeights) {
-          const float* cl = (const float*)(kst + kPPCnt);
-#pragma unroll
-          for (int j = 0; j < 8; ++j) w4[j] = *(const f32x4*)(cl + (j >> 2) * 32 + 8 * (j & 3) + 4 * hl);
-        }
         if (kPureV) {
           mask_pure(s, (const int*)(kst + kPPTs), row, hl);
         } else if (t >= n1) {
           if ((a.causal && key0 + kTileN - 1 > r0w) || key0 + kTileN > a.Nk)
             mask_dense(s, key0, row, hl, a.Nk, a.causal);
         }
-        float mx = -INFINITY;
+        // two chains of three-input maxima
+        float ma = __builtin_fmaxf(s[0][0], s[1][0]), mb = __builtin_fmaxf(s[0][1], s[1][1]);
 #pragma unroll
-        for (int r = 0; r < 16; ++r) mx = __builtin_fmaxf(mx, __builtin_fmaxf(s[0][r], s[1][r]));
-        mx = halves_max(mx);
+        for (int r = 2; r < 16; r += 2) {
+          ma = __builtin_fmaxf(__builtin_fmaxf(ma, s[0][r]), s[1][r]);
+          mb = __builtin_fmaxf(__builtin_fmaxf(mb, s[0][r + 1]), s[1][r + 1]);
+        }
+        float mx = halves_max(__builtin_fmaxf(ma, mb));
         const bool upd = mx > m_used + lazy_thr;  // no NaN when m_used = -inf
         issue_once();
         if (__ballot(upd)) {
@@ -857,7 +879,10 @@ void attn_pp_kernel(AttnArgs a) {
           m_used = m_new;
         }
         const float neg = (m_used == -INFINITY) ? 0.0f : -m_used * c;
-        float psum = 0.0f;
+        // P in bf16 for the P.V MFMAs; the row sum adds the same bf16 values (two-term
+        // dot products with ones), so numerator and denominator see one rounding of p
+        float psa = 0.0f, psb = 0.0f;
+        const bf16x2 ones2 = {(__bf16)1.0f, (__bf16)1.0f};
 #pragma unroll
         for (int kb2 = 0; kb2 < 2; ++kb2) {
 #pragma unroll
@@ -865,16 +890,14 @@ void attn_pp_kernel(AttnArgs a) {
             float p[4];
 #pragma unroll
             for (int e = 0; e < 4; ++e) p[e] = exp2_fast(__builtin_fmaf(s[kb2][4 * r4 + e], c, neg));
-            if (kWeights) {
-#pragma unroll
-              for (int e = 0; e < 4; ++e) p[e] *= w4[4 * kb2 + r4][e];
-            }
-            psum += (p[0] + p[1]) + (p[2] + p[3]);
-            pw[2 * kb2 + (r4 >> 1)][(r4 & 1) * 2 + 0] = pack_bf16x2(p[0], p[1]);
-            pw[2 * kb2 + (r4 >> 1)][(r4 & 1) * 2 + 1] = pack_bf16x2(p[2], p[3]);
+            const uint32_t w01 = pack_bf16x2(p[0], p[1]), w23 = pack_bf16x2(p[2], p[3]);
+            pw[2 * kb2 + (r4 >> 1)][(r4 & 1) * 2 + 0] = w01;
+            pw[2 * kb2 + (r4 >> 1)][(r4 & 1) * 2 + 1] = w23;
+            psa = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w01), ones2, psa, false);
+            psb = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w23), ones2, psb, false);
           }
         }
-        l_i += psum;
+        l_i += psa + psb;
       }
     }
     issue_once();
@@ -913,17 +936,20 @@ void attn_pp_kernel(AttnArgs a) {
 // Per (batch, kv head): maxima of packed blocks of 128 timestamps (lanes at or
 // beyond P read seq_len_k + 1, deltaFlashAttention.py:70) and their prefix maxima.
 // Blocks with blockIdx.y = 0 do that; those with blockIdx.y = 1 + c (when wts is set)
-// write the fp32 weights of packed rows [1024 c, 1024 c + 1024) (the count, 1 with
-// no_count, 0 at and beyond P: modeling_llama.py:321-324 and the masked loads of
-// deltaFlashAttention.py:84-90), with tsw set the timestamps with INT_MAX where the
-// weight is 0, and block (0, 1) writes 64 ones.
+// write, for packed rows [1024 c, 1024 c + 1024), the key bias log2(w) / scale_log2 of
+// the row's weight w (the count, 1 with no_count, 0 at and beyond P:
+// modeling_llama.py:321-324 and the masked loads of deltaFlashAttention.py:84-90; -inf
+// for w = 0), so that exp2(scale_log2 (q.k + bias) - m) = w exp2(scale_log2 q.k - m);
+// with tsw set the timestamps with INT_MAX where the weight is 0; block (0, 1) writes
+// 64 zero biases.
 struct SchedPrep {
   const void* cnt;
   int64_t scnt_b, scnt_h;
   int cnt_is_float, no_count;
+  float scale_log2;
   float* wts;
   int32_t* tsw;
-  float* ones;
+  float* zeros;
   int wcap;
 };
 __global__ __launch_bounds__(256) void hybrid_schedule_kernel(const int32_t* __restrict__ ts,
@@ -959,10 +985,10 @@ __global__ __launch_bounds__(256) void hybrid_schedule_kernel(const int32_t* __r
         w = prep.no_count ? 1.0f : (prep.cnt_is_float ? __int_as_float(raw) : (float)raw);
         if (trow && w > 0.0f) tv = row[i];
       }
-      wrow[i] = w;
+      wrow[i] = w > 0.0f ? log2f(w) / prep.scale_log2 : -INFINITY;
       if (trow) trow[i] = tv;
     }
-    if (bg == 0 && blockIdx.y == 1 && tid < kTileN) prep.ones[tid] = 1.0f;
+    if (bg == 0 && blockIdx.y == 1 && tid < kTileN) prep.zeros[tid] = 0.0f;
     return;
   }
   for (int jb = wid; jb < nblk; jb += 4) {
@@ -1112,12 +1138,12 @@ static int fill_common(AttnArgs& a, const void* q, const void* k, const void* v,
 using namespace da;
 
 // Workspace of da_hybrid_prefill: the schedule ([B*Hkv][2][nblk] int32), then, each at
-// a 256-byte boundary, the weights ([B*Hkv][wcap] fp32), the timestamps of the pure
-// Phase-1 variant ([B*Hkv][wcap] int32) and 64 ones; nblk = ceil(num_packed / 128)
+// a 256-byte boundary, the key biases ([B*Hkv][wcap] fp32), the timestamps of the pure
+// Phase-1 variant ([B*Hkv][wcap] int32) and 64 zeros; nblk = ceil(num_packed / 128)
 // (at least 1), wcap = 128 nblk.
 struct HybridWs {
   int nblk, wcap;
-  int64_t w_off, ts_off, ones_off, total;
+  int64_t w_off, ts_off, zeros_off, total;
 };
 static int64_t round256(int64_t x) { return (x + 255) & ~(int64_t)255; }
 static HybridWs hybrid_ws(int64_t B, int64_t Hkv, int64_t num_packed) {
@@ -1127,8 +1153,8 @@ static HybridWs hybrid_ws(int64_t B, int64_t Hkv, int64_t num_packed) {
   w.wcap = (int)(nblk * kBlock);
   w.w_off = round256(B * Hkv * 2 * nblk * (int64_t)sizeof(int32_t));
   w.ts_off = w.w_off + round256(B * Hkv * w.wcap * (int64_t)sizeof(float));
-  w.ones_off = w.ts_off + round256(B * Hkv * w.wcap * (int64_t)sizeof(int32_t));
-  w.total = w.ones_off + 256;
+  w.zeros_off = w.ts_off + round256(B * Hkv * w.wcap * (int64_t)sizeof(int32_t));
+  w.total = w.zeros_off + 256;
   return w;
 }
 
@@ -1183,7 +1209,7 @@ extern "C" int da_hybrid_prefill(const void* q, const void* k, const void* v, co
   a.wcap = wl.wcap;
   a.wts = (const float*)(ws + wl.w_off);
   a.tsw = (const int32_t*)(ws + wl.ts_off);
-  a.ones = (const float*)(ws + wl.ones_off);
+  a.zeros = (const float*)(ws + wl.zeros_off);
   hipStream_t st = (hipStream_t)stream;
   SchedPrep prep = {};
   if (variant != DA_VARIANT_SANITY) {
@@ -1192,9 +1218,10 @@ extern "C" int da_hybrid_prefill(const void* q, const void* k, const void* v, co
     prep.scnt_h = a.scnt_h;
     prep.cnt_is_float = a.cnt_is_float;
     prep.no_count = a.no_count;
+    prep.scale_log2 = a.scale_log2;
     prep.wts = (float*)(ws + wl.w_off);
     prep.tsw = variant == DA_VARIANT_PURE_PHASE1 ? (int32_t*)(ws + wl.ts_off) : nullptr;
-    prep.ones = (float*)(ws + wl.ones_off);
+    prep.zeros = (float*)(ws + wl.zeros_off);
     prep.wcap = wl.wcap;
   }
   const unsigned prep_chunks = prep.wts ? (unsigned)((wl.wcap + 1023) / 1024) : 0u;

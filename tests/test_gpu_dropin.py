@@ -107,7 +107,11 @@ def test_hybrid_kernel_objects_on_expanded_inputs(gpu, variant):
                      BLOCK_M=128, BLOCK_N=128, BLOCK_D=128, num_warps=8, num_stages=1)
     native = ops.hybrid_prefill(qg, kg, vg, pk.k_packed, pk.v_packed, pk.timestamps, pk.counts,
                                 window=128, variant=variant)
-    assert torch.allclose(out.float(), native.float(), atol=1e-2, rtol=0)
+    # The expanded inputs run the per-head kernel (exact running max, weights multiplied
+    # after exp2), the GQA-native call the grouped kernel (lazy running max, weights as
+    # key biases): P is rounded to bf16 at different reference points, so the two agree
+    # to that rounding -- the bar the oracle applies to each of them.
+    _close(out.float().cpu().numpy(), native.float().cpu().numpy(), f"{variant} object vs native")
     kf, vf = k.float().numpy(), v.float().numpy()
     p = O.pack(kf, vf, keep.cpu().numpy())
     ref = O.hybrid_attention(q.float().numpy(), kf, vf, p["k_packed"], p["v_packed"],
