@@ -764,9 +764,11 @@ void attn_pp_kernel(AttnArgs a) {
   for (int sec = 0; sec < nsec; ++sec) {
     const int tl = sec >> 1;
     const int sw = sec - grp;
-    // window tl loads K(tl + 2) and V(tl + 1) in its first section, in the middle of
-    // the section's work so that the loads of the eight waves do not queue up together
-    bool issued = (sec & 1) != 0;
+    // window tl loads K(tl + 2) and V(tl + 1), group A in its matrix section (between
+    // its P.V and Q.K blocks).  Group B issues them in its softmax section in the
+    // variants with packed tiles and in its matrix section in the dense one (the faster
+    // placement of each, measured).
+    bool issued = (sec & 1) != (VARIANT == kDense ? grp : 0);
     auto issue_once = [&]() {
       if (!issued) {
         dma_issue(tl + 2, tl + 1);
@@ -867,7 +869,7 @@ void attn_pp_kernel(AttnArgs a) {
         }
         float mx = halves_max(__builtin_fmaxf(ma, mb));
         const bool upd = mx > m_used + lazy_thr;  // no NaN when m_used = -inf
-        issue_once();
+        if (VARIANT != kDense) issue_once();
         if (__ballot(upd)) {
           const float m_new = upd ? mx : m_used;
           const float alpha = exp2_fast((m_used - m_new) * c);
