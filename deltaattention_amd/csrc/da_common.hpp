@@ -93,6 +93,22 @@ __device__ __forceinline__ float wave_tree_sum(float t) {
   return (r0 + r1) + (r2 + r3);
 }
 
+// The same tree, with the sum in every lane: after the four DPP levels every 16-lane
+// row holds its row sum; v_permlane16_swap pairs rows 0/1 and 2/3, v_permlane32_swap
+// the two halves, so every lane computes (r0 + r1) + (r2 + r3) (additions commute
+// bit-exactly).  No scalar round trip.
+__device__ __forceinline__ float wave_tree_sum_all(float t) {
+#pragma clang fp contract(off)
+  t = t + dpp_f32<kDppXor1>(t);
+  t = t + dpp_f32<kDppXor2>(t);
+  t = t + dpp_f32<kDppHalfMirror>(t);
+  t = t + dpp_f32<kDppMirror>(t);
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(t), __float_as_uint(t), false, false);
+  const float u = __uint_as_float(r[0]) + __uint_as_float(r[1]);
+  const auto q = __builtin_amdgcn_permlane32_swap(__float_as_uint(u), __float_as_uint(u), false, false);
+  return __uint_as_float(q[0]) + __uint_as_float(q[1]);
+}
+
 // x0*y0 + x1*y1 with both products rounded (no fused multiply-add).
 __device__ __forceinline__ float pair_dot(float x0, float x1, float y0, float y1) {
 #pragma clang fp contract(off)

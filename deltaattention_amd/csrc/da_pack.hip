@@ -5,8 +5,9 @@
 // (tritonModules.py:72-132, launch modeling_llama.py:658-680) and the run-length
 // scatter_add_ (modeling_llama.py:682-685).
 //
-// pack_scan_kernel (one workgroup per (batch, kv head)): the keep mask is read in
-// 64-row groups; a ballot gives each group's anchor count and first anchor.  A
+// pack_scan_kernel (one 1024-thread workgroup per (batch, kv head)): the keep mask is
+// read in 64-row groups, 32 groups per wave at once; a ballot gives each group's
+// anchor count and first anchor.  A
 // block-wide exclusive scan gives every group's first packed index and a suffix
 // minimum gives the first anchor after each group, which ends the run of the
 // group's last anchor.  The head's anchor count c goes to anchor_counts.
@@ -48,32 +49,44 @@ __device__ __forceinline__ int wave_reduce_max(int v) {
   return v;
 }
 
-__global__ __launch_bounds__(256) void pack_scan_kernel(const int32_t* __restrict__ keep,
-                                                        int64_t N, int ngroups,
-                                                        int32_t* __restrict__ ws_off,
-                                                        int32_t* __restrict__ ws_next,
-                                                        int32_t* __restrict__ anchor_counts) {
+constexpr int kScanThreads = 1024;
+constexpr int kScanWaves = kScanThreads / 64;
+constexpr int kScanUnroll = 32;  // groups per wave per pass: that many loads in flight
+
+__global__ __launch_bounds__(kScanThreads) void pack_scan_kernel(const int32_t* __restrict__ keep,
+                                                                 int64_t N, int ngroups,
+                                                                 int32_t* __restrict__ ws_off,
+                                                                 int32_t* __restrict__ ws_next,
+                                                                 int32_t* __restrict__ anchor_counts) {
   __shared__ int32_t s_info[kMaxGroups];  // count | first << 8
-  __shared__ int32_t s_wave[4];
-  __shared__ int32_t s_suffix[256];
+  __shared__ int32_t s_wave[kScanWaves];
+  __shared__ int32_t s_suffix[kScanThreads];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int64_t bh = blockIdx.x;
   const int32_t* krow = keep + bh * N;
 
-  for (int g = wid; g < ngroups; g += 4) {
-    const int64_t r = (int64_t)g * 64 + lane;
-    const bool kp = r < N && krow[r] != 0;
-    const uint64_t bits = __ballot(kp);
-    if (lane == 0) {
-      const int cnt = __popcll(bits);
-      const int first = bits ? __builtin_ctzll(bits) : 64;
-      s_info[g] = cnt | (first << 8);
+  // wave w takes groups 32w .. 32w + 31 of every 32 * kScanWaves
+  for (int gb = wid * kScanUnroll; gb < ngroups; gb += kScanWaves * kScanUnroll) {
+    bool kp[kScanUnroll];
+#pragma unroll
+    for (int j = 0; j < kScanUnroll; ++j) {
+      const int64_t r = (int64_t)(gb + j) * 64 + lane;
+      kp[j] = gb + j < ngroups && r < N && krow[r] != 0;
+    }
+#pragma unroll
+    for (int j = 0; j < kScanUnroll; ++j) {
+      const uint64_t bits = __ballot(kp[j]);
+      if (lane == 0 && gb + j < ngroups) {
+        const int cnt = __popcll(bits);
+        const int first = bits ? __builtin_ctzll(bits) : 64;
+        s_info[gb + j] = cnt | (first << 8);
+      }
     }
   }
   __syncthreads();
 
   // Each thread owns a contiguous slice of groups.
-  const int per = (ngroups + 255) / 256;
+  const int per = (ngroups + kScanThreads - 1) / kScanThreads;
   const int g0 = min(tid * per, ngroups), g1 = min(g0 + per, ngroups);
   int sum = 0;
   int first_pos = (int)N;  // first anchor inside the slice (N if none)
@@ -86,25 +99,27 @@ __global__ __launch_bounds__(256) void pack_scan_kernel(const int32_t* __restric
   int incl = wave_incl_scan_add(sum, lane);
   if (lane == 63) s_wave[wid] = incl;
   __syncthreads();
-  int wave_prefix = 0;
-  for (int w2 = 0; w2 < wid; ++w2) wave_prefix += s_wave[w2];
-  const int total = s_wave[0] + s_wave[1] + s_wave[2] + s_wave[3];
+  int wave_prefix = 0, total = 0;
+  for (int w2 = 0; w2 < kScanWaves; ++w2) {
+    if (w2 < wid) wave_prefix += s_wave[w2];
+    total += s_wave[w2];
+  }
   int run = wave_prefix + incl - sum;
   __syncthreads();
   // suffix minimum of first_pos over later slices: scan the reversed sequence
   s_suffix[tid] = first_pos;
   __syncthreads();
-  const int rv = s_suffix[255 - tid];
+  const int rv = s_suffix[kScanThreads - 1 - tid];
   int rincl = wave_incl_scan_min(rv, lane);
   if (lane == 63) s_wave[wid] = rincl;
   __syncthreads();
   int rpre = (int)N;
   for (int w2 = 0; w2 < wid; ++w2) rpre = min(rpre, s_wave[w2]);
-  rincl = min(rincl, rpre);  // min over original slices [255 - tid, 255]
+  rincl = min(rincl, rpre);  // min over original slices [kScanThreads - 1 - tid, end)
   __syncthreads();
-  s_suffix[255 - tid] = rincl;
+  s_suffix[kScanThreads - 1 - tid] = rincl;
   __syncthreads();
-  int nxt = (tid < 255) ? s_suffix[tid + 1] : (int)N;
+  int nxt = (tid < kScanThreads - 1) ? s_suffix[tid + 1] : (int)N;
 
   int32_t* off_row = ws_off + bh * ngroups;
   int32_t* next_row = ws_next + bh * ngroups;
@@ -243,7 +258,7 @@ extern "C" int da_pack(const int32_t* keep, const void* k, const void* v, int dt
   hipStream_t st = (hipStream_t)stream;
   int32_t* ws_off = (int32_t*)workspace;
   int32_t* ws_next = ws_off + B * Hkv * ngroups;
-  hipLaunchKernelGGL(pack_scan_kernel, dim3((unsigned)(B * Hkv)), dim3(256), 0, st, keep, N,
+  hipLaunchKernelGGL(pack_scan_kernel, dim3((unsigned)(B * Hkv)), dim3(kScanThreads), 0, st, keep, N,
                      (int)ngroups, ws_off, ws_next, anchor_counts);
   int rc = check_launch("da_pack(scan)");
   if (rc) return rc;

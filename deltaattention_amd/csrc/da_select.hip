@@ -15,19 +15,39 @@
 // to the CPU restatement of the same tree.
 //
 // Rows are prefetched 32 at a time one batch ahead, since loads never depend on
-// the decisions.  Keep decisions collect in a 64-bit scalar mask and are stored as
-// int32 (the reference's keep-mask format) 64 rows at a time.
+// the decisions.  The distance reaches every lane through v_permlane16/32_swap (no
+// scalar round trip), the anchor update is a select, and a batch's decisions collect
+// in a 32-bit mask stored as int32 (the reference's keep-mask format).
 #include "da_common.hpp"
 
 namespace da {
 
-__device__ __forceinline__ void store_keep_bits(int32_t* keep_row, int64_t base, int64_t end,
-                                                uint64_t bits, int lane) {
-  const int64_t r = base + lane;
-  if (r < end) keep_row[r] = (int32_t)((bits >> lane) & 1ull);
-}
-
 constexpr int kSelBatch = 32;
+
+// One key of the walk: the decision and the anchor update without a branch (the
+// decision is the same in every lane).
+template <bool COS>
+__device__ __forceinline__ bool select_step(uint32_t xb, float& a0, float& a1, float& a_norm,
+                                            float thr) {
+#pragma clang fp contract(off)
+  const float x0 = bf16_lo(xb), x1 = bf16_hi(xb);
+  const float eps = 1e-8f;
+  bool kp;
+  float x_norm = 0.0f;
+  if (COS) {  // tritonModules.py:48-54
+    const float dot = wave_tree_sum_all(pair_dot(x0, x1, a0, a1));
+    x_norm = __fsqrt_rn(wave_tree_sum_all(pair_dot(x0, x1, x0, x1)) + eps);
+    const float sim = __fdiv_rn(dot, x_norm * a_norm);
+    kp = sim < thr;
+  } else {  // tritonModules.py:55-58
+    const float d0 = x0 - a0, d1 = x1 - a1;
+    kp = wave_tree_sum_all(pair_dot(d0, d1, d0, d1)) > thr;
+  }
+  a0 = kp ? x0 : a0;  // tritonModules.py:60-63
+  a1 = kp ? x1 : a1;
+  if (COS) a_norm = kp ? x_norm : a_norm;
+  return kp;
+}
 
 template <bool COS>
 __global__ __launch_bounds__(256) void select_kernel(
@@ -41,74 +61,50 @@ __global__ __launch_bounds__(256) void select_kernel(
   const int64_t bh = w / nc;
   const int64_t c = w - bh * nc;
   const int64_t b = bh / H, h = bh - (bh / H) * H;
-  const int64_t s = c * cs;
-  if (s >= N) {  // tritonModules.py:34-35 (count stays 0, modeling_llama.py:637)
+  if (c * cs >= N) {  // tritonModules.py:34-35 (count stays 0, modeling_llama.py:637)
     if (lane == 0) chunk_counts[w] = 0;
     return;
   }
-  const int64_t e = (s + cs < N) ? s + cs : N;
+  // rows are 32-bit from here on (N < 2^31)
+  const int s = (int)(c * cs);
+  const int e = (int)((c * cs + cs < N) ? c * cs + cs : N);
   const uint16_t* base = k + b * sk_b + h * sk_h + 2 * lane;
   const bool active = 2 * lane < D;
   int32_t* keep_row = keep + bh * N;
+  auto row_bits = [&](int r) -> uint32_t {
+    return (active && r < e) ? *(const uint32_t*)(base + (int64_t)r * sk_n) : 0u;
+  };
 
-  const uint32_t a_bits = active ? *(const uint32_t*)(base + s * sk_n) : 0u;
+  const uint32_t a_bits = row_bits(s);
   float a0 = bf16_lo(a_bits), a1 = bf16_hi(a_bits);
-  const float eps = 1e-8f;
   float a_norm = 0.0f;
-  if (COS) a_norm = __fsqrt_rn(wave_tree_sum(pair_dot(a0, a1, a0, a1)) + eps);
-
+  if (COS) a_norm = __fsqrt_rn(wave_tree_sum_all(pair_dot(a0, a1, a0, a1)) + 1e-8f);
+  if (lane == 0) keep_row[s] = 1;  // row s is an anchor (tritonModules.py:41)
   int count = 1;
-  uint64_t bits = 1ull;  // row s is an anchor (tritonModules.py:41)
-  int64_t wbase = s;
 
+  // Rows s + 1 .. e - 1 in batches of 32, each loaded one batch ahead (the loads never
+  // depend on the decisions); a batch's 32 decisions are stored by lanes 0..31.
   uint32_t cur[kSelBatch], nxt[kSelBatch];
 #pragma unroll
-  for (int j = 0; j < kSelBatch; ++j) {
-    const int64_t r = s + 1 + j;
-    cur[j] = (active && r < e) ? *(const uint32_t*)(base + r * sk_n) : 0u;
-  }
-  for (int64_t i0 = s + 1; i0 < e; i0 += kSelBatch) {
-    const int64_t n0 = i0 + kSelBatch;
+  for (int j = 0; j < kSelBatch; ++j) cur[j] = row_bits(s + 1 + j);
+  for (int i0 = s + 1; i0 < e; i0 += kSelBatch) {
 #pragma unroll
-    for (int j = 0; j < kSelBatch; ++j) {
-      const int64_t r = n0 + j;
-      nxt[j] = (active && r < e) ? *(const uint32_t*)(base + r * sk_n) : 0u;
-    }
+    for (int j = 0; j < kSelBatch; ++j) nxt[j] = row_bits(i0 + kSelBatch + j);
+    uint32_t bb = 0;
+    if (i0 + kSelBatch <= e) {
 #pragma unroll
-    for (int j = 0; j < kSelBatch; ++j) {
-      const int64_t i = i0 + j;
-      if (i < e) {
-        const float x0 = bf16_lo(cur[j]), x1 = bf16_hi(cur[j]);
-        bool kp;
-        float x_norm = 0.0f;
-        if (COS) {  // tritonModules.py:48-54
-          const float dot = wave_tree_sum(pair_dot(x0, x1, a0, a1));
-          x_norm = __fsqrt_rn(wave_tree_sum(pair_dot(x0, x1, x0, x1)) + eps);
-          const float sim = __fdiv_rn(dot, x_norm * a_norm);
-          kp = sim < thr;
-        } else {  // tritonModules.py:55-58
-          const float d0 = x0 - a0, d1 = x1 - a1;
-          kp = wave_tree_sum(pair_dot(d0, d1, d0, d1)) > thr;
-        }
-        if (kp) {  // tritonModules.py:60-63
-          a0 = x0;
-          a1 = x1;
-          if (COS) a_norm = x_norm;
-          ++count;
-        }
-        const int64_t off = i - wbase;
-        if (off == 64) {
-          store_keep_bits(keep_row, wbase, e, bits, lane);
-          wbase += 64;
-          bits = 0ull;
-        }
-        bits |= (uint64_t)kp << (i - wbase);
-      }
+      for (int j = 0; j < kSelBatch; ++j)
+        bb |= (uint32_t)select_step<COS>(cur[j], a0, a1, a_norm, thr) << j;
+    } else {
+#pragma unroll
+      for (int j = 0; j < kSelBatch; ++j)
+        if (i0 + j < e) bb |= (uint32_t)select_step<COS>(cur[j], a0, a1, a_norm, thr) << j;
     }
+    count += __builtin_popcount(bb);  // tritonModules.py:68
+    if (lane < kSelBatch && i0 + lane < e) keep_row[i0 + lane] = (int32_t)((bb >> lane) & 1u);
 #pragma unroll
     for (int j = 0; j < kSelBatch; ++j) cur[j] = nxt[j];
   }
-  store_keep_bits(keep_row, wbase, e, bits, lane);
   if (lane == 0) chunk_counts[w] = count;  // tritonModules.py:68-69
 }
 
