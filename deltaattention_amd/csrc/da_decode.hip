@@ -12,9 +12,9 @@
 // (deltaDecoding.py:236-362).  The key list of a kv head is its packed anchors
 // [0, length) followed by the ring slots [0, exact_len).  Packed scores get
 // + log(count) (so a count-c anchor weighs like c equal keys, and padding with count 0
-// gets no weight); ring scores are unmasked.  The list is cut into slices of 256 keys;
-// one workgroup scores a slice for all query heads of the group (the key and value
-// rows are read once per group), keeps the slice's max / sum / P.V partials, and the
+// gets no weight); ring scores are unmasked.  The list is cut into slices of 64 keys;
+// one wave scores a slice for all query heads of the group (the key and value rows
+// are read once per group), keeps the slice's max / sum / P.V partials, and the
 // combine kernel merges the slices exactly (rescaling by exp(m_s - M)).  As in the
 // reference, P is rounded to bf16 before the P.V product while the row sum stays fp32.
 #include "da_common.hpp"
@@ -98,7 +98,7 @@ __global__ __launch_bounds__(256) void decode_update_kernel(DecodeUpdateArgs a) 
   }
 }
 
-constexpr int kDecSlice = 256;
+constexpr int kDecSlice = 64;
 constexpr int kDecMaxG = 8;
 constexpr int kDecD = 128;
 
@@ -124,49 +124,48 @@ struct DecodeAttnArgs {
   int B, Hq, Hkv, G;
 };
 
-__device__ __forceinline__ float block_reduce(float v, float* sh, bool is_max) {
-  const int lane = threadIdx.x & 63, wid = threadIdx.x >> 6;
+__device__ __forceinline__ float wave_max_all(float v) {
 #pragma unroll
-  for (int d = 32; d >= 1; d >>= 1) {
-    const float o = __shfl_xor(v, d, 64);
-    v = is_max ? __builtin_fmaxf(v, o) : v + o;
-  }
-  __syncthreads();
-  if (lane == 0) sh[wid] = v;
-  __syncthreads();
-  const float r = is_max ? __builtin_fmaxf(__builtin_fmaxf(sh[0], sh[1]), __builtin_fmaxf(sh[2], sh[3]))
-                         : (sh[0] + sh[1]) + (sh[2] + sh[3]);
-  return r;
+  for (int d = 32; d >= 1; d >>= 1) v = __builtin_fmaxf(v, __shfl_xor(v, d, 64));
+  return v;
+}
+__device__ __forceinline__ float wave_sum_all(float v) {
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) v += __shfl_xor(v, d, 64);
+  return v;
 }
 
-__global__ __launch_bounds__(256) void decode_attn_kernel(DecodeAttnArgs a) {
-  __shared__ float s_q[kDecMaxG][kDecD];
-  __shared__ float s_p[kDecMaxG][kDecSlice];
-  __shared__ float s_acc[4][kDecMaxG][kDecD];
-  __shared__ float s_red[4];
-  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+// One wave per (batch, kv head, 64-key slice).  Lane t scores key j0 + t for every
+// query head of the group (its whole 256-byte key row in flight at once, q broadcast
+// from LDS); the slice max and sum are wave reductions; for P.V lane l owns dims 2l and
+// 2l + 1 and the slice's 64 value rows are loaded together.  Small slices keep many
+// waves in flight per CU: the kernel is latency-bound at decode sizes.
+template <int G>
+__global__ __launch_bounds__(64) void decode_attn_kernel(DecodeAttnArgs a) {
+  __shared__ float s_q[G][kDecD];
+  __shared__ float s_p[G][kDecSlice];
+  const int lane = threadIdx.x;
   const int bg = blockIdx.x, slice = blockIdx.y;
   const int b = bg / a.Hkv, g = bg - (bg / a.Hkv) * a.Hkv;
-  const int G = a.G;
   int plen = a.lengths[bg];
   plen = plen < 0 ? 0 : (plen > a.capacity ? (int)a.capacity : plen);
   const int total = plen + a.exact_len;
   const int j0 = slice * kDecSlice;
   if (j0 >= total) return;  // the combine kernel skips slices past the end
 
-  for (int i = tid; i < G * kDecD; i += 256) {
+  for (int i = lane; i < G * kDecD; i += 64) {
     const int hh = i / kDecD, d = i - hh * kDecD;
     const uint16_t* qrow = a.q + b * a.sq_b + (int64_t)(g * G + hh) * a.sq_h;
     s_q[hh][d] = __uint_as_float((uint32_t)qrow[d] << 16);
   }
   __syncthreads();
 
-  // ---- scores: thread t scores key j0 + t for every head of the group ----
-  const int j = j0 + tid;
+  // ---- scores ----
+  const int j = j0 + lane;
   const bool valid = j < total;
-  float sc[kDecMaxG];
+  float sc[G];
 #pragma unroll
-  for (int hh = 0; hh < kDecMaxG; ++hh) sc[hh] = -INFINITY;
+  for (int hh = 0; hh < G; ++hh) sc[hh] = -INFINITY;
   if (valid) {
     const uint16_t* krow;
     float bias = 0.0f;
@@ -178,97 +177,145 @@ __global__ __launch_bounds__(256) void decode_attn_kernel(DecodeAttnArgs a) {
     } else {
       krow = a.kx + b * a.sx_b + g * a.sx_h + (int64_t)(j - plen) * a.sx_s;
     }
-    float acc[kDecMaxG];
+    u32x4 kw[kDecD / 8];
 #pragma unroll
-    for (int hh = 0; hh < kDecMaxG; ++hh) acc[hh] = 0.0f;
-#pragma unroll 4
+    for (int c8 = 0; c8 < kDecD / 8; ++c8) kw[c8] = *(const u32x4*)(krow + 8 * c8);
+    float acc[G];
+#pragma unroll
+    for (int hh = 0; hh < G; ++hh) acc[hh] = 0.0f;
+#pragma unroll
     for (int c8 = 0; c8 < kDecD / 8; ++c8) {
-      const u32x4 w = *(const u32x4*)(krow + 8 * c8);
+      const u32x4 w = kw[c8];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const float k0 = bf16_lo(w[e]), k1 = bf16_hi(w[e]);
 #pragma unroll
-        for (int hh = 0; hh < kDecMaxG; ++hh) {
-          if (hh < G) {
-            acc[hh] = __builtin_fmaf(s_q[hh][8 * c8 + 2 * e], k0, acc[hh]);
-            acc[hh] = __builtin_fmaf(s_q[hh][8 * c8 + 2 * e + 1], k1, acc[hh]);
-          }
+        for (int hh = 0; hh < G; ++hh) {
+          acc[hh] = __builtin_fmaf(s_q[hh][8 * c8 + 2 * e], k0, acc[hh]);
+          acc[hh] = __builtin_fmaf(s_q[hh][8 * c8 + 2 * e + 1], k1, acc[hh]);
         }
       }
     }
 #pragma unroll
-    for (int hh = 0; hh < kDecMaxG; ++hh)
+    for (int hh = 0; hh < G; ++hh)
       if (hh < G) sc[hh] = acc[hh] * a.scale + bias;
   }
 
   // ---- per-head slice max and sum; bf16-rounded weights to LDS ----
   float* part = a.part + ((int64_t)bg * a.nslice + slice) * G * (kDecD + 2);
+#pragma unroll
   for (int hh = 0; hh < G; ++hh) {
-    const float m = block_reduce(sc[hh], s_red, true);
-    const float p = (sc[hh] == -INFINITY) ? 0.0f : __expf(sc[hh] - m);
-    const float l = block_reduce(p, s_red, false);
-    s_p[hh][tid] = __uint_as_float((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)p) << 16);
-    if (tid == 0) {
-      part[hh * (kDecD + 2)] = m;
-      part[hh * (kDecD + 2) + 1] = l;
+    if (hh < G) {
+      const float m = wave_max_all(sc[hh]);
+      const float p = (sc[hh] == -INFINITY) ? 0.0f : __expf(sc[hh] - m);
+      const float l = wave_sum_all(p);
+      s_p[hh][lane] = __uint_as_float((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)p) << 16);
+      if (lane == 0) {
+        part[hh * (kDecD + 2)] = m;
+        part[hh * (kDecD + 2) + 1] = l;
+      }
     }
   }
   __syncthreads();
 
-  // ---- P.V: wave w covers keys [64w, 64w + 64) of the slice, lane l dims 2l, 2l+1 ----
-  float av[kDecMaxG][2];
+  // ---- P.V: lane l owns dims 2l, 2l+1; the slice's value rows are loaded together
+  // (rows past the end load nothing and carry p = 0) ----
+  uint32_t vw[kDecSlice];
 #pragma unroll
-  for (int hh = 0; hh < kDecMaxG; ++hh) av[hh][0] = av[hh][1] = 0.0f;
-  for (int jj = wid * 64; jj < wid * 64 + 64; ++jj) {
-    const int jk = j0 + jj;
-    if (jk >= total) break;
+  for (int u = 0; u < kDecSlice; ++u) {
+    const int jk = j0 + u;
     const uint16_t* vrow = jk < plen ? a.vp + b * a.sp_b + g * a.sp_h + (int64_t)jk * a.sp_s
                                      : a.vx + b * a.sx_b + g * a.sx_h + (int64_t)(jk - plen) * a.sx_s;
-    const uint32_t w = *(const uint32_t*)(vrow + 2 * lane);
-    const float v0 = bf16_lo(w), v1 = bf16_hi(w);
+    vw[u] = jk < total ? *(const uint32_t*)(vrow + 2 * lane) : 0u;
+  }
+  float av[G][2];
 #pragma unroll
-    for (int hh = 0; hh < kDecMaxG; ++hh)
+  for (int hh = 0; hh < G; ++hh) av[hh][0] = av[hh][1] = 0.0f;
+#pragma unroll
+  for (int u = 0; u < kDecSlice; ++u) {
+    const float v0 = bf16_lo(vw[u]), v1 = bf16_hi(vw[u]);
+#pragma unroll
+    for (int hh = 0; hh < G; ++hh)
       if (hh < G) {
-        av[hh][0] = __builtin_fmaf(s_p[hh][jj], v0, av[hh][0]);
-        av[hh][1] = __builtin_fmaf(s_p[hh][jj], v1, av[hh][1]);
+        av[hh][0] = __builtin_fmaf(s_p[hh][u], v0, av[hh][0]);
+        av[hh][1] = __builtin_fmaf(s_p[hh][u], v1, av[hh][1]);
       }
   }
 #pragma unroll
-  for (int hh = 0; hh < kDecMaxG; ++hh)
+  for (int hh = 0; hh < G; ++hh)
     if (hh < G) {
-      s_acc[wid][hh][2 * lane] = av[hh][0];
-      s_acc[wid][hh][2 * lane + 1] = av[hh][1];
+      part[hh * (kDecD + 2) + 2 + 2 * lane] = av[hh][0];
+      part[hh * (kDecD + 2) + 3 + 2 * lane] = av[hh][1];
     }
-  __syncthreads();
-  for (int i = tid; i < G * kDecD; i += 256) {
-    const int hh = i / kDecD, d = i - hh * kDecD;
-    part[hh * (kDecD + 2) + 2 + d] = (s_acc[0][hh][d] + s_acc[1][hh][d]) + (s_acc[2][hh][d] + s_acc[3][hh][d]);
-  }
 }
 
-__global__ __launch_bounds__(128) void decode_combine_kernel(DecodeAttnArgs a) {
+// Merge of the slices of one query head.  The slice maxima and sums go through LDS
+// once; then thread (dim d, half q) adds dim d of the P.V partials of the slices
+// s = q (mod 2), 32 slices at a time with all 32 loads in flight, and the two halves
+// are added in LDS.
+constexpr int kDecMaxSlices = 16384;
+constexpr int kCombUnroll = 32;
+__global__ __launch_bounds__(256) void decode_combine_kernel(DecodeAttnArgs a) {
+  __shared__ float s_f[kDecMaxSlices];
+  __shared__ float s_red[4];
+  __shared__ float s_half[kDecD];
   const int bhq = blockIdx.x;
   const int b = bhq / a.Hq, hq = bhq - (bhq / a.Hq) * a.Hq;
   const int g = hq / a.G, hh = hq - g * a.G;
   const int bg = b * a.Hkv + g;
+  const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   int plen = a.lengths[bg];
   plen = plen < 0 ? 0 : (plen > a.capacity ? (int)a.capacity : plen);
   const int total = plen + a.exact_len;
   const int ns = (total + kDecSlice - 1) / kDecSlice;
   const float* base = a.part + (int64_t)bg * a.nslice * a.G * (kDecD + 2) + hh * (kDecD + 2);
   const int64_t sstride = (int64_t)a.G * (kDecD + 2);
-  float M = -INFINITY;
-  for (int s = 0; s < ns; ++s) M = __builtin_fmaxf(M, base[s * sstride]);
-  float L = 0.0f, acc = 0.0f;
-  const int d = threadIdx.x;
-  for (int s = 0; s < ns; ++s) {
-    const float ms = base[s * sstride];
-    if (ms == -INFINITY) continue;
-    const float f = __expf(ms - M);
-    L += base[s * sstride + 1] * f;
-    acc += base[s * sstride + 2 + d] * f;
+  // slice maxima -> M
+  float m = -INFINITY;
+  for (int s2 = tid; s2 < ns; s2 += 256) {
+    const float ms = base[s2 * sstride];
+    s_f[s2] = ms;
+    m = __builtin_fmaxf(m, ms);
   }
-  a.out[b * a.so_b + hq * a.so_h + d] = __builtin_bit_cast(uint16_t, (__bf16)(acc / L));
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) m = __builtin_fmaxf(m, __shfl_xor(m, d, 64));
+  if (lane == 0) s_red[wid] = m;
+  __syncthreads();
+  const float M = __builtin_fmaxf(__builtin_fmaxf(s_red[0], s_red[1]), __builtin_fmaxf(s_red[2], s_red[3]));
+  __syncthreads();
+  // slice factors and L
+  float l = 0.0f;
+  for (int s2 = tid; s2 < ns; s2 += 256) {
+    const float ms = s_f[s2];
+    const float f = ms == -INFINITY ? 0.0f : __expf(ms - M);
+    s_f[s2] = f;
+    l += f == 0.0f ? 0.0f : base[s2 * sstride + 1] * f;
+  }
+#pragma unroll
+  for (int d = 32; d >= 1; d >>= 1) l += __shfl_xor(l, d, 64);
+  if (lane == 0) s_red[wid] = l;
+  __syncthreads();
+  const float L = (s_red[0] + s_red[1]) + (s_red[2] + s_red[3]);
+  // P.V partials of dim d over the slices of this half
+  const int d = tid & (kDecD - 1), q = tid >> 7;
+  float acc = 0.0f;
+  for (int s0 = q; s0 < ns; s0 += 2 * kCombUnroll) {
+    float x[kCombUnroll];
+#pragma unroll
+    for (int u = 0; u < kCombUnroll; ++u) {
+      const int s2 = s0 + 2 * u;
+      x[u] = s2 < ns ? base[s2 * sstride + 2 + d] : 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < kCombUnroll; ++u) {
+      const int s2 = s0 + 2 * u;
+      const float f = s2 < ns ? s_f[s2] : 0.0f;
+      acc += f == 0.0f ? 0.0f : x[u] * f;
+    }
+  }
+  if (q == 1) s_half[d] = acc;
+  __syncthreads();
+  if (q == 0) a.out[b * a.so_b + hq * a.so_h + d] = __builtin_bit_cast(uint16_t, (__bf16)((acc + s_half[d]) / L));
 }
 
 }  // namespace da
@@ -330,6 +377,8 @@ extern "C" int da_decode_attention(const void* q, int dtype, int64_t B, int64_t 
              "da_decode_attention: bad cache lengths");
   DA_REQUIRE(((sp_b | sp_h | sp_s | sx_b | sx_h | sx_s) & 7) == 0 && (((uintptr_t)k_packed | (uintptr_t)k_exact) & 15) == 0,
              "da_decode_attention: key rows must be 16-byte aligned");
+  if ((capacity + window + kDecSlice - 1) / kDecSlice > kDecMaxSlices)
+    return set_error(DA_ERR_UNSUPPORTED, "da_decode_attention: cache longer than %d keys", kDecMaxSlices * kDecSlice);
   const int64_t need = da_decode_workspace_size(B, Hq, capacity, window);
   if (!workspace || workspace_bytes < need)
     return set_error(DA_ERR_WORKSPACE, "da_decode_attention: workspace of %lld bytes required", (long long)need);
@@ -343,9 +392,19 @@ extern "C" int da_decode_attention(const void* q, int dtype, int64_t B, int64_t 
   a.nslice = (int)((capacity + window + kDecSlice - 1) / kDecSlice);
   a.B = (int)B; a.Hq = (int)Hq; a.Hkv = (int)Hkv; a.G = (int)(Hq / Hkv);
   hipStream_t st = (hipStream_t)stream;
-  hipLaunchKernelGGL(decode_attn_kernel, dim3((unsigned)(B * Hkv), (unsigned)a.nslice), dim3(256), 0, st, a);
+  const dim3 agrid((unsigned)(B * Hkv), (unsigned)a.nslice);
+  switch (a.G) {
+    case 1: hipLaunchKernelGGL(decode_attn_kernel<1>, agrid, dim3(64), 0, st, a); break;
+    case 2: hipLaunchKernelGGL(decode_attn_kernel<2>, agrid, dim3(64), 0, st, a); break;
+    case 3: hipLaunchKernelGGL(decode_attn_kernel<3>, agrid, dim3(64), 0, st, a); break;
+    case 4: hipLaunchKernelGGL(decode_attn_kernel<4>, agrid, dim3(64), 0, st, a); break;
+    case 5: hipLaunchKernelGGL(decode_attn_kernel<5>, agrid, dim3(64), 0, st, a); break;
+    case 6: hipLaunchKernelGGL(decode_attn_kernel<6>, agrid, dim3(64), 0, st, a); break;
+    case 7: hipLaunchKernelGGL(decode_attn_kernel<7>, agrid, dim3(64), 0, st, a); break;
+    default: hipLaunchKernelGGL(decode_attn_kernel<8>, agrid, dim3(64), 0, st, a); break;
+  }
   int rc = check_launch("da_decode_attention");
   if (rc) return rc;
-  hipLaunchKernelGGL(decode_combine_kernel, dim3((unsigned)(B * Hq)), dim3(128), 0, st, a);
+  hipLaunchKernelGGL(decode_combine_kernel, dim3((unsigned)(B * Hq)), dim3(256), 0, st, a);
   return check_launch("da_decode_attention(combine)");
 }
