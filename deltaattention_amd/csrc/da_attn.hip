@@ -993,12 +993,20 @@ __global__ __launch_bounds__(256) void hybrid_schedule_kernel(const int32_t* __r
     if (bg == 0 && blockIdx.y == 1 && tid < kTileN) prep.zeros[tid] = 0.0f;
     return;
   }
-  for (int jb = wid; jb < nblk; jb += 4) {
-    const int i0 = jb * kBlock + lane, i1 = i0 + 64;
-    int m = max(i0 < P ? row[i0] : Nk + 1, i1 < P ? row[i1] : Nk + 1);
+  // wave w takes blocks 8w .. 8w + 7 of every 32, their loads in flight together
+  for (int jb0 = wid * 8; jb0 < nblk; jb0 += 32) {
+    int m[8];
 #pragma unroll
-    for (int d = 32; d >= 1; d >>= 1) m = max(m, __shfl_xor(m, d, 64));
-    if (lane == 0) s_bmax[jb] = m;
+    for (int u = 0; u < 8; ++u) {
+      const int i0 = (jb0 + u) * kBlock + lane, i1 = i0 + 64;
+      m[u] = max(i0 < P ? row[i0] : Nk + 1, i1 < P ? row[i1] : Nk + 1);
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+#pragma unroll
+      for (int d = 32; d >= 1; d >>= 1) m[u] = max(m[u], __shfl_xor(m[u], d, 64));
+      if (lane == 0 && jb0 + u < nblk) s_bmax[jb0 + u] = m[u];
+    }
   }
   __syncthreads();
   const int per = (nblk + 255) / 256;

@@ -171,32 +171,34 @@ __global__ __launch_bounds__(256) void pack_scatter_kernel(
         cnt[prow + dst] = (int32_t)(next - r);      // modeling_llama.py:683-685
       }
     }
-    // Copy the anchor rows; four rows per step to keep loads in flight.
+    // Copy the anchor rows, sixteen rows per step so that their loads are in flight
+    // together (a 64-row group holds about 64 / r anchors).
+    constexpr int kRows = 16;
     const uint16_t* kbase = k + b * sk_b + h * sk_h + 2 * lane;
     const uint16_t* vbase = v + b * sv_b + h * sv_h + 2 * lane;
     const bool act = lane < nw;
     uint64_t rem = bits;
     int64_t dst = off;
     while (rem) {
-      int rows[4];
+      int rows[kRows];
       int nr = 0;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
+      for (int j = 0; j < kRows; ++j) {
         rows[j] = rem ? (int)__builtin_ctzll(rem) : -1;
         if (rem) {
           rem &= rem - 1ull;
           ++nr;
         }
       }
-      uint32_t kw[4], vw[4];
+      uint32_t kw[kRows], vw[kRows];
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
+      for (int j = 0; j < kRows; ++j) {
         const int64_t src = (int64_t)g * 64 + rows[j];
         kw[j] = (act && j < nr) ? *(const uint32_t*)(kbase + src * sk_n) : 0u;
         vw[j] = (act && j < nr) ? *(const uint32_t*)(vbase + src * sv_n) : 0u;
       }
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
+      for (int j = 0; j < kRows; ++j) {
         const int64_t d = dst + j;
         if (act && j < nr && d < capacity) {
           *(uint32_t*)(kp + (prow + d) * D + 2 * lane) = kw[j];
