@@ -359,7 +359,6 @@ void attn_kernel(AttnArgs a) {
       // S^T registers 8 * (r4 >> 1) .. +7 of block kb2.
       u32x4 pw[4];
       float psum = 0.0f;
-      const bf16x2 ones2 = {(__bf16)1.0f, (__bf16)1.0f};
       const bool weighted = (VARIANT == kPure) || (VARIANT == kHybrid && ph1);
       const float* cl = (const float*)(stage + kCntOff);
 #pragma unroll
@@ -374,12 +373,9 @@ void attn_kernel(AttnArgs a) {
             p[e] = exp2_fast(__builtin_fmaf(s[kb2][4 * r4 + e], c, neg));
             if (weighted) p[e] *= w4[e];
           }
-          // the row sum adds the bf16 values the P.V MFMAs use
-          const uint32_t w01 = pack_bf16x2(p[0], p[1]), w23 = pack_bf16x2(p[2], p[3]);
-          pw[2 * kb2 + (r4 >> 1)][(r4 & 1) * 2 + 0] = w01;
-          pw[2 * kb2 + (r4 >> 1)][(r4 & 1) * 2 + 1] = w23;
-          psum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w01), ones2, psum, false);
-          psum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w23), ones2, psum, false);
+          psum += (p[0] + p[1]) + (p[2] + p[3]);
+          pw[2 * kb2 + (r4 >> 1)][(r4 & 1) * 2 + 0] = pack_bf16x2(p[0], p[1]);
+          pw[2 * kb2 + (r4 >> 1)][(r4 & 1) * 2 + 1] = pack_bf16x2(p[2], p[3]);
         }
       }
       l_i = l_i * alpha + psum;
@@ -860,14 +856,10 @@ void attn_pp_kernel(AttnArgs a) {
           if ((a.causal && key0 + kTileN - 1 > r0w) || key0 + kTileN > a.Nk)
             mask_dense(s, key0, row, hl, a.Nk, a.causal);
         }
-        // two chains of three-input maxima
-        float ma = __builtin_fmaxf(s[0][0], s[1][0]), mb = __builtin_fmaxf(s[0][1], s[1][1]);
+        float mx = -INFINITY;
 #pragma unroll
-        for (int r = 2; r < 16; r += 2) {
-          ma = __builtin_fmaxf(__builtin_fmaxf(ma, s[0][r]), s[1][r]);
-          mb = __builtin_fmaxf(__builtin_fmaxf(mb, s[0][r + 1]), s[1][r + 1]);
-        }
-        float mx = halves_max(__builtin_fmaxf(ma, mb));
+        for (int r = 0; r < 16; ++r) mx = __builtin_fmaxf(mx, __builtin_fmaxf(s[0][r], s[1][r]));
+        mx = halves_max(mx);
         const bool upd = mx > m_used + lazy_thr;  // no NaN when m_used = -inf
         if (VARIANT != kDense) issue_once();
         if (__ballot(upd)) {
@@ -881,10 +873,9 @@ void attn_pp_kernel(AttnArgs a) {
           m_used = m_new;
         }
         const float neg = (m_used == -INFINITY) ? 0.0f : -m_used * c;
-        // P in bf16 for the P.V MFMAs; the row sum adds the same bf16 values (two-term
-        // dot products with ones), so numerator and denominator see one rounding of p
+        // P in bf16 for the P.V MFMAs; the row sum adds the fp32 p, as
+        // deltaFlashAttention.py:86-98
         float psa = 0.0f, psb = 0.0f;
-        const bf16x2 ones2 = {(__bf16)1.0f, (__bf16)1.0f};
 #pragma unroll
         for (int kb2 = 0; kb2 < 2; ++kb2) {
 #pragma unroll
@@ -892,11 +883,10 @@ void attn_pp_kernel(AttnArgs a) {
             float p[4];
 #pragma unroll
             for (int e = 0; e < 4; ++e) p[e] = exp2_fast(__builtin_fmaf(s[kb2][4 * r4 + e], c, neg));
-            const uint32_t w01 = pack_bf16x2(p[0], p[1]), w23 = pack_bf16x2(p[2], p[3]);
-            pw[2 * kb2 + (r4 >> 1)][(r4 & 1) * 2 + 0] = w01;
-            pw[2 * kb2 + (r4 >> 1)][(r4 & 1) * 2 + 1] = w23;
-            psa = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w01), ones2, psa, false);
-            psb = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, w23), ones2, psb, false);
+            pw[2 * kb2 + (r4 >> 1)][(r4 & 1) * 2 + 0] = pack_bf16x2(p[0], p[1]);
+            pw[2 * kb2 + (r4 >> 1)][(r4 & 1) * 2 + 1] = pack_bf16x2(p[2], p[3]);
+            psa += p[0] + p[1];
+            psb += p[2] + p[3];
           }
         }
         l_i += psa + psb;

@@ -159,6 +159,10 @@ def test_hybrid_golden(gpu, case, variant):
     (1, 4, 2, 900, 9.0, 128, "pure_phase1", False),
     (1, 8, 2, 3000, 12.0, 128, "hybrid", False),
     (1, 2, 1, 2048, 1e6, 128, "hybrid", False),   # only chunk starts are anchors
+    # GQA group of 4 (the grouped kernel), counts of 512: the largest key biases
+    (1, 8, 2, 2048, 1e6, 128, "hybrid", False),
+    (1, 8, 2, 2048, 1e6, 128, "pure_phase1", False),
+    (1, 8, 2, 2048, 1e6, 128, "hybrid", True),
 ])
 def test_delta_prefill_vs_oracle(gpu, B, Hq, Hkv, N, tau, W, variant, no_count):
     from deltaattention_amd import ops
