@@ -16,10 +16,10 @@
 // Logical schedule (deltaFlashAttention.py:58-113).  Phase 1 takes packed blocks of
 // 128 anchors while their maximum timestamp is < start_m - W; Phase 2 covers dense
 // keys from ((last + 1) / 128) * 128 to the diagonal.  The prefix of safe packed
-// blocks is found by a binary search over the per-head prefix maxima of the block
-// maxima (hybrid_schedule_kernel), which reproduces the reference's
-// stop-at-first-unsafe-block loop for any timestamps, including its zero-padding
-// behaviour (fully padded blocks have maximum 0).
+// blocks is counted over the per-head prefix maxima of the block maxima
+// (hybrid_schedule_kernel), which reproduces the reference's stop-at-first-unsafe-block
+// loop for any timestamps, including its zero-padding behaviour (fully padded blocks
+// have maximum 0).
 //
 // MFMA formulation.  Scores are computed transposed, S^T = K Q^T, with
 // v_mfma_f32_32x32x16_bf16: K (32 keys x 16 dims) comes from LDS as the A operand,
@@ -189,6 +189,43 @@ __device__ __forceinline__ void store_tile(const TileRegs& r, char* stage, int t
   }
 }
 
+// Phase-1 extent of a query block (deltaFlashAttention.py:58-80): n_safe = the number of
+// packed blocks whose prefix maximum timestamp is below thr -- the prefix maxima do not
+// decrease, so these are exactly the blocks before the first unsafe one -- and last = the
+// maximum timestamp of the last of them (-1 if none).  A ballot per 64 blocks counts
+// them; the entries of 256 blocks are loaded together, so the usual case is one round
+// trip to memory.  Needs all 64 lanes of the wave.
+__device__ __forceinline__ void safe_prefix(const int32_t* __restrict__ bmax, const int32_t* __restrict__ pmax,
+                                            int nblk, int thr, int& n_safe, int& last) {
+  const int lane = threadIdx.x & 63;
+  int n = 0, prev_last = -1;
+  last = -1;
+  for (int base = 0; base < nblk; base += 256) {
+    int pv[4], bv[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int i = base + 64 * j + lane;
+      pv[j] = i < nblk ? pmax[i] : INT_MAX;
+      bv[j] = i < nblk ? bmax[i] : -1;
+    }
+    int cnt = 0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) cnt += __popcll(__ballot(pv[j] < thr));
+    n += cnt;
+    if (cnt > 0) {
+      const int k = cnt - 1;  // the last safe block is entry k of this chunk
+      const int j = k >> 6;
+      const int v = j == 0 ? bv[0] : j == 1 ? bv[1] : j == 2 ? bv[2] : bv[3];
+      last = __builtin_amdgcn_readlane(v, k & 63);
+    } else {
+      last = prev_last;
+    }
+    if (cnt < 256) break;
+    prev_last = last;
+  }
+  n_safe = n;
+}
+
 template <int VARIANT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void attn_kernel(AttnArgs a) {
@@ -228,14 +265,8 @@ void attn_kernel(AttnArgs a) {
     const int nblk = (P + kBlock - 1) / kBlock;
     const int32_t* bmax = a.sched + (int64_t)bg * 2 * a.nblk_cap;
     const int32_t* pmax = bmax + a.nblk_cap;
-    const int thr = start_m - a.window;
-    int lo = 0, hi = nblk;
-    while (lo < hi) {
-      const int mid = (lo + hi) >> 1;
-      if (pmax[mid] < thr) lo = mid + 1; else hi = mid;
-    }
-    const int n_safe = lo;
-    const int last = n_safe > 0 ? bmax[n_safe - 1] : -1;
+    int n_safe, last;
+    safe_prefix(bmax, pmax, nblk, start_m - a.window, n_safe, last);
     ds = max(0, ((last + 1) / kBlock) * kBlock);
     if (VARIANT == kHybrid) n1 = n_safe * (kBlock / kTileN);
     kend = min(a.Nk, wg_end);
@@ -600,15 +631,10 @@ void attn_pp_kernel(AttnArgs a) {
     const int nblk = (P + kBlock - 1) / kBlock;
     const int32_t* bmax = a.sched + (int64_t)bg * 2 * a.nblk_cap;
     const int32_t* pmax = bmax + a.nblk_cap;
-    const int thr = start_m - a.window;
-    int lo = 0, hi = nblk;
-    while (lo < hi) {
-      const int mid = (lo + hi) >> 1;
-      if (pmax[mid] < thr) lo = mid + 1; else hi = mid;
-    }
-    const int last = lo > 0 ? bmax[lo - 1] : -1;
+    int n_safe, last;
+    safe_prefix(bmax, pmax, nblk, start_m - a.window, n_safe, last);
     ds = max(0, ((last + 1) / kBlock) * kBlock);
-    if (VARIANT == kHybrid) n1 = lo * (kBlock / kTileN);
+    if (VARIANT == kHybrid) n1 = n_safe * (kBlock / kTileN);
     kend = min(a.Nk, wg_end);
   } else if (VARIANT == kPure) {
     n1 = (P + kTileN - 1) / kTileN;
@@ -715,21 +741,6 @@ void attn_pp_kernel(AttnArgs a) {
     for (int db = 0; db < 4; ++db) v_off[db] = base + 64 * (db ^ q);
   }
 
-  // ---- Q^T in registers ----
-  bf16x8 qreg[kD / 16];
-  {
-    const uint16_t* qrow = a.q + (int64_t)b * a.sq_b + (int64_t)h * a.sq_h + (int64_t)row * a.sq_n;
-#pragma unroll
-    for (int t = 0; t < kD / 16; ++t) {
-      u32x4 w = (row < a.Nq) ? *(const u32x4*)(qrow + 16 * t + 8 * hl) : u32x4{0, 0, 0, 0};
-      qreg[t] = __builtin_bit_cast(bf16x8, w);
-    }
-    // Redefine Q^T here so the loop does not see it as an outstanding load: otherwise
-    // every S = K Q^T block waits for all memory loads, including the staging loads
-    // meant to land two sections later.
-#pragma unroll
-    for (int t = 0; t < kD / 16; ++t) asm volatile("" : "+v"(qreg[t]));
-  }
 
   f32x16 o[4];
 #pragma unroll
@@ -752,6 +763,25 @@ void attn_pp_kernel(AttnArgs a) {
     dma_rows(true, 0);
     if (wid_s == 0) dma_meta(0);
     dma_issue(1, 0);
+  }
+  // ---- Q^T in registers, loaded while the first tiles are in flight ----
+  bf16x8 qreg[kD / 16];
+  {
+    // rows past Nq load row Nq - 1 (no branch between the loads) and are zeroed after
+    const uint16_t* qrow = a.q + (int64_t)b * a.sq_b + (int64_t)h * a.sq_h + (int64_t)min(row, a.Nq - 1) * a.sq_n;
+    u32x4 w[kD / 16];
+#pragma unroll
+    for (int t = 0; t < kD / 16; ++t) w[t] = *(const u32x4*)(qrow + 16 * t + 8 * hl);
+    // Redefine Q^T here so the loop does not see it as an outstanding load: otherwise
+    // every S = K Q^T block waits for all memory loads, including the staging loads
+    // meant to land two sections later.
+#pragma unroll
+    for (int t = 0; t < kD / 16; ++t) {
+      asm volatile("" : "+v"(w[t]));
+      qreg[t] = __builtin_bit_cast(bf16x8, row < a.Nq ? w[t] : u32x4{0, 0, 0, 0});
+    }
+  }
+  if (T > 0) {
     __builtin_amdgcn_s_waitcnt(vmcnt_only(0));
     lds_barrier();
   }
