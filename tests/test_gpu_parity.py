@@ -188,3 +188,60 @@ def test_hybrid_float_counts_matches_int(gpu):
     a = ops.hybrid_prefill(qg, kg, vg, pk.k_packed, pk.v_packed, pk.timestamps, pk.counts)
     b = ops.hybrid_prefill(qg, kg, vg, pk.k_packed, pk.v_packed, pk.timestamps, pk.counts.float())
     assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("N,Hq", [(40960, 4), (70000, 4), (70000, 2)])
+def test_keep_all_hybrid_equals_dense_full_size(gpu, N, Hq):
+    """tau = 0 keeps every distinct key with count 1, so the hybrid prefill covers every
+    key once and must agree with dense causal attention.  At these sizes the packed
+    blocks number 320 and 547 (more than one 256-block pass of the Phase-1 count); a
+    GQA group of 2 runs the per-head kernel, a group of 4 the grouped one."""
+    from deltaattention_amd import ops
+    q, k, v = _bf16_inputs(1, Hq, 1, N, 128, seed=5)
+    qg, kg, vg = q.to(gpu), k.to(gpu), v.to(gpu)
+    announce(f"keep-all hybrid vs dense N={N} Hq={Hq}")
+    keep, counts = ops.select(kg, 0.0, 512)
+    assert int(keep.sum()) == N
+    pk = ops.pack(keep, kg, vg)
+    hyb = ops.hybrid_prefill(qg, kg, vg, pk.k_packed, pk.v_packed, pk.timestamps, pk.counts,
+                             window=128, num_packed_dev=pk.num_packed)
+    dense = ops.dense_prefill(qg, kg, vg)
+    _close(hyb.float().cpu().numpy(), dense.float().cpu().numpy(), f"keep-all N={N}")
+
+
+@pytest.mark.parametrize("Hq", [4, 2])
+def test_phase1_extent_full_size(gpu, Hq):
+    """Q = 0 makes every score 0, so each output row is the count-weighted mean of the
+    V rows it sees: weight 2 for the packed keys of Phase 1, 1 for the exact keys of
+    Phase 2.  With every key kept (timestamps 0..N-1) the Phase-1 extent of a 128-row
+    query block has the closed form L = 128 * #{b : 128 b + 127 < start_m - W}
+    (deltaFlashAttention.py:58-80), so the expected output is exact: V[:, 0] marks the
+    keys at or beyond 32768, V[:, 1] is 1.  N = 70000 gives 547 packed blocks, more than
+    one 256-block pass of the count; a wrong extent moves thousands of keys between
+    weights 2 and 1."""
+    from deltaattention_amd import ops
+    N, W, D = 70000, 128, 128
+    announce(f"phase-1 extent, closed form, N={N} Hq={Hq}")
+    q = torch.zeros((1, Hq, N, D), dtype=torch.bfloat16, device=gpu)
+    k = torch.randn((1, 1, N, D), generator=torch.Generator().manual_seed(3)).to(torch.bfloat16).to(gpu)
+    v = torch.zeros((1, 1, N, D), dtype=torch.bfloat16)
+    v[0, 0, 32768:, 0] = 1.0
+    v[0, 0, :, 1] = 1.0
+    v = v.to(gpu)
+    keep = torch.ones((1, 1, N), dtype=torch.int32, device=gpu)
+    pk = ops.pack(keep, k, v)
+    out = ops.hybrid_prefill(q, k, v, pk.k_packed, pk.v_packed, pk.timestamps, pk.counts * 2,
+                             window=W, num_packed_dev=pk.num_packed)
+    got = out[0, :, :, :2].float().cpu().numpy()
+    i = np.arange(N, dtype=np.int64)
+    start_m = (i // 128) * 128
+    n_safe = np.maximum(0, -(-(start_m - W - 127) // 128))   # ceil, clipped at 0
+    L = 128 * n_safe
+    late = lambda a, b: np.maximum(0, b - np.maximum(a, 32768))   # keys in [a, b) at >= 32768
+    num = 2.0 * late(0, L) + late(L, i + 1)
+    den = 2.0 * L + (i + 1 - L)
+    want0 = num / den
+    assert np.all(got[..., 1] == 1.0)
+    err = np.abs(got[..., 0] - want0[None, :])
+    print(f"phase-1 extent: max-abs {err.max():.3e}", flush=True)
+    assert err.max() <= 4e-3   # bf16 rounding of values in [0, 1]
