@@ -52,14 +52,20 @@ class KernelLauncher:
         raise NotImplementedError
 
 
+# the 16-bit element types the kernels take (one of them per call)
+HALF = (torch.bfloat16, torch.float16)
+
+
 def tensor(a, name: str, dtype=None) -> torch.Tensor:
+    """Argument `name` as a GPU tensor; dtype is one torch dtype or a tuple of them."""
     t = a[name]
     if not isinstance(t, torch.Tensor):
         raise TypeError(f"{name} must be a tensor")
     if t.device.type != "cuda":
         raise ValueError(f"{name} is on {t.device}; the native kernels take GPU tensors")
-    if dtype is not None and t.dtype != dtype:
-        raise TypeError(f"{name} must be {dtype}, got {t.dtype}")
+    allowed = dtype if isinstance(dtype, tuple) else (dtype,)
+    if dtype is not None and t.dtype not in allowed:
+        raise TypeError(f"{name} must be {' or '.join(str(d) for d in allowed)}, got {t.dtype}")
     return t
 
 

@@ -13,6 +13,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(HERE, "libdeltaattn.so")
 
 DA_BF16 = 1
+DA_F16 = 2
 DA_I32 = 3
 DA_F32 = 4
 DA_VARIANT = {"hybrid": 0, "sanity": 1, "pure_phase1": 2}
@@ -89,3 +90,16 @@ def strides_array(values) -> ctypes.Array:
     for i, v in enumerate(values):
         arr[i] = int(v)
     return arr
+
+
+def dtype_code(*ts) -> int:
+    """DA_BF16 or DA_F16 for tensors that all share one of those dtypes."""
+    import torch
+    codes = {torch.bfloat16: DA_BF16, torch.float16: DA_F16}
+    dt = ts[0].dtype
+    if dt not in codes:
+        raise TypeError(f"expected bfloat16 or float16 tensors, got {dt}")
+    for t in ts[1:]:
+        if t is not None and t.dtype != dt:
+            raise TypeError(f"all tensors must share one dtype ({dt}), got {t.dtype}")
+    return codes[dt]

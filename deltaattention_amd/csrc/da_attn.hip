@@ -22,11 +22,13 @@
 // have maximum 0).
 //
 // MFMA formulation.  Scores are computed transposed, S^T = K Q^T, with
-// v_mfma_f32_32x32x16_bf16: K (32 keys x 16 dims) comes from LDS as the A operand,
+// v_mfma_f32_32x32x16_bf16 (the _f16 form for fp16 tensors; the kernels are templated on
+// the 16-bit type, and P is rounded to it as the reference rounds p to V's type): K
+// (32 keys x 16 dims) comes from LDS as the A operand,
 // Q^T stays in registers as the B operand for the whole key loop.  In the S^T
 // accumulator a lane holds one query and 16 keys, so the row max and row sum of the
 // online softmax are mostly in-lane (one exchange with lane ^ 32 per tile).  The
-// output is accumulated transposed too, O^T += V^T P^T: the bf16 probabilities are
+// output is accumulated transposed too, O^T += V^T P^T: the 16-bit probabilities are
 // already in the B-operand layout, and V^T comes from an LDS tile that the loader
 // transposes while staging it.
 //
@@ -226,7 +228,7 @@ __device__ __forceinline__ void safe_prefix(const int32_t* __restrict__ bmax, co
   n_safe = n;
 }
 
-template <int VARIANT>
+template <int VARIANT, int DT>
 __global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void attn_kernel(AttnArgs a) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
@@ -286,15 +288,13 @@ void attn_kernel(AttnArgs a) {
   const bool meta = (VARIANT == kHybrid || VARIANT == kPure);
 
   // ---- Q^T in registers (B operand): lane (ql, hl) holds dims 16t + 8hl .. +7 ----
-  bf16x8 qreg[kD / 16];
+  u32x4 qreg[kD / 16];
   {
     const int row = r0w + ql;
     const uint16_t* qrow = a.q + (int64_t)b * a.sq_b + (int64_t)h * a.sq_h + (int64_t)row * a.sq_n;
 #pragma unroll
-    for (int t = 0; t < kD / 16; ++t) {
-      u32x4 w = (row < a.Nq) ? *(const u32x4*)(qrow + 16 * t + 8 * hl) : u32x4{0, 0, 0, 0};
-      qreg[t] = __builtin_bit_cast(bf16x8, w);
-    }
+    for (int t = 0; t < kD / 16; ++t)
+      qreg[t] = (row < a.Nq) ? *(const u32x4*)(qrow + 16 * t + 8 * hl) : u32x4{0, 0, 0, 0};
   }
 
   f32x16 o[4];
@@ -347,8 +347,7 @@ void attn_kernel(AttnArgs a) {
 #pragma unroll
         for (int kb2 = 0; kb2 < 2; ++kb2) {
           const u32x4 w = *(const u32x4*)(stage + k_lds_off(kb2 * 32 + ql, 2 * tt + hl));
-          s[kb2] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, w), qreg[tt],
-                                                            s[kb2], 0, 0, 0);
+          s[kb2] = E16<DT>::mfma(w, qreg[tt], s[kb2]);
         }
       }
       // ---- masks ----
@@ -405,8 +404,8 @@ void attn_kernel(AttnArgs a) {
             if (weighted) p[e] *= w4[e];
           }
           psum += (p[0] + p[1]) + (p[2] + p[3]);
-          pw[2 * kb2 + (r4 >> 1)][(r4 & 1) * 2 + 0] = pack_bf16x2(p[0], p[1]);
-          pw[2 * kb2 + (r4 >> 1)][(r4 & 1) * 2 + 1] = pack_bf16x2(p[2], p[3]);
+          pw[2 * kb2 + (r4 >> 1)][(r4 & 1) * 2 + 0] = E16<DT>::pack(p[0], p[1]);
+          pw[2 * kb2 + (r4 >> 1)][(r4 & 1) * 2 + 1] = E16<DT>::pack(p[2], p[3]);
         }
       }
       l_i = l_i * alpha + psum;
@@ -420,13 +419,11 @@ void attn_kernel(AttnArgs a) {
       // ---- O^T += V^T P^T ----
 #pragma unroll
       for (int u = 0; u < 4; ++u) {
-        const bf16x8 pbv = __builtin_bit_cast(bf16x8, pw[u]);
 #pragma unroll
         for (int db = 0; db < 4; ++db) {
           const int d = db * 32 + ql;
           const u32x4 vw = *(const u32x4*)(stage + vt_lds_chunk(d, 2 * u + hl));
-          o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, vw), pbv, o[db],
-                                                           0, 0, 0);
+          o[db] = E16<DT>::mfma(vw, pw[u], o[db]);
         }
       }
     }
@@ -449,8 +446,8 @@ void attn_kernel(AttnArgs a) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         u32x2 w;
-        w[0] = pack_bf16x2(o[db][4 * j + 0] * inv, o[db][4 * j + 1] * inv);
-        w[1] = pack_bf16x2(o[db][4 * j + 2] * inv, o[db][4 * j + 3] * inv);
+        w[0] = E16<DT>::pack(o[db][4 * j + 0] * inv, o[db][4 * j + 1] * inv);
+        w[1] = E16<DT>::pack(o[db][4 * j + 2] * inv, o[db][4 * j + 3] * inv);
         *(u32x2*)(orow + db * 32 + 8 * j + 4 * hl) = w;
       }
   }
@@ -588,7 +585,7 @@ constexpr int kPPCnt = kKBytes;
 constexpr int kPPTs = kKBytes + kTileN * 4;
 constexpr float kLazyLog2 = 8.0f;
 
-template <int VARIANT>
+template <int VARIANT, int DT>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void attn_pp_kernel(AttnArgs a) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
@@ -765,7 +762,7 @@ void attn_pp_kernel(AttnArgs a) {
     dma_issue(1, 0);
   }
   // ---- Q^T in registers, loaded while the first tiles are in flight ----
-  bf16x8 qreg[kD / 16];
+  u32x4 qreg[kD / 16];
   {
     // rows past Nq load row Nq - 1 (no branch between the loads) and are zeroed after
     const uint16_t* qrow = a.q + (int64_t)b * a.sq_b + (int64_t)h * a.sq_h + (int64_t)min(row, a.Nq - 1) * a.sq_n;
@@ -778,7 +775,7 @@ void attn_pp_kernel(AttnArgs a) {
 #pragma unroll
     for (int t = 0; t < kD / 16; ++t) {
       asm volatile("" : "+v"(w[t]));
-      qreg[t] = __builtin_bit_cast(bf16x8, row < a.Nq ? w[t] : u32x4{0, 0, 0, 0});
+      qreg[t] = row < a.Nq ? w[t] : u32x4{0, 0, 0, 0};
     }
   }
   if (T > 0) {
@@ -846,9 +843,7 @@ void attn_pp_kernel(AttnArgs a) {
             constexpr int after = 2 * ((i + kTrAhead - 1 < 15 ? i + kTrAhead - 1 : 15) - i);
             lgkm_wait<after>(vlo[i], vhi[i]);
             const i16x8 vw = __builtin_shufflevector(vlo[i], vhi[i], 0, 1, 2, 3, 4, 5, 6, 7);
-            o[i & 3] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, vw),
-                                                                __builtin_bit_cast(bf16x8, pw[i >> 2]),
-                                                                o[i & 3], 0, 0, 0);
+            o[i & 3] = E16<DT>::mfma(__builtin_bit_cast(u32x4, vw), pw[i >> 2], o[i & 3]);
             if constexpr (i + kTrAhead < 16) {
               constexpr int j = i + kTrAhead;
               vlo[j] = ds_read_tr16<(j >> 2) * 4096>(va[j & 3]);
@@ -869,8 +864,7 @@ void attn_pp_kernel(AttnArgs a) {
 #pragma unroll
             for (int kb2 = 0; kb2 < 2; ++kb2) {
               const u32x4 w = *(const u32x4*)(kst + k_off[tt] + kb2 * 8192);
-              s[kb2] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, w),
-                                                                qreg[tt], s[kb2], 0, 0, 0);
+              s[kb2] = E16<DT>::mfma(w, qreg[tt], s[kb2]);
             }
           }
           pipe_mfma_reads_deep();
@@ -903,7 +897,7 @@ void attn_pp_kernel(AttnArgs a) {
           m_used = m_new;
         }
         const float neg = (m_used == -INFINITY) ? 0.0f : -m_used * c;
-        // P in bf16 for the P.V MFMAs; the row sum adds the fp32 p, as
+        // P in the 16-bit type for the P.V MFMAs; the row sum adds the fp32 p, as
         // deltaFlashAttention.py:86-98
         float psa = 0.0f, psb = 0.0f;
 #pragma unroll
@@ -913,8 +907,8 @@ void attn_pp_kernel(AttnArgs a) {
             float p[4];
 #pragma unroll
             for (int e = 0; e < 4; ++e) p[e] = exp2_fast(__builtin_fmaf(s[kb2][4 * r4 + e], c, neg));
-            pw[2 * kb2 + (r4 >> 1)][(r4 & 1) * 2 + 0] = pack_bf16x2(p[0], p[1]);
-            pw[2 * kb2 + (r4 >> 1)][(r4 & 1) * 2 + 1] = pack_bf16x2(p[2], p[3]);
+            pw[2 * kb2 + (r4 >> 1)][(r4 & 1) * 2 + 0] = E16<DT>::pack(p[0], p[1]);
+            pw[2 * kb2 + (r4 >> 1)][(r4 & 1) * 2 + 1] = E16<DT>::pack(p[2], p[3]);
             psa += p[0] + p[1];
             psb += p[2] + p[3];
           }
@@ -948,8 +942,8 @@ void attn_pp_kernel(AttnArgs a) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         u32x2 w;
-        w[0] = pack_bf16x2(o[db][4 * j + 0] * inv, o[db][4 * j + 1] * inv);
-        w[1] = pack_bf16x2(o[db][4 * j + 2] * inv, o[db][4 * j + 3] * inv);
+        w[0] = E16<DT>::pack(o[db][4 * j + 0] * inv, o[db][4 * j + 1] * inv);
+        w[1] = E16<DT>::pack(o[db][4 * j + 2] * inv, o[db][4 * j + 3] * inv);
         *(u32x2*)(orow + db * 32 + 8 * j + 4 * hl) = w;
       }
   }
@@ -1055,11 +1049,11 @@ __global__ __launch_bounds__(256) void hybrid_schedule_kernel(const int32_t* __r
   }
 }
 
-template <int V>
+template <int V, int DT>
 static int allow_lds(size_t bytes) {
   static int done = 0;
   if (!done) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_kernel<V>),
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_kernel<V, DT>),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
     if (e != hipSuccess) return set_error(DA_ERR_HIP, "hipFuncSetAttribute: %s", hipGetErrorString(e));
     done = 1;
@@ -1067,11 +1061,11 @@ static int allow_lds(size_t bytes) {
   return DA_OK;
 }
 
-template <int V>
+template <int V, int DT>
 static int allow_lds_pp(size_t bytes) {
   static int done = 0;
   if (!done) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_pp_kernel<V>),
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_pp_kernel<V, DT>),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
     if (e != hipSuccess) return set_error(DA_ERR_HIP, "hipFuncSetAttribute: %s", hipGetErrorString(e));
     done = 1;
@@ -1079,55 +1073,36 @@ static int allow_lds_pp(size_t bytes) {
   return DA_OK;
 }
 
-static int launch_attn_pp(int variant, AttnArgs& a, hipStream_t st) {
-  a.rows_per_wg = 64;
-  a.n_row_groups = (a.Nq + 63) / 64;
-  const size_t lds = kPPLds;
-  const unsigned grid = (unsigned)((int64_t)a.n_row_groups * a.units);
-  int rc = DA_OK;
-  switch (variant) {
-    case kHybrid: rc = allow_lds_pp<kHybrid>(lds); break;
-    case kSanity: rc = allow_lds_pp<kSanity>(lds); break;
-    case kPure: rc = allow_lds_pp<kPure>(lds); break;
-    default: rc = allow_lds_pp<kDense>(lds); break;
+template <int V, int DT>
+static int launch_attn_t(AttnArgs& a, hipStream_t st) {
+  if (a.hpw == 4) {
+    a.rows_per_wg = 64;
+    a.n_row_groups = (a.Nq + 63) / 64;
+    const size_t lds = kPPLds;
+    const unsigned grid = (unsigned)((int64_t)a.n_row_groups * a.units);
+    if (int rc = allow_lds_pp<V, DT>(lds)) return rc;
+    hipLaunchKernelGGL((attn_pp_kernel<V, DT>), dim3(grid), dim3(512), lds, st, a);
+    return check_launch("attention kernel (ping-pong)");
   }
-  if (rc) return rc;
-  switch (variant) {
-    case kHybrid: hipLaunchKernelGGL(attn_pp_kernel<kHybrid>, dim3(grid), dim3(512), lds, st, a); break;
-    case kSanity: hipLaunchKernelGGL(attn_pp_kernel<kSanity>, dim3(grid), dim3(512), lds, st, a); break;
-    case kPure: hipLaunchKernelGGL(attn_pp_kernel<kPure>, dim3(grid), dim3(512), lds, st, a); break;
-    default: hipLaunchKernelGGL(attn_pp_kernel<kDense>, dim3(grid), dim3(512), lds, st, a); break;
-  }
-  return check_launch("attention kernel (ping-pong)");
-}
-
-static int launch_attn(int variant, AttnArgs& a, hipStream_t st) {
   const size_t lds = 2 * kStageBytes;
   const unsigned grid = (unsigned)((int64_t)a.n_row_groups * a.units);
-  int rc = DA_OK;
-  switch (variant) {
-    case kHybrid: rc = allow_lds<kHybrid>(lds); break;
-    case kSanity: rc = allow_lds<kSanity>(lds); break;
-    case kPure: rc = allow_lds<kPure>(lds); break;
-    default: rc = allow_lds<kDense>(lds); break;
-  }
-  if (rc) return rc;
-  if (a.hpw == 4) return launch_attn_pp(variant, a, st);
-  switch (variant) {
-    case kHybrid:
-      hipLaunchKernelGGL(attn_kernel<kHybrid>, dim3(grid), dim3(256), lds, st, a);
-      break;
-    case kSanity:
-      hipLaunchKernelGGL(attn_kernel<kSanity>, dim3(grid), dim3(256), lds, st, a);
-      break;
-    case kPure:
-      hipLaunchKernelGGL(attn_kernel<kPure>, dim3(grid), dim3(256), lds, st, a);
-      break;
-    default:
-      hipLaunchKernelGGL(attn_kernel<kDense>, dim3(grid), dim3(256), lds, st, a);
-      break;
-  }
+  if (int rc = allow_lds<V, DT>(lds)) return rc;
+  hipLaunchKernelGGL((attn_kernel<V, DT>), dim3(grid), dim3(256), lds, st, a);
   return check_launch("attention kernel");
+}
+
+template <int DT>
+static int launch_attn_dt(int variant, AttnArgs& a, hipStream_t st) {
+  switch (variant) {
+    case kHybrid: return launch_attn_t<kHybrid, DT>(a, st);
+    case kSanity: return launch_attn_t<kSanity, DT>(a, st);
+    case kPure: return launch_attn_t<kPure, DT>(a, st);
+    default: return launch_attn_t<kDense, DT>(a, st);
+  }
+}
+
+static int launch_attn(int variant, int dtype, AttnArgs& a, hipStream_t st) {
+  return dtype == DA_F16 ? launch_attn_dt<DA_F16>(variant, a, st) : launch_attn_dt<DA_BF16>(variant, a, st);
 }
 
 static bool aligned16(const void* p) { return ((uintptr_t)p & 15) == 0; }
@@ -1200,7 +1175,8 @@ extern "C" int da_hybrid_prefill(const void* q, const void* k, const void* v, co
                                  const int32_t* num_packed_dev, int64_t window, float scale,
                                  int variant, int no_count, void* workspace,
                                  int64_t workspace_bytes, void* stream) {
-  if (dtype != DA_BF16) return set_error(DA_ERR_UNSUPPORTED, "da_hybrid_prefill: only bf16 is supported");
+  if (dtype != DA_BF16 && dtype != DA_F16)
+    return set_error(DA_ERR_UNSUPPORTED, "da_hybrid_prefill: tensors must be bf16 or fp16");
   AttnArgs a = {};
   int rc = fill_common(a, q, k, v, out, B, Hq, Hkv, Nq, Nk, D, strides, scale, "da_hybrid_prefill");
   if (rc) return rc;
@@ -1262,19 +1238,20 @@ extern "C" int da_hybrid_prefill(const void* q, const void* k, const void* v, co
   rc = check_launch("da_hybrid_prefill(schedule)");
   if (rc) return rc;
   const int kv = variant == DA_VARIANT_HYBRID ? kHybrid : (variant == DA_VARIANT_SANITY ? kSanity : kPure);
-  return launch_attn(kv, a, st);
+  return launch_attn(kv, dtype, a, st);
 }
 
 extern "C" int da_dense_prefill(const void* q, const void* k, const void* v, void* out, int dtype,
                                 int64_t B, int64_t Hq, int64_t Hkv, int64_t Nq, int64_t Nk,
                                 int64_t D, const int64_t* strides, int causal, float scale,
                                 void* stream) {
-  if (dtype != DA_BF16) return set_error(DA_ERR_UNSUPPORTED, "da_dense_prefill: only bf16 is supported");
+  if (dtype != DA_BF16 && dtype != DA_F16)
+    return set_error(DA_ERR_UNSUPPORTED, "da_dense_prefill: tensors must be bf16 or fp16");
   AttnArgs a = {};
   int rc = fill_common(a, q, k, v, out, B, Hq, Hkv, Nq, Nk, D, strides, scale, "da_dense_prefill");
   if (rc) return rc;
   a.kp = a.k; a.vp = a.v;
   a.causal = causal ? 1 : 0;
   a.P_host = 0;
-  return launch_attn(kDense, a, (hipStream_t)stream);
+  return launch_attn(kDense, dtype, a, (hipStream_t)stream);
 }

@@ -16,7 +16,8 @@
 // one wave scores a slice for all query heads of the group (the key and value rows
 // are read once per group), keeps the slice's max / sum / P.V partials, and the
 // combine kernel merges the slices exactly (rescaling by exp(m_s - M)).  As in the
-// reference, P is rounded to bf16 before the P.V product while the row sum stays fp32.
+// reference, P is rounded to the cache's 16-bit type before the P.V product while the
+// row sum stays fp32.  The cache is bf16 or fp16 (the E16 element type).
 #include "da_common.hpp"
 
 namespace da {
@@ -41,7 +42,7 @@ struct DecodeUpdateArgs {
   float thr;
 };
 
-template <bool COS>
+template <bool COS, int DT>
 __global__ __launch_bounds__(256) void decode_update_kernel(DecodeUpdateArgs a) {
 #pragma clang fp contract(off)
   const int lane = threadIdx.x & 63;
@@ -63,7 +64,7 @@ __global__ __launch_bounds__(256) void decode_update_kernel(DecodeUpdateArgs a) 
     bool merge = false;
     if (plen > 0) {                                                  // :61-77
       const uint32_t lk = act ? *(const uint32_t*)(pk + (int64_t)(plen - 1) * a.sp_s) : 0u;
-      const float e0 = bf16_lo(ek), e1 = bf16_hi(ek), l0 = bf16_lo(lk), l1 = bf16_hi(lk);
+      const float e0 = E16<DT>::lo(ek), e1 = E16<DT>::hi(ek), l0 = E16<DT>::lo(lk), l1 = E16<DT>::hi(lk);
       if (COS) {
         const float eps = 1e-8f;
         const float dot = wave_tree_sum(pair_dot(e0, e1, l0, l1));
@@ -140,7 +141,7 @@ __device__ __forceinline__ float wave_sum_all(float v) {
 // from LDS); the slice max and sum are wave reductions; for P.V lane l owns dims 2l and
 // 2l + 1 and the slice's 64 value rows are loaded together.  Small slices keep many
 // waves in flight per CU: the kernel is latency-bound at decode sizes.
-template <int G>
+template <int G, int DT>
 __global__ __launch_bounds__(64) void decode_attn_kernel(DecodeAttnArgs a) {
   __shared__ float s_q[G][kDecD];
   __shared__ float s_p[G][kDecSlice];
@@ -156,7 +157,7 @@ __global__ __launch_bounds__(64) void decode_attn_kernel(DecodeAttnArgs a) {
   for (int i = lane; i < G * kDecD; i += 64) {
     const int hh = i / kDecD, d = i - hh * kDecD;
     const uint16_t* qrow = a.q + b * a.sq_b + (int64_t)(g * G + hh) * a.sq_h;
-    s_q[hh][d] = __uint_as_float((uint32_t)qrow[d] << 16);
+    s_q[hh][d] = E16<DT>::one(qrow[d]);
   }
   __syncthreads();
 
@@ -188,7 +189,7 @@ __global__ __launch_bounds__(64) void decode_attn_kernel(DecodeAttnArgs a) {
       const u32x4 w = kw[c8];
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const float k0 = bf16_lo(w[e]), k1 = bf16_hi(w[e]);
+        const float k0 = E16<DT>::lo(w[e]), k1 = E16<DT>::hi(w[e]);
 #pragma unroll
         for (int hh = 0; hh < G; ++hh) {
           acc[hh] = __builtin_fmaf(s_q[hh][8 * c8 + 2 * e], k0, acc[hh]);
@@ -201,7 +202,7 @@ __global__ __launch_bounds__(64) void decode_attn_kernel(DecodeAttnArgs a) {
       if (hh < G) sc[hh] = acc[hh] * a.scale + bias;
   }
 
-  // ---- per-head slice max and sum; bf16-rounded weights to LDS ----
+  // ---- per-head slice max and sum; weights rounded to the cache's type, to LDS ----
   float* part = a.part + ((int64_t)bg * a.nslice + slice) * G * (kDecD + 2);
 #pragma unroll
   for (int hh = 0; hh < G; ++hh) {
@@ -209,7 +210,7 @@ __global__ __launch_bounds__(64) void decode_attn_kernel(DecodeAttnArgs a) {
       const float m = wave_max_all(sc[hh]);
       const float p = (sc[hh] == -INFINITY) ? 0.0f : __expf(sc[hh] - m);
       const float l = wave_sum_all(p);
-      s_p[hh][lane] = __uint_as_float((uint32_t)__builtin_bit_cast(uint16_t, (__bf16)p) << 16);
+      s_p[hh][lane] = E16<DT>::one(E16<DT>::bits(p));  // p rounded to the cache's type
       if (lane == 0) {
         part[hh * (kDecD + 2)] = m;
         part[hh * (kDecD + 2) + 1] = l;
@@ -233,7 +234,7 @@ __global__ __launch_bounds__(64) void decode_attn_kernel(DecodeAttnArgs a) {
   for (int hh = 0; hh < G; ++hh) av[hh][0] = av[hh][1] = 0.0f;
 #pragma unroll
   for (int u = 0; u < kDecSlice; ++u) {
-    const float v0 = bf16_lo(vw[u]), v1 = bf16_hi(vw[u]);
+    const float v0 = E16<DT>::lo(vw[u]), v1 = E16<DT>::hi(vw[u]);
 #pragma unroll
     for (int hh = 0; hh < G; ++hh)
       if (hh < G) {
@@ -255,6 +256,7 @@ __global__ __launch_bounds__(64) void decode_attn_kernel(DecodeAttnArgs a) {
 // are added in LDS.
 constexpr int kDecMaxSlices = 16384;
 constexpr int kCombUnroll = 32;
+template <int DT>
 __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeAttnArgs a) {
   __shared__ float s_f[kDecMaxSlices];
   __shared__ float s_red[4];
@@ -315,7 +317,7 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeAttnArgs a) {
   }
   if (q == 1) s_half[d] = acc;
   __syncthreads();
-  if (q == 0) a.out[b * a.so_b + hq * a.so_h + d] = __builtin_bit_cast(uint16_t, (__bf16)((acc + s_half[d]) / L));
+  if (q == 0) a.out[b * a.so_b + hq * a.so_h + d] = E16<DT>::bits((acc + s_half[d]) / L);
 }
 
 }  // namespace da
@@ -332,7 +334,8 @@ extern "C" int da_decode_update(const void* new_k, const void* new_v, int dtype,
                                 float threshold, int use_cosine, void* stream) {
   DA_REQUIRE(new_k && new_v && k_exact && v_exact && k_packed && v_packed && counts && timestamps && lengths,
              "da_decode_update: null pointer");
-  if (dtype != DA_BF16) return set_error(DA_ERR_UNSUPPORTED, "da_decode_update: only bf16 is supported");
+  if (dtype != DA_BF16 && dtype != DA_F16)
+    return set_error(DA_ERR_UNSUPPORTED, "da_decode_update: the cache must be bf16 or fp16");
   DA_REQUIRE(B > 0 && Hkv > 0 && window > 0 && capacity > 0, "da_decode_update: empty shape");
   if (D > 128 || (D & 1)) return set_error(DA_ERR_UNSUPPORTED, "da_decode_update: head_dim must be even and <= 128");
   DA_REQUIRE(exact_seq_len >= 0 && total_seq_len >= 0, "da_decode_update: negative lengths");
@@ -346,11 +349,32 @@ extern "C" int da_decode_update(const void* new_k, const void* new_v, int dtype,
   a.capacity = capacity; a.exact_len = exact_seq_len; a.total_len = total_seq_len; a.window = window;
   a.B = (int)B; a.H = (int)Hkv; a.D = (int)D; a.thr = threshold;
   const unsigned blocks = (unsigned)((B * Hkv + 3) / 4);
-  if (use_cosine)
-    hipLaunchKernelGGL(decode_update_kernel<true>, dim3(blocks), dim3(256), 0, (hipStream_t)stream, a);
-  else
-    hipLaunchKernelGGL(decode_update_kernel<false>, dim3(blocks), dim3(256), 0, (hipStream_t)stream, a);
+  hipStream_t st = (hipStream_t)stream;
+  if (dtype == DA_F16) {
+    if (use_cosine) hipLaunchKernelGGL((decode_update_kernel<true, DA_F16>), dim3(blocks), dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((decode_update_kernel<false, DA_F16>), dim3(blocks), dim3(256), 0, st, a);
+  } else {
+    if (use_cosine) hipLaunchKernelGGL((decode_update_kernel<true, DA_BF16>), dim3(blocks), dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((decode_update_kernel<false, DA_BF16>), dim3(blocks), dim3(256), 0, st, a);
+  }
   return check_launch("da_decode_update");
+}
+
+template <int DT>
+static int launch_decode(DecodeAttnArgs& a, dim3 agrid, int64_t n_heads, hipStream_t st) {
+  switch (a.G) {
+    case 1: hipLaunchKernelGGL((decode_attn_kernel<1, DT>), agrid, dim3(64), 0, st, a); break;
+    case 2: hipLaunchKernelGGL((decode_attn_kernel<2, DT>), agrid, dim3(64), 0, st, a); break;
+    case 3: hipLaunchKernelGGL((decode_attn_kernel<3, DT>), agrid, dim3(64), 0, st, a); break;
+    case 4: hipLaunchKernelGGL((decode_attn_kernel<4, DT>), agrid, dim3(64), 0, st, a); break;
+    case 5: hipLaunchKernelGGL((decode_attn_kernel<5, DT>), agrid, dim3(64), 0, st, a); break;
+    case 6: hipLaunchKernelGGL((decode_attn_kernel<6, DT>), agrid, dim3(64), 0, st, a); break;
+    case 7: hipLaunchKernelGGL((decode_attn_kernel<7, DT>), agrid, dim3(64), 0, st, a); break;
+    default: hipLaunchKernelGGL((decode_attn_kernel<8, DT>), agrid, dim3(64), 0, st, a); break;
+  }
+  if (int rc = check_launch("da_decode_attention")) return rc;
+  hipLaunchKernelGGL((decode_combine_kernel<DT>), dim3((unsigned)n_heads), dim3(256), 0, st, a);
+  return check_launch("da_decode_attention(combine)");
 }
 
 extern "C" int64_t da_decode_workspace_size(int64_t B, int64_t Hq, int64_t capacity, int64_t window) {
@@ -369,7 +393,8 @@ extern "C" int da_decode_attention(const void* q, int dtype, int64_t B, int64_t 
                                    int64_t workspace_bytes, void* stream) {
   DA_REQUIRE(q && k_packed && v_packed && counts && lengths && k_exact && v_exact && out,
              "da_decode_attention: null pointer");
-  if (dtype != DA_BF16) return set_error(DA_ERR_UNSUPPORTED, "da_decode_attention: only bf16 is supported");
+  if (dtype != DA_BF16 && dtype != DA_F16)
+    return set_error(DA_ERR_UNSUPPORTED, "da_decode_attention: the cache must be bf16 or fp16");
   if (D != kDecD) return set_error(DA_ERR_UNSUPPORTED, "da_decode_attention: head_dim must be 128");
   DA_REQUIRE(B > 0 && Hq > 0 && Hkv > 0 && Hq % Hkv == 0, "da_decode_attention: bad head counts");
   if (Hq / Hkv > kDecMaxG) return set_error(DA_ERR_UNSUPPORTED, "da_decode_attention: GQA group above %d", kDecMaxG);
@@ -393,18 +418,5 @@ extern "C" int da_decode_attention(const void* q, int dtype, int64_t B, int64_t 
   a.B = (int)B; a.Hq = (int)Hq; a.Hkv = (int)Hkv; a.G = (int)(Hq / Hkv);
   hipStream_t st = (hipStream_t)stream;
   const dim3 agrid((unsigned)(B * Hkv), (unsigned)a.nslice);
-  switch (a.G) {
-    case 1: hipLaunchKernelGGL(decode_attn_kernel<1>, agrid, dim3(64), 0, st, a); break;
-    case 2: hipLaunchKernelGGL(decode_attn_kernel<2>, agrid, dim3(64), 0, st, a); break;
-    case 3: hipLaunchKernelGGL(decode_attn_kernel<3>, agrid, dim3(64), 0, st, a); break;
-    case 4: hipLaunchKernelGGL(decode_attn_kernel<4>, agrid, dim3(64), 0, st, a); break;
-    case 5: hipLaunchKernelGGL(decode_attn_kernel<5>, agrid, dim3(64), 0, st, a); break;
-    case 6: hipLaunchKernelGGL(decode_attn_kernel<6>, agrid, dim3(64), 0, st, a); break;
-    case 7: hipLaunchKernelGGL(decode_attn_kernel<7>, agrid, dim3(64), 0, st, a); break;
-    default: hipLaunchKernelGGL(decode_attn_kernel<8>, agrid, dim3(64), 0, st, a); break;
-  }
-  int rc = check_launch("da_decode_attention");
-  if (rc) return rc;
-  hipLaunchKernelGGL(decode_combine_kernel, dim3((unsigned)(B * Hq)), dim3(256), 0, st, a);
-  return check_launch("da_decode_attention(combine)");
+  return dtype == DA_F16 ? launch_decode<DA_F16>(a, agrid, B * Hq, st) : launch_decode<DA_BF16>(a, agrid, B * Hq, st);
 }

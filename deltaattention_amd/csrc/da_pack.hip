@@ -244,7 +244,8 @@ extern "C" int da_pack(const int32_t* keep, const void* k, const void* v, int dt
   DA_REQUIRE(keep && k && v && k_packed && v_packed && timestamps && counts && anchor_counts &&
                  num_packed,
              "da_pack: null pointer");
-  if (dtype != DA_BF16) return set_error(DA_ERR_UNSUPPORTED, "da_pack: only bf16 is supported");
+  if (dtype != DA_BF16 && dtype != DA_F16)
+    return set_error(DA_ERR_UNSUPPORTED, "da_pack: K and V must be bf16 or fp16");
   DA_REQUIRE(B > 0 && Hkv > 0 && N > 0 && D > 0 && capacity > 0, "da_pack: empty shape");
   if (D > 128 || (D & 1)) return set_error(DA_ERR_UNSUPPORTED, "da_pack: head_dim must be even and <= 128");
   const int64_t ngroups = (N + 63) / 64;

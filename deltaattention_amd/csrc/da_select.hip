@@ -26,11 +26,11 @@ constexpr int kSelBatch = 32;
 
 // One key of the walk: the decision and the anchor update without a branch (the
 // decision is the same in every lane).
-template <bool COS>
+template <bool COS, int DT>
 __device__ __forceinline__ bool select_step(uint32_t xb, float& a0, float& a1, float& a_norm,
                                             float thr) {
 #pragma clang fp contract(off)
-  const float x0 = bf16_lo(xb), x1 = bf16_hi(xb);
+  const float x0 = E16<DT>::lo(xb), x1 = E16<DT>::hi(xb);
   const float eps = 1e-8f;
   bool kp;
   float x_norm = 0.0f;
@@ -49,7 +49,7 @@ __device__ __forceinline__ bool select_step(uint32_t xb, float& a0, float& a1, f
   return kp;
 }
 
-template <bool COS>
+template <bool COS, int DT>
 __global__ __launch_bounds__(256) void select_kernel(
     const uint16_t* __restrict__ k, int64_t sk_b, int64_t sk_h, int64_t sk_n, int H, int64_t N,
     int D, int64_t cs, int64_t nc, int64_t total_chunks, float thr, int32_t* __restrict__ keep,
@@ -76,7 +76,7 @@ __global__ __launch_bounds__(256) void select_kernel(
   };
 
   const uint32_t a_bits = row_bits(s);
-  float a0 = bf16_lo(a_bits), a1 = bf16_hi(a_bits);
+  float a0 = E16<DT>::lo(a_bits), a1 = E16<DT>::hi(a_bits);
   float a_norm = 0.0f;
   if (COS) a_norm = __fsqrt_rn(wave_tree_sum_all(pair_dot(a0, a1, a0, a1)) + 1e-8f);
   if (lane == 0) keep_row[s] = 1;  // row s is an anchor (tritonModules.py:41)
@@ -94,11 +94,11 @@ __global__ __launch_bounds__(256) void select_kernel(
     if (i0 + kSelBatch <= e) {
 #pragma unroll
       for (int j = 0; j < kSelBatch; ++j)
-        bb |= (uint32_t)select_step<COS>(cur[j], a0, a1, a_norm, thr) << j;
+        bb |= (uint32_t)select_step<COS, DT>(cur[j], a0, a1, a_norm, thr) << j;
     } else {
 #pragma unroll
       for (int j = 0; j < kSelBatch; ++j)
-        if (i0 + j < e) bb |= (uint32_t)select_step<COS>(cur[j], a0, a1, a_norm, thr) << j;
+        if (i0 + j < e) bb |= (uint32_t)select_step<COS, DT>(cur[j], a0, a1, a_norm, thr) << j;
     }
     count += __builtin_popcount(bb);  // tritonModules.py:68
     if (lane < kSelBatch && i0 + lane < e) keep_row[i0 + lane] = (int32_t)((bb >> lane) & 1u);
@@ -117,7 +117,8 @@ extern "C" int da_select(const void* k, int dtype, int64_t B, int64_t Hkv, int64
                          int64_t chunk_size, int64_t num_chunks, int32_t* keep,
                          int32_t* chunk_counts, void* stream) {
   DA_REQUIRE(k && keep && chunk_counts, "da_select: null pointer");
-  if (dtype != DA_BF16) return set_error(DA_ERR_UNSUPPORTED, "da_select: only bf16 keys are supported");
+  if (dtype != DA_BF16 && dtype != DA_F16)
+    return set_error(DA_ERR_UNSUPPORTED, "da_select: keys must be bf16 or fp16");
   DA_REQUIRE(B > 0 && Hkv > 0 && N > 0 && D > 0, "da_select: empty shape");
   if (D > 128 || (D & 1)) return set_error(DA_ERR_UNSUPPORTED, "da_select: head_dim must be even and <= 128 (got %lld)", (long long)D);
   DA_REQUIRE(chunk_size > 0 && num_chunks > 0, "da_select: chunk_size and num_chunks must be positive");
@@ -128,13 +129,17 @@ extern "C" int da_select(const void* k, int dtype, int64_t B, int64_t Hkv, int64
   const int64_t blocks = (total + 3) / 4;
   DA_REQUIRE(blocks < (1ll << 31), "da_select: too many chunks");
   hipStream_t st = (hipStream_t)stream;
-  if (use_cosine)
-    hipLaunchKernelGGL(select_kernel<true>, dim3((unsigned)blocks), dim3(256), 0, st,
-                       (const uint16_t*)k, sk_b, sk_h, sk_n, (int)Hkv, N, (int)D, chunk_size,
-                       num_chunks, total, threshold, keep, chunk_counts);
-  else
-    hipLaunchKernelGGL(select_kernel<false>, dim3((unsigned)blocks), dim3(256), 0, st,
-                       (const uint16_t*)k, sk_b, sk_h, sk_n, (int)Hkv, N, (int)D, chunk_size,
-                       num_chunks, total, threshold, keep, chunk_counts);
+#define DA_SELECT_LAUNCH(COS, DT)                                                                       \
+  hipLaunchKernelGGL((select_kernel<COS, DT>), dim3((unsigned)blocks), dim3(256), 0, st, (const uint16_t*)k, \
+                     sk_b, sk_h, sk_n, (int)Hkv, N, (int)D, chunk_size, num_chunks, total, threshold, keep,  \
+                     chunk_counts)
+  if (dtype == DA_F16) {
+    if (use_cosine) DA_SELECT_LAUNCH(true, DA_F16);
+    else DA_SELECT_LAUNCH(false, DA_F16);
+  } else {
+    if (use_cosine) DA_SELECT_LAUNCH(true, DA_BF16);
+    else DA_SELECT_LAUNCH(false, DA_BF16);
+  }
+#undef DA_SELECT_LAUNCH
   return check_launch("da_select");
 }

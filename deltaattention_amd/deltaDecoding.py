@@ -15,8 +15,8 @@ from typing import Optional
 import torch
 
 from . import globVR
-from ._launch import KernelLauncher, tensor, unit_stride
-from ._native import DA_BF16, check, lib
+from ._launch import HALF, KernelLauncher, tensor, unit_stride
+from ._native import check, dtype_code, lib
 
 try:  # transformers' Cache base (the reference subclasses it, deltaDecoding.py:2, 111)
     from transformers import Cache as _CacheBase
@@ -54,12 +54,12 @@ class _DecodeUpdate(KernelLauncher):
               "num_heads", "head_dim", "BLOCK_D", "USE_COSINE")
 
     def launch(self, grid, a):
-        nk = tensor(a, "new_k_ptr", torch.bfloat16)
-        nv = tensor(a, "new_v_ptr", torch.bfloat16)
-        kx = tensor(a, "k_exact_ptr", torch.bfloat16)
-        vx = tensor(a, "v_exact_ptr", torch.bfloat16)
-        kp = tensor(a, "k_packed_ptr", torch.bfloat16)
-        vp = tensor(a, "v_packed_ptr", torch.bfloat16)
+        nk = tensor(a, "new_k_ptr", HALF)
+        nv = tensor(a, "new_v_ptr", HALF)
+        kx = tensor(a, "k_exact_ptr", HALF)
+        vx = tensor(a, "v_exact_ptr", HALF)
+        kp = tensor(a, "k_packed_ptr", HALF)
+        vp = tensor(a, "v_packed_ptr", HALF)
         cnt = tensor(a, "packed_counts_ptr", torch.int32)
         ts = tensor(a, "packed_timestamps_ptr", torch.int32)
         lens = tensor(a, "packed_lengths_ptr", torch.int32)
@@ -69,7 +69,7 @@ class _DecodeUpdate(KernelLauncher):
             raise ValueError("grid[0] must be batch * num_heads")
         B = grid[0] // H
         rc = lib().da_decode_update(
-            nk.data_ptr(), nv.data_ptr(), DA_BF16, B, H, int(a["head_dim"]),
+            nk.data_ptr(), nv.data_ptr(), dtype_code(nk, nv, kx, vx, kp, vp), B, H, int(a["head_dim"]),
             int(a["stride_new_b"]), int(a["stride_new_h"]), kx.data_ptr(), vx.data_ptr(),
             int(a["stride_exact_b"]), int(a["stride_exact_h"]), int(a["stride_exact_s"]),
             kp.data_ptr(), vp.data_ptr(), int(a["stride_pack_b"]), int(a["stride_pack_h"]),
@@ -95,14 +95,14 @@ class _DecodeAttention(KernelLauncher):
               "head_dim", "BLOCK_M", "BLOCK_N", "BLOCK_D")
 
     def launch(self, grid, a):
-        q = tensor(a, "Q", torch.bfloat16)
-        kp = tensor(a, "K_packed", torch.bfloat16)
-        vp = tensor(a, "V_packed", torch.bfloat16)
+        q = tensor(a, "Q", HALF)
+        kp = tensor(a, "K_packed", HALF)
+        vp = tensor(a, "V_packed", HALF)
         cnt = tensor(a, "Packed_Counts", torch.int32)
         lens = tensor(a, "Packed_Lengths", torch.int32)
-        kx = tensor(a, "K_exact", torch.bfloat16)
-        vx = tensor(a, "V_exact", torch.bfloat16)
-        out = tensor(a, "Out", torch.bfloat16)
+        kx = tensor(a, "K_exact", HALF)
+        vx = tensor(a, "V_exact", HALF)
+        out = tensor(a, "Out", HALF)
         unit_stride(a, "stride_qd", "stride_kpd", "stride_vpd", "stride_cn", "stride_ked",
                     "stride_ved", "stride_od", "stride_lh")
         if (int(a["stride_kpb"]), int(a["stride_kph"]), int(a["stride_kpn"])) != \
@@ -130,7 +130,7 @@ def _decode_attention_launch(q, sq_b, sq_h, kp, vp, sp, cnt, sc, lens, kx, vx, s
     ws_bytes = lib().da_decode_workspace_size(B, Hq, capacity, window)
     ws = torch.empty((max(1, ws_bytes),), dtype=torch.uint8, device=q.device)
     rc = lib().da_decode_attention(
-        q.data_ptr(), DA_BF16, B, Hq, Hkv, D, sq_b, sq_h, kp.data_ptr(), vp.data_ptr(),
+        q.data_ptr(), dtype_code(q, kp, vp, kx, vx, out), B, Hq, Hkv, D, sq_b, sq_h, kp.data_ptr(), vp.data_ptr(),
         sp[0], sp[1], sp[2], cnt.data_ptr(), sc[0], sc[1], lens.data_ptr(), capacity,
         kx.data_ptr(), vx.data_ptr(), sx[0], sx[1], sx[2], window, exact_len,
         ctypes.c_float(scale), out.data_ptr(), so_b, so_h, ws.data_ptr(), ws_bytes, _stream())
@@ -230,7 +230,7 @@ class HybridCompressedCache(_CacheBase):
             value_states = value_states.contiguous()
             key_states = key_states.contiguous()
         rc = lib().da_decode_update(
-            key_states.data_ptr(), value_states.data_ptr(), DA_BF16, self.bsz, self.n_kv_heads,
+            key_states.data_ptr(), value_states.data_ptr(), dtype_code(key_states, value_states, kx, vx, kp, vp), self.bsz, self.n_kv_heads,
             self.head_dim, key_states.stride(0), key_states.stride(1), kx.data_ptr(), vx.data_ptr(),
             kx.stride(0), kx.stride(1), kx.stride(2), kp.data_ptr(), vp.data_ptr(), kp.stride(0),
             kp.stride(1), kp.stride(2), cnt.data_ptr(), ts.data_ptr(), cnt.stride(0), cnt.stride(1),

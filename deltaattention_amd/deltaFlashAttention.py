@@ -13,8 +13,8 @@ import ctypes
 
 import torch
 
-from ._launch import KernelLauncher, tensor, unit_stride
-from ._native import DA_BF16, DA_F32, DA_I32, DA_VARIANT, check, lib, strides_array
+from ._launch import HALF, KernelLauncher, tensor, unit_stride
+from ._native import DA_F32, DA_I32, DA_VARIANT, check, dtype_code, lib, strides_array
 
 __all__ = ["hybrid_compressed_flash_kernel", "hybrid_compressed_flash_kernel_sanity",
            "pure_phase1_flash_kernel"]
@@ -45,14 +45,14 @@ class _HybridKernel(KernelLauncher):
             raise NotImplementedError(
                 f"{self.NAME}: the schedule is defined on 128x128 logical blocks "
                 "(BLOCK_M = BLOCK_N = 128, modeling_llama.py:328-329)")
-        q = tensor(a, "Q", torch.bfloat16)
-        kd = tensor(a, "K_dense", torch.bfloat16)
-        vd = tensor(a, "V_dense", torch.bfloat16)
-        kp = tensor(a, "K_packed", torch.bfloat16)
-        vp = tensor(a, "V_packed", torch.bfloat16)
+        q = tensor(a, "Q", HALF)
+        kd = tensor(a, "K_dense", HALF)
+        vd = tensor(a, "V_dense", HALF)
+        kp = tensor(a, "K_packed", HALF)
+        vp = tensor(a, "V_packed", HALF)
         ts = tensor(a, "Packed_Timestamps", torch.int32)
         cnt = tensor(a, "Packed_Counts")
-        out = tensor(a, "Out", torch.bfloat16)
+        out = tensor(a, "Out", HALF)
         if cnt.dtype not in (torch.float32, torch.int32):
             raise TypeError("Packed_Counts must be float32 or int32")
         unit_stride(a, "stride_qd", "stride_kdd", "stride_vdd", "stride_kpd", "stride_vpd",
@@ -73,7 +73,7 @@ class _HybridKernel(KernelLauncher):
         rc = lib().da_hybrid_prefill(
             q.data_ptr(), kd.data_ptr(), vd.data_ptr(), kp.data_ptr(), vp.data_ptr(),
             ts.data_ptr(), cnt.data_ptr(), DA_F32 if cnt.dtype == torch.float32 else DA_I32,
-            out.data_ptr(), DA_BF16, B, H, H, nq, nk, D, st, P, None, int(a["denseWindowSize"]),
+            out.data_ptr(), dtype_code(q, kd, vd, kp, vp, out), B, H, H, nq, nk, D, st, P, None, int(a["denseWindowSize"]),
             ctypes.c_float(float(a["sm_scale"])), DA_VARIANT[self.variant], 0, ws.data_ptr(),
             ws_bytes, ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))
         check(rc, self.NAME)

@@ -10,8 +10,8 @@ import ctypes
 import torch
 
 from . import ops
-from ._launch import KernelLauncher, tensor, unit_stride
-from ._native import DA_BF16, check, lib, strides_array
+from ._launch import HALF, KernelLauncher, tensor, unit_stride
+from ._native import check, dtype_code, lib, strides_array
 
 __all__ = ["triton_flash_attention", "_attn_fwd_flat"]
 
@@ -32,10 +32,10 @@ class _AttnFwdFlat(KernelLauncher):
               "Z", "H", "N_CTX", "HEAD_DIM", "BLOCK_M", "BLOCK_N", "IS_CAUSAL")
 
     def launch(self, grid, a):
-        q = tensor(a, "Q", torch.bfloat16)
-        k = tensor(a, "K", torch.bfloat16)
-        v = tensor(a, "V", torch.bfloat16)
-        o = tensor(a, "Out", torch.bfloat16)
+        q = tensor(a, "Q", HALF)
+        k = tensor(a, "K", HALF)
+        v = tensor(a, "V", HALF)
+        o = tensor(a, "Out", HALF)
         unit_stride(a, "stride_qk", "stride_kk", "stride_vn", "stride_on")
         Z, H, N, D = int(a["Z"]), int(a["H"]), int(a["N_CTX"]), int(a["HEAD_DIM"])
         st = strides_array([a["stride_qz"], a["stride_qh"], a["stride_qm"],
@@ -43,7 +43,7 @@ class _AttnFwdFlat(KernelLauncher):
                             a["stride_vz"], a["stride_vh"], a["stride_vk"],
                             0, 0, 0, 0, 0, 0,
                             a["stride_oz"], a["stride_oh"], a["stride_om"]] + [0] * 6)
-        rc = lib().da_dense_prefill(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), DA_BF16,
+        rc = lib().da_dense_prefill(q.data_ptr(), k.data_ptr(), v.data_ptr(), o.data_ptr(), dtype_code(q, k, v, o),
                                     Z, H, H, N, N, D, st, 1 if a["IS_CAUSAL"] else 0,
                                     ctypes.c_float(float(a["sm_scale"])),
                                     ctypes.c_void_p(torch.cuda.current_stream().cuda_stream))

@@ -17,7 +17,7 @@ from typing import Optional, Tuple
 import torch
 
 from . import _native
-from ._native import DA_BF16, DA_F32, DA_I32, DA_VARIANT, check, lib, strides_array
+from ._native import DA_F32, DA_I32, DA_VARIANT, check, dtype_code, lib, strides_array
 
 __all__ = ["PackedKV", "chunking", "select", "pack", "hybrid_prefill", "dense_prefill",
            "delta_prefill"]
@@ -38,10 +38,9 @@ def _require_device(*ts: torch.Tensor) -> None:
                              f"(got a tensor on {t.device}); there is no CPU path")
 
 
-def _require_bf16(*ts: torch.Tensor) -> None:
-    for t in ts:
-        if t.dtype != torch.bfloat16:
-            raise TypeError(f"expected bfloat16 tensors, got {t.dtype}")
+def _require_half(*ts: torch.Tensor) -> int:
+    """The library's code of the one 16-bit dtype (bf16 or fp16) the tensors share."""
+    return dtype_code(*ts)
 
 
 def _last_dim_contig(t: torch.Tensor) -> torch.Tensor:
@@ -70,7 +69,7 @@ def select(k: torch.Tensor, threshold: float, chunk_size: int = 512, divide_to: 
     [B, Hkv, num_chunks] int32.
     """
     _require_device(k)
-    _require_bf16(k)
+    dt = _require_half(k)
     k = _last_dim_contig(k)
     B, H, N, D = k.shape
     cs, nc = chunking(N, chunk_size, divide_to)
@@ -80,7 +79,7 @@ def select(k: torch.Tensor, threshold: float, chunk_size: int = 512, divide_to: 
         keep = torch.zeros((B, H, N), dtype=torch.int32, device=k.device)
     if chunk_counts is None:
         chunk_counts = torch.empty((B, H, nc), dtype=torch.int32, device=k.device)
-    rc = lib().da_select(k.data_ptr(), DA_BF16, B, H, N, D, k.stride(0), k.stride(1), k.stride(2),
+    rc = lib().da_select(k.data_ptr(), dt, B, H, N, D, k.stride(0), k.stride(1), k.stride(2),
                          ctypes.c_float(thr), 1 if use_cos else 0, cs, nc, keep.data_ptr(),
                          chunk_counts.data_ptr(), _stream())
     check(rc, "da_select")
@@ -123,7 +122,7 @@ def pack(keep: torch.Tensor, k: torch.Tensor, v: torch.Tensor, capacity: Optiona
     anchor, so nothing waits for P on the host.
     """
     _require_device(keep, k, v)
-    _require_bf16(k, v)
+    dt = _require_half(k, v)
     k, v = _last_dim_contig(k), _last_dim_contig(v)
     keep = keep.contiguous()
     if keep.dtype != torch.int32:
@@ -145,7 +144,7 @@ def pack(keep: torch.Tensor, k: torch.Tensor, v: torch.Tensor, capacity: Optiona
             raise ValueError("packed outputs must be contiguous")
     ws_bytes = lib().da_pack_workspace_size(B, H, N)
     ws = torch.empty((max(1, ws_bytes),), dtype=torch.uint8, device=dev)
-    rc = lib().da_pack(keep.data_ptr(), k.data_ptr(), v.data_ptr(), DA_BF16, B, H, N, D,
+    rc = lib().da_pack(keep.data_ptr(), k.data_ptr(), v.data_ptr(), dt, B, H, N, D,
                        k.stride(0), k.stride(1), k.stride(2), v.stride(0), v.stride(1),
                        v.stride(2), out.capacity, out.k_packed.data_ptr(), out.v_packed.data_ptr(),
                        out.timestamps.data_ptr(), out.counts.data_ptr(),
@@ -179,7 +178,7 @@ def hybrid_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, k_packed: 
     if variant not in DA_VARIANT:
         raise ValueError(f"variant must be one of {sorted(DA_VARIANT)}")
     _require_device(q, k, v, k_packed, v_packed, timestamps, counts)
-    _require_bf16(q, k, v, k_packed, v_packed)
+    dt = _require_half(q, k, v, k_packed, v_packed)
     q, k, v = _last_dim_contig(q), _last_dim_contig(k), _last_dim_contig(v)
     k_packed, v_packed = _last_dim_contig(k_packed), _last_dim_contig(v_packed)
     timestamps = _last_dim_contig(timestamps)
@@ -195,13 +194,14 @@ def hybrid_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, k_packed: 
         scale = D ** -0.5
     if out is None:
         out = torch.empty_like(q)
+    dtype_code(q, out)
     ws_bytes = lib().da_hybrid_workspace_size(B, Hkv, max(P, 1))
     ws = torch.empty((max(1, ws_bytes),), dtype=torch.uint8, device=q.device)
     st = _attn_strides(q, k, v, out, k_packed, v_packed, timestamps, counts)
     rc = lib().da_hybrid_prefill(
         q.data_ptr(), k.data_ptr(), v.data_ptr(), k_packed.data_ptr(), v_packed.data_ptr(),
         timestamps.data_ptr(), counts.data_ptr(),
-        DA_F32 if counts.dtype == torch.float32 else DA_I32, out.data_ptr(), DA_BF16,
+        DA_F32 if counts.dtype == torch.float32 else DA_I32, out.data_ptr(), dt,
         B, Hq, Hkv, Nq, Nk, D, st, P, _ptr(num_packed_dev), int(window), ctypes.c_float(scale),
         DA_VARIANT[variant], 1 if no_count else 0, ws.data_ptr(), ws_bytes, _stream())
     check(rc, "da_hybrid_prefill")
@@ -212,7 +212,7 @@ def dense_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: boo
                   scale: Optional[float] = None, out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Dense flash prefill (flashAttention.py:5-130) with GQA indexing."""
     _require_device(q, k, v)
-    _require_bf16(q, k, v)
+    dt = _require_half(q, k, v)
     q, k, v = _last_dim_contig(q), _last_dim_contig(k), _last_dim_contig(v)
     B, Hq, Nq, D = q.shape
     Hkv, Nk = k.shape[1], k.shape[2]
@@ -220,8 +220,9 @@ def dense_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: boo
         scale = D ** -0.5
     if out is None:
         out = torch.empty_like(q)
+    dtype_code(q, out)
     st = _attn_strides(q, k, v, out)
-    rc = lib().da_dense_prefill(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), DA_BF16,
+    rc = lib().da_dense_prefill(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), dt,
                                 B, Hq, Hkv, Nq, Nk, D, st, 1 if causal else 0,
                                 ctypes.c_float(scale), _stream())
     check(rc, "da_dense_prefill")

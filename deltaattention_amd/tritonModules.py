@@ -9,8 +9,8 @@ import ctypes
 
 import torch
 
-from ._launch import KernelLauncher, tensor, unit_stride
-from ._native import DA_BF16, check, lib
+from ._launch import HALF, KernelLauncher, tensor, unit_stride
+from ._native import check, dtype_code, lib
 
 __all__ = ["chunked_eval_kernel", "parallel_scatter_pack_kv_kernel"]
 
@@ -35,7 +35,7 @@ class _ChunkedEval(KernelLauncher):
               "seq_len", "head_dim", "chunk_size", "num_heads", "BLOCK_D", "USE_COSINE")
 
     def launch(self, grid, a):
-        k = tensor(a, "in_ptr", torch.bfloat16)
+        k = tensor(a, "in_ptr", HALF)
         keep = tensor(a, "keep_mask_ptr", torch.int32)
         cc = tensor(a, "chunk_counts_ptr", torch.int32)
         unit_stride(a, "stride_in_d")
@@ -47,7 +47,7 @@ class _ChunkedEval(KernelLauncher):
             raise ValueError("keep_mask must be a contiguous [B, H, N] tensor")
         if (int(a["stride_cc_c"]), int(a["stride_cc_h"]), int(a["stride_cc_b"])) != (1, nc, H * nc):
             raise ValueError("chunk_counts must be a contiguous [B, H, num_chunks] tensor")
-        rc = lib().da_select(k.data_ptr(), DA_BF16, B, H, N, D, int(a["stride_in_b"]),
+        rc = lib().da_select(k.data_ptr(), dtype_code(k), B, H, N, D, int(a["stride_in_b"]),
                              int(a["stride_in_h"]), int(a["stride_in_s"]),
                              ctypes.c_float(float(a["threshold_sq"])), 1 if a["USE_COSINE"] else 0,
                              int(a["chunk_size"]), nc, keep.data_ptr(), cc.data_ptr(), _stream())
@@ -78,10 +78,10 @@ class _ScatterPack(KernelLauncher):
               "seq_len", "head_dim", "num_heads", "BLOCK_S", "BLOCK_D")
 
     def launch(self, grid, a):
-        k = tensor(a, "k_in_ptr", torch.bfloat16)
-        v = tensor(a, "v_in_ptr", torch.bfloat16)
-        kp = tensor(a, "k_packed_ptr", torch.bfloat16)
-        vp = tensor(a, "v_packed_ptr", torch.bfloat16)
+        k = tensor(a, "k_in_ptr", HALF)
+        v = tensor(a, "v_in_ptr", HALF)
+        kp = tensor(a, "k_packed_ptr", HALF)
+        vp = tensor(a, "v_packed_ptr", HALF)
         ts = tensor(a, "pt_ptr", torch.int32)
         keep = tensor(a, "keep_mask_ptr")
         unit_stride(a, "stride_kd", "stride_vd", "stride_kpd", "stride_vpd")
@@ -100,7 +100,7 @@ class _ScatterPack(KernelLauncher):
         num = torch.empty((1,), dtype=torch.int32, device=k.device)
         ws_bytes = lib().da_pack_workspace_size(B, H, N)
         ws = torch.empty((max(1, ws_bytes),), dtype=torch.uint8, device=k.device)
-        rc = lib().da_pack(keep.data_ptr(), k.data_ptr(), v.data_ptr(), DA_BF16, B, H, N, D,
+        rc = lib().da_pack(keep.data_ptr(), k.data_ptr(), v.data_ptr(), dtype_code(k, v, kp, vp), B, H, N, D,
                            int(a["stride_kb"]), int(a["stride_kh"]), int(a["stride_ks"]),
                            int(a["stride_vb"]), int(a["stride_vh"]), int(a["stride_vs"]), P,
                            kp.data_ptr(), vp.data_ptr(), ts.data_ptr(), counts.data_ptr(),

@@ -32,6 +32,7 @@ extern "C" {
 
 /* element types */
 #define DA_BF16 1
+#define DA_F16 2
 #define DA_I32 3
 #define DA_F32 4
 
@@ -50,7 +51,8 @@ int da_version(void);
  * Delta-mode anchor selection.  Replaces chunked_eval_kernel
  * (tritonModules.py:7-69) and its launch (modeling_llama.py:634-653).
  *
- * k: [B, Hkv, N, D] bf16, strides (sk_b, sk_h, sk_n), D even and <= 128.
+ * k: [B, Hkv, N, D] bf16 or fp16 (dtype DA_BF16 / DA_F16), strides (sk_b, sk_h, sk_n),
+ * D even and <= 128.
  * threshold: tau^2 for Euclidean, tau for cosine (modeling_llama.py:641-642).
  * chunk_size / num_chunks: from the chunking rule of modeling_llama.py:602-610.
  * keep: [B, Hkv, N] int32 contiguous, 1 for anchors and 0 otherwise (rows of
@@ -72,7 +74,7 @@ int da_select(const void* k, int dtype, int64_t B, int64_t Hkv, int64_t N, int64
  *
  * keep: [B, Hkv, N] int32 contiguous; keep[..., 0] must be 1 (every mode of the
  *   reference guarantees it, modeling_llama.py:623/630 and tritonModules.py:41).
- * k, v: [B, Hkv, N, D] bf16 with strides (s*_b, s*_h, s*_n).
+ * k, v: [B, Hkv, N, D] bf16 or fp16 (dtype) with strides (s*_b, s*_h, s*_n).
  * capacity: rows allocated per head in the packed outputs; must be >= P
  *   (N always suffices).
  * k_packed, v_packed: [B, Hkv, capacity, D] contiguous; rows [0, c) receive the
@@ -96,8 +98,9 @@ int da_pack(const int32_t* keep, const void* k, const void* v, int dtype, int64_
  * including the repeat_kv expansion (:701-708): query head h reads KV head
  * h / (Hq / Hkv) directly.
  *
- * q, out: [B, Hq, Nq, D] bf16; k, v: [B, Hkv, Nk, D] bf16;
- * k_packed, v_packed: [B, Hkv, >=P, D] bf16; timestamps: [B, Hkv, >=P] int32;
+ * q, out: [B, Hq, Nq, D]; k, v: [B, Hkv, Nk, D]; k_packed, v_packed: [B, Hkv, >=P, D], all
+ * of one 16-bit type (dtype DA_BF16 or DA_F16; P is rounded to it before P.V, as
+ * deltaFlashAttention.py:98, 137 round p to V's type); timestamps: [B, Hkv, >=P] int32;
  * counts: [B, Hkv, >=P] int32 or fp32 (counts_dtype DA_I32 / DA_F32).
  * num_packed: P (rows of the packed tensors that are read); if num_packed_dev
  *   is non-null the device value is used instead (it must be <= num_packed).
@@ -131,7 +134,7 @@ int da_dense_prefill(const void* q, const void* k, const void* v, void* out, int
  * Decode step of the compressed cache.  Replaces fused_hybrid_decode_update_kernel
  * (deltaDecoding.py:9-104) as launched by HybridCompressedCache.update (:181-211).
  *
- * new_k, new_v: [B, Hkv, 1, D] bf16 (strides sn_b, sn_h).
+ * new_k, new_v: [B, Hkv, 1, D] bf16 or fp16 like the cache (strides sn_b, sn_h).
  * k_exact, v_exact: ring [B, Hkv, W, D] (strides sx_*); k_packed, v_packed:
  *   [B, Hkv, capacity, D] (strides sp_*); counts, timestamps: [B, Hkv, capacity]
  *   int32 (strides sc_b, sc_h, packed axis contiguous); lengths: [B * Hkv] int32.
@@ -154,7 +157,8 @@ int da_decode_update(const void* new_k, const void* new_v, int dtype, int64_t B,
  * q_len = 1 attention over the compressed cache.  Replaces fused_hybrid_decode_kernel
  * (deltaDecoding.py:236-362) and its wrapper (modeling_llama.py:453-518).
  *
- * q: [B, Hq, D] bf16 (strides sq_b, sq_h); query head h reads kv head h / (Hq / Hkv).
+ * q: [B, Hq, D] bf16 or fp16 like the cache (strides sq_b, sq_h); query head h reads kv
+ * head h / (Hq / Hkv).
  * Scores over the packed anchors [0, lengths[b*Hkv + g]) get + log(count); then the
  * ring slots [0, exact_len) (exact_len = min(exact_seq_len, W)).  out: [B, Hq, D]
  * (strides so_b, so_h).  D must be 128, Hq / Hkv <= 8.

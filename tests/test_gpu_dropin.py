@@ -170,15 +170,16 @@ def O_decode_state(B, H, D, cap, W):
             "v_exact": np.zeros((B, H, W, D), np.float32), "exact_len": 0, "total_len": 0, "window": W}
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
 @pytest.mark.parametrize("metric,tau", [("euclidean", 9.5), ("cosine", 0.9)])
-def test_decode_cache_matches_oracle(gpu, metric, tau):
+def test_decode_cache_matches_oracle(gpu, metric, tau, dtype):
     """Prefill hand-off then 80 decode steps: cache state bit-exact and attention within
     tolerance against the oracle (deltaDecoding.py:9-362, modeling_llama.py:453-518)."""
     from types import SimpleNamespace
     from deltaattention_amd import attention, globVR, synth
     from deltaattention_amd.deltaDecoding import HybridCompressedCache, decode_attention
     B, Hq, Hkv, N, W, steps = 1, 8, 2, 700, 50, 80
-    q, k, v = _inputs(B, Hq, Hkv, N + steps, 5)
+    q, k, v = (t.to(dtype) for t in _inputs(B, Hq, Hkv, N + steps, 5))
     cfg = SimpleNamespace(hidden_size=Hq * 128, num_attention_heads=Hq, num_key_value_heads=Hkv,
                           num_hidden_layers=1, head_dim=128)
     saved = dict(vars(globVR))
@@ -186,7 +187,7 @@ def test_decode_cache_matches_oracle(gpu, metric, tau):
         globVR.packing_mode, globVR.chunk_size = "delta", 512
         globVR.row_delta_threshold, globVR.row_similarity_metric = tau, metric
         globVR.time_internal = False
-        cache = HybridCompressedCache(cfg, B, dtype=torch.bfloat16, exact_window_size=W,
+        cache = HybridCompressedCache(cfg, B, dtype=dtype, exact_window_size=W,
                                       initial_capacity=64)
         qg, kg, vg = q.to(gpu), k.to(gpu), v.to(gpu)
         announce(f"decode {metric}: prefill hand-off")
@@ -198,7 +199,7 @@ def test_decode_cache_matches_oracle(gpu, metric, tau):
         outs = []
         for t in range(steps):
             if t == 0:
-                announce(f"decode {metric}: {steps} update+attention steps")
+                announce(f"decode {metric} {dtype}: {steps} update+attention steps")
             cache.update(kg[:, :, N + t:N + t + 1], vg[:, :, N + t:N + t + 1], 0)
             outs.append(decode_attention(qg[:, :, N + t:N + t + 1], cache, 0))
             O.decode_update(st, kf[:, :, N + t:N + t + 1], vf[:, :, N + t:N + t + 1], tau, metric)

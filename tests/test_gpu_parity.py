@@ -245,3 +245,74 @@ def test_phase1_extent_full_size(gpu, Hq):
     err = np.abs(got[..., 0] - want0[None, :])
     print(f"phase-1 extent: max-abs {err.max():.3e}", flush=True)
     assert err.max() <= 4e-3   # bf16 rounding of values in [0, 1]
+
+
+# --------------------------------------------------------------------------------------
+# fp16 inputs: the same kernels on the other 16-bit type (P rounded to fp16 before P.V,
+# as the reference rounds p to V's type, deltaFlashAttention.py:98, 137)
+# --------------------------------------------------------------------------------------
+def _f16_inputs(B, Hq, Hkv, N, D, seed):
+    q, k, v = _bf16_inputs(B, Hq, Hkv, N, D, seed)
+    return q.half(), k.half(), v.half()
+
+
+@pytest.mark.parametrize("metric,tau", [("euclidean", 9.0), ("cosine", 0.85)])
+def test_select_bitexact_fp16(gpu, metric, tau):
+    from deltaattention_amd import ops
+    _, k, _ = _f16_inputs(2, 4, 2, 1500, 128, seed=21)
+    announce(f"select fp16 {metric} tau={tau}")
+    keep, counts = ops.select(k.to(gpu), tau, 512, 0, metric)
+    ref_keep, ref_counts = OC.select_delta(k.float().numpy(), tau, 512, 0, metric)
+    assert np.array_equal(keep.cpu().numpy(), ref_keep)
+    assert np.array_equal(counts.cpu().numpy(), ref_counts)
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,N,tau,W,variant", [
+    (1, 8, 2, 2048, 10.0, 128, "hybrid"),
+    (1, 4, 2, 1100, 8.0, 300, "hybrid"),
+    (2, 8, 2, 1024, 10.0, 128, "sanity"),
+    (1, 8, 2, 2048, 1e6, 128, "pure_phase1"),
+])
+def test_delta_prefill_fp16_vs_oracle(gpu, B, Hq, Hkv, N, tau, W, variant):
+    from deltaattention_amd import ops
+    q, k, v = _f16_inputs(B, Hq, Hkv, N, 128, seed=N + 7)
+    announce(f"delta_prefill fp16 B={B} Hq={Hq} Hkv={Hkv} N={N} {variant}")
+    out = ops.delta_prefill(q.to(gpu), k.to(gpu), v.to(gpu), tau, 512, window=W, variant=variant)
+    assert out.dtype == torch.float16
+    kf, vf = k.float().numpy(), v.float().numpy()
+    keep, _ = OC.select_delta(kf, tau, 512)
+    p = O.pack(kf, vf, keep)
+    ref = O.hybrid_attention(q.float().numpy(), kf, vf, p["k_packed"], p["v_packed"],
+                             p["timestamps"], p["counts"], W, variant=variant)
+    _close(out.float().cpu().numpy(), ref, f"delta fp16 {variant} N={N}")
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,N", [(1, 8, 2, 700), (1, 6, 3, 384)])
+def test_dense_fp16_vs_oracle(gpu, B, Hq, Hkv, N):
+    from deltaattention_amd import ops
+    q, k, v = _f16_inputs(B, Hq, Hkv, N, 128, seed=4)
+    announce(f"dense fp16 B={B} Hq={Hq} Hkv={Hkv} N={N}")
+    out = ops.dense_prefill(q.to(gpu), k.to(gpu), v.to(gpu))
+    assert out.dtype == torch.float16
+    ref = O.dense_attention(q.float().numpy(), k.float().numpy(), v.float().numpy(), True)
+    _close(out.float().cpu().numpy(), ref, f"dense fp16 N={N}")
+
+
+def test_keep_all_fp16_hybrid_equals_dense(gpu):
+    from deltaattention_amd import ops
+    q, k, v = _f16_inputs(1, 4, 1, 40960, 128, seed=5)
+    qg, kg, vg = q.to(gpu), k.to(gpu), v.to(gpu)
+    announce("keep-all fp16 hybrid vs dense N=40960")
+    keep, _ = ops.select(kg, 0.0, 512)
+    pk = ops.pack(keep, kg, vg)
+    hyb = ops.hybrid_prefill(qg, kg, vg, pk.k_packed, pk.v_packed, pk.timestamps, pk.counts,
+                             window=128, num_packed_dev=pk.num_packed)
+    dense = ops.dense_prefill(qg, kg, vg)
+    _close(hyb.float().cpu().numpy(), dense.float().cpu().numpy(), "keep-all fp16")
+
+
+def test_mixed_dtypes_are_rejected(gpu):
+    from deltaattention_amd import ops
+    q, k, v = _bf16_inputs(1, 4, 1, 256, 128, seed=1)
+    with pytest.raises(TypeError):
+        ops.dense_prefill(q.to(gpu), k.half().to(gpu), v.to(gpu))
