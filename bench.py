@@ -47,6 +47,8 @@ def parse_args():
     ap.add_argument("--seq", type=int, default=0, help="override the sequence length")
     ap.add_argument("--window", type=int, default=128)
     ap.add_argument("--seed", type=int, default=0)
+    ap.add_argument("--dtype", choices=("bf16", "fp16"), default="bf16",
+                    help="16-bit type of Q, K, V (configs 1 and 2); bf16 is the headline")
     ap.add_argument("--only", choices=("delta", "hybrid", "dense", "compress", "copy"), default=None,
                     help="run one part for K steps (copy: a 1 GiB device copy, the reference for "
                          "calibrating the FETCH_SIZE / WRITE_SIZE counters)")
@@ -410,7 +412,8 @@ def main():
     W = args.window
     log(f"config {args.config}: N={N} r={args.ratio} W={W}")
     q, k, v = synth.make_layer_inputs(B, Hq, Hkv, N, D, rope_base=500000.0, seed=args.seed,
-                                      device=dev, qv_on_device=True)
+                                      device=dev, qv_on_device=True,
+                                      dtype=torch.float16 if args.dtype == "fp16" else torch.bfloat16)
     torch.cuda.synchronize()
     tau, r_real = synth.calibrate_threshold(k, args.ratio)
     log(f"calibrated tau={tau:.4f} realised r={r_real:.3f}")
@@ -504,12 +507,12 @@ def main():
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "bf16",
+        "dtype": args.dtype,
         "data": (f"synthetic: AR(1) keys rho=0.9 sigma=0.44 + RoPE base 5e5, Gaussian Q/V, "
                  f"seed {args.seed}; Euclidean tau={tau:.4f} calibrated to r={args.ratio:g} "
                  f"(realised {r_real:.3f}), chunk 512, W={W}"),
         "config": {"workload": (f"config{args.config}: delta prefill attention, one layer, "
-                                f"B={B} Hq={Hq} Hkv={Hkv} D={D} N={N} bf16 causal r={args.ratio:g}"),
+                                f"B={B} Hq={Hq} Hkv={Hkv} D={D} N={N} {args.dtype} causal r={args.ratio:g}"),
                    "seq_len": N, "global_batch": B, "parallelism": "none (1 GPU)"},
         "speedup_vs_dense": round(ms_dense / ms_step, 3),
         "kernel_speedup_vs_dense": round(ms_dense / ms_hybrid, 3),
