@@ -136,11 +136,14 @@ __device__ __forceinline__ float wave_sum_all(float v) {
   return v;
 }
 
-// One wave per (batch, kv head, 64-key slice).  Lane t scores key j0 + t for every
-// query head of the group (its whole 256-byte key row in flight at once, q broadcast
-// from LDS); the slice max and sum are wave reductions; for P.V lane l owns dims 2l and
-// 2l + 1 and the slice's 64 value rows are loaded together.  Small slices keep many
-// waves in flight per CU: the kernel is latency-bound at decode sizes.
+// One wave per (batch, kv head, 64-key slice).  After the length of the list, lane t's
+// whole 256-byte key row and the group's query rows are loaded together; the slice's
+// 64 value rows are issued as soon as the scores are done and arrive during the
+// softmax.  Lane t scores key j0 + t for every query head of the group (q broadcast
+// from LDS); the slice max and sum are wave reductions; for P.V lane l owns dims 2l
+// and 2l + 1.  Small slices keep many waves in flight per CU: the kernel is
+// latency-bound at decode sizes, and holding K and V rows at once would halve the
+// waves per SIMD.
 template <int G, int DT>
 __global__ __launch_bounds__(64) void decode_attn_kernel(DecodeAttnArgs a) {
   __shared__ float s_q[G][kDecD];
@@ -154,33 +157,40 @@ __global__ __launch_bounds__(64) void decode_attn_kernel(DecodeAttnArgs a) {
   const int j0 = slice * kDecSlice;
   if (j0 >= total) return;  // the combine kernel skips slices past the end
 
-  for (int i = lane; i < G * kDecD; i += 64) {
-    const int hh = i / kDecD, d = i - hh * kDecD;
-    const uint16_t* qrow = a.q + b * a.sq_b + (int64_t)(g * G + hh) * a.sq_h;
-    s_q[hh][d] = E16<DT>::one(qrow[d]);
+  // This lane's key row and count and the group's query rows (G * D / 64 elements per
+  // lane) go out together, before the first wait.
+  const int j = j0 + lane;
+  const bool valid = j < total;
+  u32x4 kw[kDecD / 8];
+  int cnt = 1;
+  if (valid) {
+    const uint16_t* krow = j < plen ? a.kp + b * a.sp_b + g * a.sp_h + (int64_t)j * a.sp_s
+                                    : a.kx + b * a.sx_b + g * a.sx_h + (int64_t)(j - plen) * a.sx_s;
+#pragma unroll
+    for (int c8 = 0; c8 < kDecD / 8; ++c8) kw[c8] = *(const u32x4*)(krow + 8 * c8);
+    if (j < plen) cnt = a.counts[b * a.sc_b + g * a.sc_h + j];
+  }
+  constexpr int kQPerLane = G * kDecD / 64;
+  uint16_t qh[kQPerLane];
+#pragma unroll
+  for (int it = 0; it < kQPerLane; ++it) {
+    const int i = lane + 64 * it, hh = i / kDecD, d = i - hh * kDecD;
+    qh[it] = a.q[b * a.sq_b + (int64_t)(g * G + hh) * a.sq_h + d];
+  }
+#pragma unroll
+  for (int it = 0; it < kQPerLane; ++it) {
+    const int i = lane + 64 * it, hh = i / kDecD, d = i - hh * kDecD;
+    s_q[hh][d] = E16<DT>::one(qh[it]);
   }
   __syncthreads();
 
-  // ---- scores ----
-  const int j = j0 + lane;
-  const bool valid = j < total;
+  // ---- scores: lane t scores key j0 + t for every query head of the group ----
   float sc[G];
 #pragma unroll
   for (int hh = 0; hh < G; ++hh) sc[hh] = -INFINITY;
   if (valid) {
-    const uint16_t* krow;
-    float bias = 0.0f;
-    if (j < plen) {
-      krow = a.kp + b * a.sp_b + g * a.sp_h + (int64_t)j * a.sp_s;
-      const int c = a.counts[b * a.sc_b + g * a.sc_h + j];
-      bias = __logf((float)c);  // log(0) = -inf: padding anchors get no weight (:309-311)
-      if (c <= 0) bias = -INFINITY;
-    } else {
-      krow = a.kx + b * a.sx_b + g * a.sx_h + (int64_t)(j - plen) * a.sx_s;
-    }
-    u32x4 kw[kDecD / 8];
-#pragma unroll
-    for (int c8 = 0; c8 < kDecD / 8; ++c8) kw[c8] = *(const u32x4*)(krow + 8 * c8);
+    // log(count) bias; log(0) = -inf: padding anchors get no weight (:309-311)
+    const float bias = j >= plen ? 0.0f : (cnt <= 0 ? -INFINITY : __logf((float)cnt));
     float acc[G];
 #pragma unroll
     for (int hh = 0; hh < G; ++hh) acc[hh] = 0.0f;
@@ -202,6 +212,17 @@ __global__ __launch_bounds__(64) void decode_attn_kernel(DecodeAttnArgs a) {
       if (hh < G) sc[hh] = acc[hh] * a.scale + bias;
   }
 
+  // ---- the slice's 64 value rows (rows past the end load nothing and carry p = 0),
+  // in flight during the softmax ----
+  uint32_t vw[kDecSlice];
+#pragma unroll
+  for (int u = 0; u < kDecSlice; ++u) {
+    const int jk = j0 + u;
+    const uint16_t* vrow = jk < plen ? a.vp + b * a.sp_b + g * a.sp_h + (int64_t)jk * a.sp_s
+                                     : a.vx + b * a.sx_b + g * a.sx_h + (int64_t)(jk - plen) * a.sx_s;
+    vw[u] = jk < total ? *(const uint32_t*)(vrow + 2 * lane) : 0u;
+  }
+
   // ---- per-head slice max and sum; weights rounded to the cache's type, to LDS ----
   float* part = a.part + ((int64_t)bg * a.nslice + slice) * G * (kDecD + 2);
 #pragma unroll
@@ -219,16 +240,7 @@ __global__ __launch_bounds__(64) void decode_attn_kernel(DecodeAttnArgs a) {
   }
   __syncthreads();
 
-  // ---- P.V: lane l owns dims 2l, 2l+1; the slice's value rows are loaded together
-  // (rows past the end load nothing and carry p = 0) ----
-  uint32_t vw[kDecSlice];
-#pragma unroll
-  for (int u = 0; u < kDecSlice; ++u) {
-    const int jk = j0 + u;
-    const uint16_t* vrow = jk < plen ? a.vp + b * a.sp_b + g * a.sp_h + (int64_t)jk * a.sp_s
-                                     : a.vx + b * a.sx_b + g * a.sx_h + (int64_t)(jk - plen) * a.sx_s;
-    vw[u] = jk < total ? *(const uint32_t*)(vrow + 2 * lane) : 0u;
-  }
+  // ---- P.V: lane l owns dims 2l, 2l+1 ----
   float av[G][2];
 #pragma unroll
   for (int hh = 0; hh < G; ++hh) av[hh][0] = av[hh][1] = 0.0f;
@@ -250,16 +262,17 @@ __global__ __launch_bounds__(64) void decode_attn_kernel(DecodeAttnArgs a) {
     }
 }
 
-// Merge of the slices of one query head.  The slice maxima and sums go through LDS
-// once; then thread (dim d, half q) adds dim d of the P.V partials of the slices
-// s = q (mod 2), 32 slices at a time with all 32 loads in flight, and the two halves
-// are added in LDS.
+// Merge of the slices of one query head.  Thread (dim d, half q) adds dim d of the P.V
+// partials of the slices s = q (mod 2), 32 slices at a time with all 32 loads in flight;
+// the first 32 are loaded together with the slice maxima and sums, which each thread
+// folds into a running (max, sum) before one workgroup reduction.  The two halves are
+// added in LDS.
 constexpr int kDecMaxSlices = 16384;
 constexpr int kCombUnroll = 32;
 template <int DT>
 __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeAttnArgs a) {
   __shared__ float s_f[kDecMaxSlices];
-  __shared__ float s_red[4];
+  __shared__ float s_red[8];
   __shared__ float s_half[kDecD];
   const int bhq = blockIdx.x;
   const int b = bhq / a.Hq, hq = bhq - (bhq / a.Hq) * a.Hq;
@@ -271,48 +284,62 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeAttnArgs a) {
   const int total = plen + a.exact_len;
   const int ns = (total + kDecSlice - 1) / kDecSlice;
   const float* base = a.part + (int64_t)bg * a.nslice * a.G * (kDecD + 2) + hh * (kDecD + 2);
-  const int64_t sstride = (int64_t)a.G * (kDecD + 2);
-  // slice maxima -> M
-  float m = -INFINITY;
-  for (int s2 = tid; s2 < ns; s2 += 256) {
-    const float ms = base[s2 * sstride];
-    s_f[s2] = ms;
-    m = __builtin_fmaxf(m, ms);
-  }
-#pragma unroll
-  for (int d = 32; d >= 1; d >>= 1) m = __builtin_fmaxf(m, __shfl_xor(m, d, 64));
-  if (lane == 0) s_red[wid] = m;
-  __syncthreads();
-  const float M = __builtin_fmaxf(__builtin_fmaxf(s_red[0], s_red[1]), __builtin_fmaxf(s_red[2], s_red[3]));
-  __syncthreads();
-  // slice factors and L
-  float l = 0.0f;
-  for (int s2 = tid; s2 < ns; s2 += 256) {
-    const float ms = s_f[s2];
-    const float f = ms == -INFINITY ? 0.0f : __expf(ms - M);
-    s_f[s2] = f;
-    l += f == 0.0f ? 0.0f : base[s2 * sstride + 1] * f;
-  }
-#pragma unroll
-  for (int d = 32; d >= 1; d >>= 1) l += __shfl_xor(l, d, 64);
-  if (lane == 0) s_red[wid] = l;
-  __syncthreads();
-  const float L = (s_red[0] + s_red[1]) + (s_red[2] + s_red[3]);
-  // P.V partials of dim d over the slices of this half
+  // 32-bit offsets within one (batch, KV head): nslice * G * (D + 2) stays below 2^31
+  // under the launch's limits on slices and group size
+  const int sstride = a.G * (kDecD + 2);
+  // the first batch of P.V partials goes out first: it does not depend on the maxima.
+  // Slice indexes past the last are clamped to a slice that exists and masked when
+  // added, so the 32 loads issue without branches.
   const int d = tid & (kDecD - 1), q = tid >> 7;
-  float acc = 0.0f;
-  for (int s0 = q; s0 < ns; s0 += 2 * kCombUnroll) {
-    float x[kCombUnroll];
+  const int last = ns > 0 ? ns - 1 : 0;
+  const float* pv = base + 2 + d;
+  float x[kCombUnroll];
 #pragma unroll
-    for (int u = 0; u < kCombUnroll; ++u) {
-      const int s2 = s0 + 2 * u;
-      x[u] = s2 < ns ? base[s2 * sstride + 2 + d] : 0.0f;
+  for (int u = 0; u < kCombUnroll; ++u) x[u] = pv[__builtin_elementwise_min(q + 2 * u, last) * sstride];
+  // slice maxima and sums: a running (max, sum) per thread, then over the workgroup
+  float m = -INFINITY, l = 0.0f;
+  for (int s2 = tid; s2 < ns; s2 += 256) {
+    const float ms = base[s2 * sstride], ls = base[s2 * sstride + 1];
+    s_f[s2] = ms;
+    if (ms == -INFINITY) continue;
+    if (ms > m) {
+      l = m == -INFINITY ? 0.0f : l * __expf(m - ms);
+      m = ms;
     }
+    l += ls * __expf(ms - m);
+  }
+  auto merge = [](float& m1, float& l1, float m2, float l2) {
+    const float mm = __builtin_fmaxf(m1, m2);
+    if (mm == -INFINITY) return;
+    l1 = (m1 == -INFINITY ? 0.0f : l1 * __expf(m1 - mm)) + (m2 == -INFINITY ? 0.0f : l2 * __expf(m2 - mm));
+    m1 = mm;
+  };
+#pragma unroll
+  for (int dd = 32; dd >= 1; dd >>= 1) merge(m, l, __shfl_xor(m, dd, 64), __shfl_xor(l, dd, 64));
+  if (lane == 0) {
+    s_red[wid] = m;
+    s_red[4 + wid] = l;
+  }
+  __syncthreads();
+  float M = s_red[0], L = s_red[4];
+#pragma unroll
+  for (int w2 = 1; w2 < 4; ++w2) merge(M, L, s_red[w2], s_red[4 + w2]);
+  // P.V partials of dim d over the slices of this half
+  float acc = 0.0f;
+#pragma unroll
+  for (int u = 0; u < kCombUnroll; ++u) {
+    const int s2 = q + 2 * u;
+    const float ms = s2 < ns ? s_f[s2] : -INFINITY;
+    acc += ms == -INFINITY ? 0.0f : x[u] * __expf(ms - M);
+  }
+  for (int s0 = q + 2 * kCombUnroll; s0 < ns; s0 += 2 * kCombUnroll) {
+#pragma unroll
+    for (int u = 0; u < kCombUnroll; ++u) x[u] = pv[__builtin_elementwise_min(s0 + 2 * u, last) * sstride];
 #pragma unroll
     for (int u = 0; u < kCombUnroll; ++u) {
       const int s2 = s0 + 2 * u;
-      const float f = s2 < ns ? s_f[s2] : 0.0f;
-      acc += f == 0.0f ? 0.0f : x[u] * f;
+      const float ms = s2 < ns ? s_f[s2] : -INFINITY;
+      acc += ms == -INFINITY ? 0.0f : x[u] * __expf(ms - M);
     }
   }
   if (q == 1) s_half[d] = acc;
