@@ -262,18 +262,20 @@ __global__ __launch_bounds__(64) void decode_attn_kernel(DecodeAttnArgs a) {
     }
 }
 
-// Merge of the slices of one query head.  Thread (dim d, half q) adds dim d of the P.V
-// partials of the slices s = q (mod 2), 32 slices at a time with all 32 loads in flight;
-// the first 32 are loaded together with the slice maxima and sums, which each thread
-// folds into a running (max, sum) before one workgroup reduction.  The two halves are
-// added in LDS.
+// Merge of the slices of one query head, split over kCombParts workgroups of
+// kCombDims dims each.  Thread (dim d, phase q) adds dim d of the P.V partials of the
+// slices s = q (mod kCombPhases), kCombUnroll slices at a time with all of their loads in
+// flight; the first batch (256 slices) goes out together with the slice maxima and sums,
+// which each thread folds into a running (max, sum) before one workgroup reduction.
+// The phases are added in LDS.
 constexpr int kDecMaxSlices = 16384;
+constexpr int kCombParts = 4, kCombDims = kDecD / kCombParts, kCombPhases = 256 / kCombDims;
 constexpr int kCombUnroll = 32;
 template <int DT>
 __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeAttnArgs a) {
   __shared__ float s_f[kDecMaxSlices];
   __shared__ float s_red[8];
-  __shared__ float s_half[kDecD];
+  __shared__ float s_acc[kCombPhases][kCombDims];
   const int bhq = blockIdx.x;
   const int b = bhq / a.Hq, hq = bhq - (bhq / a.Hq) * a.Hq;
   const int g = hq / a.G, hh = hq - g * a.G;
@@ -289,13 +291,15 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeAttnArgs a) {
   const int sstride = a.G * (kDecD + 2);
   // the first batch of P.V partials goes out first: it does not depend on the maxima.
   // Slice indexes past the last are clamped to a slice that exists and masked when
-  // added, so the 32 loads issue without branches.
-  const int d = tid & (kDecD - 1), q = tid >> 7;
+  // added, so the loads issue without branches.
+  const int dl = tid & (kCombDims - 1), q = tid / kCombDims;
+  const int d = blockIdx.y * kCombDims + dl;
   const int last = ns > 0 ? ns - 1 : 0;
   const float* pv = base + 2 + d;
   float x[kCombUnroll];
 #pragma unroll
-  for (int u = 0; u < kCombUnroll; ++u) x[u] = pv[__builtin_elementwise_min(q + 2 * u, last) * sstride];
+  for (int u = 0; u < kCombUnroll; ++u)
+    x[u] = pv[__builtin_elementwise_min(q + kCombPhases * u, last) * sstride];
   // slice maxima and sums: a running (max, sum) per thread, then over the workgroup
   float m = -INFINITY, l = 0.0f;
   for (int s2 = tid; s2 < ns; s2 += 256) {
@@ -324,27 +328,33 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeAttnArgs a) {
   float M = s_red[0], L = s_red[4];
 #pragma unroll
   for (int w2 = 1; w2 < 4; ++w2) merge(M, L, s_red[w2], s_red[4 + w2]);
-  // P.V partials of dim d over the slices of this half
+  // P.V partials of dim d over the slices of this phase
   float acc = 0.0f;
 #pragma unroll
   for (int u = 0; u < kCombUnroll; ++u) {
-    const int s2 = q + 2 * u;
+    const int s2 = q + kCombPhases * u;
     const float ms = s2 < ns ? s_f[s2] : -INFINITY;
     acc += ms == -INFINITY ? 0.0f : x[u] * __expf(ms - M);
   }
-  for (int s0 = q + 2 * kCombUnroll; s0 < ns; s0 += 2 * kCombUnroll) {
+  for (int s0 = q + kCombPhases * kCombUnroll; s0 < ns; s0 += kCombPhases * kCombUnroll) {
 #pragma unroll
-    for (int u = 0; u < kCombUnroll; ++u) x[u] = pv[__builtin_elementwise_min(s0 + 2 * u, last) * sstride];
+    for (int u = 0; u < kCombUnroll; ++u)
+      x[u] = pv[__builtin_elementwise_min(s0 + kCombPhases * u, last) * sstride];
 #pragma unroll
     for (int u = 0; u < kCombUnroll; ++u) {
-      const int s2 = s0 + 2 * u;
+      const int s2 = s0 + kCombPhases * u;
       const float ms = s2 < ns ? s_f[s2] : -INFINITY;
       acc += ms == -INFINITY ? 0.0f : x[u] * __expf(ms - M);
     }
   }
-  if (q == 1) s_half[d] = acc;
+  s_acc[q][dl] = acc;
   __syncthreads();
-  if (q == 0) a.out[b * a.so_b + hq * a.so_h + d] = E16<DT>::bits((acc + s_half[d]) / L);
+  if (q == 0) {
+    float o = acc;
+#pragma unroll
+    for (int p = 1; p < kCombPhases; ++p) o += s_acc[p][dl];
+    a.out[b * a.so_b + hq * a.so_h + d] = E16<DT>::bits(o / L);
+  }
 }
 
 }  // namespace da
@@ -400,7 +410,7 @@ static int launch_decode(DecodeAttnArgs& a, dim3 agrid, int64_t n_heads, hipStre
     default: hipLaunchKernelGGL((decode_attn_kernel<8, DT>), agrid, dim3(64), 0, st, a); break;
   }
   if (int rc = check_launch("da_decode_attention")) return rc;
-  hipLaunchKernelGGL((decode_combine_kernel<DT>), dim3((unsigned)n_heads), dim3(256), 0, st, a);
+  hipLaunchKernelGGL((decode_combine_kernel<DT>), dim3((unsigned)n_heads, kCombParts), dim3(256), 0, st, a);
   return check_launch("da_decode_attention(combine)");
 }
 
