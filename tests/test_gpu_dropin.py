@@ -218,3 +218,46 @@ def test_decode_cache_matches_oracle(gpu, metric, tau, dtype):
     finally:
         for name, val in saved.items():
             setattr(globVR, name, val)
+
+
+@pytest.mark.parametrize("B,Hq,Hkv,cap,W,exact,dtype", [
+    (1, 32, 8, 40000, 128, 128, torch.bfloat16),   # dense-like length: 600+ slices per head
+    (1, 32, 8, 40000, 128, 128, torch.float16),
+    (2, 8, 8, 3000, 128, 77, torch.bfloat16),      # G = 1
+    (1, 16, 2, 20000, 64, 0, torch.bfloat16),      # G = 8, empty ring
+    (1, 12, 4, 1000, 128, 5, torch.bfloat16),      # G = 3, one head with no anchors
+], ids=["G4-40k-bf16", "G4-40k-fp16", "G1-B2", "G8-ring0", "G3-empty-head"])
+def test_decode_attention_kernel_vs_oracle(gpu, B, Hq, Hkv, cap, W, exact, dtype):
+    """da_decode_attention on a synthetic cache against the oracle (deltaDecoding.py:236-362):
+    per-head packed lengths, counts with zero-count padding slots, key norms spread so that
+    the maximum moves between slices, and the slice merge over up to 600+ slices."""
+    from deltaattention_amd.deltaDecoding import _decode_attention_launch
+    D = 128
+    rng = np.random.default_rng(B * 1000 + Hq * 10 + Hkv)
+    lens = rng.integers(cap // 2, cap + 1, size=B * Hkv).astype(np.int32)
+    if Hkv == 4:
+        lens[1] = 0
+    kp = rng.standard_normal((B, Hkv, cap, D)).astype(np.float32)
+    kp *= rng.uniform(0.3, 2.5, size=(B, Hkv, cap, 1)).astype(np.float32)
+    vp = rng.standard_normal((B, Hkv, cap, D)).astype(np.float32)
+    cnt = rng.integers(1, 9, size=(B, Hkv, cap)).astype(np.int32)
+    cnt[rng.random((B, Hkv, cap)) < 0.05] = 0
+    kx = rng.standard_normal((B, Hkv, W, D)).astype(np.float32)
+    vx = rng.standard_normal((B, Hkv, W, D)).astype(np.float32)
+    q = rng.standard_normal((B, Hq, D)).astype(np.float32)
+    t = lambda a: torch.from_numpy(a).to(dtype)
+    kp_t, vp_t, kx_t, vx_t, q_t = t(kp), t(vp), t(kx), t(vx), t(q)
+    st = {"k_packed": kp_t.float().numpy(), "v_packed": vp_t.float().numpy(), "counts": cnt,
+          "lengths": lens, "k_exact": kx_t.float().numpy(), "v_exact": vx_t.float().numpy(),
+          "exact_len": exact, "window": W}
+    want = O.decode_attention(q_t.float().numpy(), st)
+    g = lambda x: x.to(gpu)
+    kp_g, vp_g, kx_g, vx_g, q_g = g(kp_t), g(vp_t), g(kx_t), g(vx_t), g(q_t)
+    cnt_g, lens_g = g(torch.from_numpy(cnt)), g(torch.from_numpy(lens))
+    out = torch.empty((B, Hq, D), dtype=dtype, device=gpu)
+    announce(f"da_decode_attention B={B} Hq={Hq} Hkv={Hkv} cap={cap} W={W} exact={exact} {dtype}")
+    _decode_attention_launch(q_g, Hq * D, D, kp_g, vp_g, (Hkv * cap * D, cap * D, D), cnt_g,
+                             (Hkv * cap, cap), lens_g, kx_g, vx_g, (Hkv * W * D, W * D, D), W,
+                             exact, D ** -0.5, out, Hq * D, D, B, Hq, Hkv, D, "decode attention")
+    torch.cuda.synchronize()
+    _close(out.float().cpu().numpy(), want, f"decode attention G={Hq // Hkv} cap={cap}")
