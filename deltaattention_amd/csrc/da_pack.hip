@@ -65,17 +65,20 @@ __global__ __launch_bounds__(kScanThreads) void pack_scan_kernel(const int32_t* 
   const int64_t bh = blockIdx.x;
   const int32_t* krow = keep + bh * N;
 
-  // wave w takes groups 32w .. 32w + 31 of every 32 * kScanWaves
+  // wave w takes groups 32w .. 32w + 31 of every 32 * kScanWaves.  Rows past the end
+  // are clamped to row N - 1 and masked afterwards, so the 32 loads issue without
+  // branches (a guarded load is waited for before the next one is issued).
   for (int gb = wid * kScanUnroll; gb < ngroups; gb += kScanWaves * kScanUnroll) {
-    bool kp[kScanUnroll];
+    int kv[kScanUnroll];
 #pragma unroll
     for (int j = 0; j < kScanUnroll; ++j) {
       const int64_t r = (int64_t)(gb + j) * 64 + lane;
-      kp[j] = gb + j < ngroups && r < N && krow[r] != 0;
+      kv[j] = krow[r < N ? r : N - 1];
     }
 #pragma unroll
     for (int j = 0; j < kScanUnroll; ++j) {
-      const uint64_t bits = __ballot(kp[j]);
+      const int64_t r = (int64_t)(gb + j) * 64 + lane;
+      const uint64_t bits = __ballot(r < N && kv[j] != 0);
       if (lane == 0 && gb + j < ngroups) {
         const int cnt = __popcll(bits);
         const int first = bits ? __builtin_ctzll(bits) : 64;
