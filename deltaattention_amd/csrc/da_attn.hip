@@ -990,6 +990,15 @@ __global__ __launch_bounds__(256) void hybrid_schedule_kernel(const int32_t* __r
     float* wrow = prep.wts + (int64_t)bg * prep.wcap;
     int32_t* trow = prep.tsw ? prep.tsw + (int64_t)bg * prep.wcap : nullptr;
     const int i0 = (blockIdx.y - 1) * 1024 + tid;
+    // rows at or beyond P are clamped to row P - 1 and masked after the load, so the
+    // loads of the four rows issue together (P = 0 loads nothing)
+    int32_t raw[4], tr[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int ic = min(i0 + 256 * j, P - 1);
+      raw[j] = P > 0 ? crow[ic] : 0;
+      tr[j] = P > 0 && trow ? row[ic] : INT_MAX;
+    }
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int i = i0 + 256 * j;
@@ -997,9 +1006,8 @@ __global__ __launch_bounds__(256) void hybrid_schedule_kernel(const int32_t* __r
       float w = 0.0f;
       int tv = INT_MAX;
       if (i < P) {
-        const int32_t raw = crow[i];
-        w = prep.no_count ? 1.0f : (prep.cnt_is_float ? __int_as_float(raw) : (float)raw);
-        if (trow && w > 0.0f) tv = row[i];
+        w = prep.no_count ? 1.0f : (prep.cnt_is_float ? __int_as_float(raw[j]) : (float)raw[j]);
+        if (trow && w > 0.0f) tv = tr[j];
       }
       wrow[i] = w > 0.0f ? log2f(w) / prep.scale_log2 : -INFINITY;
       if (trow) trow[i] = tv;
@@ -1007,13 +1015,22 @@ __global__ __launch_bounds__(256) void hybrid_schedule_kernel(const int32_t* __r
     if (bg == 0 && blockIdx.y == 1 && tid < kTileN) prep.zeros[tid] = 0.0f;
     return;
   }
-  // wave w takes blocks 8w .. 8w + 7 of every 32, their loads in flight together
+  // wave w takes blocks 8w .. 8w + 7 of every 32, their loads in flight together:
+  // rows at or beyond P are clamped to row P - 1 and masked after the load (a guarded
+  // load is waited for before the next one is issued); nblk > 0 implies P > 0
   for (int jb0 = wid * 8; jb0 < nblk; jb0 += 32) {
     int m[8];
+    int r0[8], r1[8];
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
       const int i0 = (jb0 + u) * kBlock + lane, i1 = i0 + 64;
-      m[u] = max(i0 < P ? row[i0] : Nk + 1, i1 < P ? row[i1] : Nk + 1);
+      r0[u] = row[min(i0, P - 1)];
+      r1[u] = row[min(i1, P - 1)];
+    }
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int i0 = (jb0 + u) * kBlock + lane, i1 = i0 + 64;
+      m[u] = max(i0 < P ? r0[u] : Nk + 1, i1 < P ? r1[u] : Nk + 1);
     }
 #pragma unroll
     for (int u = 0; u < 8; ++u) {
