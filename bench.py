@@ -386,7 +386,8 @@ def main():
     args = parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on exactly one GPU; multi-GPU runs are not "
-                                   "part of it (the path shards by KV head, see DESIGN.md)",
+                                   "part of it (the path would shard by KV head: each GPU owns whole KV heads and "
+                                   "their query heads, so attention needs no collective)",
                           "n_gpus": args.gpus}))
         sys.exit(2)
     if args.config == 3:

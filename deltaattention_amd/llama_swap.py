@@ -110,7 +110,7 @@ def attention_time_ms() -> float:
 
 
 def llama3_8b_config(attn_implementation: str = DELTA, num_layers: int = 32):
-    """Llama-3-8B shape (SURVEY config 3): hidden 4096, FFN 14336, 32 heads / 8 KV heads,
+    """Llama-3-8B shape (the end-to-end prefill configuration): hidden 4096, FFN 14336, 32 heads / 8 KV heads,
     vocab 128256, RoPE base 5e5."""
     from transformers import LlamaConfig
     cfg = LlamaConfig(vocab_size=128256, hidden_size=4096, intermediate_size=14336,
