@@ -1,6 +1,6 @@
 """Ragged batched prefill (config 4 semantics): a packed [tokens, heads, 128] batch with
-cu_seqlens, where each sequence is exactly a B = 1 delta prefill (SURVEY config 4: the
-reference has no varlen API, parity is "each sequence run as B = 1")."""
+cu_seqlens, where each sequence is exactly a B = 1 delta prefill.  The reference has no
+varlen API, so parity is each sequence run on its own as B = 1."""
 import numpy as np
 import pytest
 import torch
