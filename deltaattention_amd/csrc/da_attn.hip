@@ -78,6 +78,7 @@ struct AttnArgs {
   int64_t sts_b, sts_h;
   int64_t scnt_b, scnt_h;
   int B, Hq, Hkv, G, Nq, Nk;
+  int D;  // head dimension: a multiple of 8, at most 128 (dims D..127 are zero-filled)
   int P_host;
   const int32_t* P_dev;
   int window;
@@ -133,20 +134,22 @@ struct TileRegs {
 // after the in-register transpose the 16 lanes of one chunk write one complete
 // 128-byte V^T row, which keeps the LDS stores free of bank conflicts.
 __device__ __forceinline__ void load_tile(TileRegs& r, const uint16_t* kbase, const uint16_t* vbase,
-                                          int64_t sk_n, int64_t sv_n, int key0, int limit,
+                                          int64_t sk_n, int64_t sv_n, int key0, int limit, int D,
                                           int tid, bool with_meta, const int32_t* tsrow,
                                           const void* cntrow, int cnt_is_float, int no_count,
                                           int meta_limit, int ts_oob) {
   const int chunk = tid & 15, kg = tid >> 4;    // K mapping
   const int vchunk = tid >> 4, vkg = tid & 15;  // V mapping
+  // 8-dim chunks at or beyond the head dimension are zero (BLOCK_D padding of the reference)
+  const bool kin = chunk * 8 < D, vin = vchunk * 8 < D;
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int key = key0 + kg * 4 + j;
-    r.k[j] = key < limit ? *(const u32x4*)(kbase + (int64_t)key * sk_n + chunk * 8)
-                         : u32x4{0, 0, 0, 0};
+    r.k[j] = (kin && key < limit) ? *(const u32x4*)(kbase + (int64_t)key * sk_n + chunk * 8)
+                                  : u32x4{0, 0, 0, 0};
     const int vkey = key0 + vkg * 4 + j;
-    r.v[j] = vkey < limit ? *(const u32x4*)(vbase + (int64_t)vkey * sv_n + vchunk * 8)
-                          : u32x4{0, 0, 0, 0};
+    r.v[j] = (vin && vkey < limit) ? *(const u32x4*)(vbase + (int64_t)vkey * sv_n + vchunk * 8)
+                                   : u32x4{0, 0, 0, 0};
   }
   if (with_meta && tid < kTileN) {
     const int key = key0 + tid;
@@ -294,7 +297,8 @@ void attn_kernel(AttnArgs a) {
     const uint16_t* qrow = a.q + (int64_t)b * a.sq_b + (int64_t)h * a.sq_h + (int64_t)row * a.sq_n;
 #pragma unroll
     for (int t = 0; t < kD / 16; ++t)
-      qreg[t] = (row < a.Nq) ? *(const u32x4*)(qrow + 16 * t + 8 * hl) : u32x4{0, 0, 0, 0};
+      qreg[t] = (row < a.Nq && 16 * t + 8 * hl < a.D) ? *(const u32x4*)(qrow + 16 * t + 8 * hl)
+                                                       : u32x4{0, 0, 0, 0};
   }
 
   f32x16 o[4];
@@ -317,7 +321,7 @@ void attn_kernel(AttnArgs a) {
   if (ntiles > 0) {
     const uint16_t *kb, *vb; int64_t skn, svn; int key0, limit; bool ph1;
     tile_src(0, kb, vb, skn, svn, key0, limit, ph1);
-    load_tile(regs, kb, vb, skn, svn, key0, limit, tid, meta && ph1, ts_row, cnt_row,
+    load_tile(regs, kb, vb, skn, svn, key0, limit, a.D, tid, meta && ph1, ts_row, cnt_row,
               a.cnt_is_float, a.no_count, P, a.Nk + 1);
     store_tile(regs, smem, tid, meta && ph1);
   }
@@ -330,7 +334,7 @@ void attn_kernel(AttnArgs a) {
     if (has_next) {
       const uint16_t *kb, *vb; int64_t skn, svn; int key0, limit;
       tile_src(t + 1, kb, vb, skn, svn, key0, limit, next_ph1);
-      load_tile(regs, kb, vb, skn, svn, key0, limit, tid, meta && next_ph1, ts_row, cnt_row,
+      load_tile(regs, kb, vb, skn, svn, key0, limit, a.D, tid, meta && next_ph1, ts_row, cnt_row,
                 a.cnt_is_float, a.no_count, P, a.Nk + 1);
     }
 
@@ -448,7 +452,7 @@ void attn_kernel(AttnArgs a) {
         u32x2 w;
         w[0] = E16<DT>::pack(o[db][4 * j + 0] * inv, o[db][4 * j + 1] * inv);
         w[1] = E16<DT>::pack(o[db][4 * j + 2] * inv, o[db][4 * j + 3] * inv);
-        *(u32x2*)(orow + db * 32 + 8 * j + 4 * hl) = w;
+        if (db * 32 + 8 * j + 4 * hl < a.D) *(u32x2*)(orow + db * 32 + 8 * j + 4 * hl) = w;
       }
   }
 }
@@ -678,8 +682,9 @@ void attn_pp_kernel(AttnArgs a) {
     const char* src = isK ? (ph1 ? kb1 : kb2) : (ph1 ? vb1 : vb2);
     const void* base = uniform_ptr(src + (int64_t)key0 * snb);
     const int nrows = max(0, min(limit - key0, kTileN));
+    const int range = __builtin_amdgcn_readfirstlane(nrows * snb);
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<void*>(base), (short)0, __builtin_amdgcn_readfirstlane(nrows * snb), kBufferDword3);
+        const_cast<void*>(base), (short)0, range, kBufferDword3);
     char* dst = isK ? kst0 + (t_raw % 3) * kKBytes : vst0 + (t_raw % 3) * kVBytes;
 #pragma unroll
     for (int j = 0; j < 2; ++j) {
@@ -687,8 +692,11 @@ void attn_pp_kernel(AttnArgs a) {
       const int rowt = rc * 4 + (lane >> 4);
       const int pos = lane & 15;
       const int chunk = pos ^ (isK ? (rowt & 15) : 4 * (rowt & 3));
+      // 8-dim chunks at or beyond the head dimension read at the end of the range:
+      // out of range, so they arrive as zeros (BLOCK_D padding of the reference)
+      const int off = chunk * 8 < a.D ? rowt * snb + chunk * 16 : range;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)(dst + rc * 1024), 16,
-                                               rowt * snb + chunk * 16, 0, 0, 0);
+                                               off, 0, 0, 0);
     }
   };
   // key biases (and timestamps) of the tile's 64 keys, into slot t % 4 of their ring: a
@@ -766,16 +774,20 @@ void attn_pp_kernel(AttnArgs a) {
   {
     // rows past Nq load row Nq - 1 (no branch between the loads) and are zeroed after
     const uint16_t* qrow = a.q + (int64_t)b * a.sq_b + (int64_t)h * a.sq_h + (int64_t)min(row, a.Nq - 1) * a.sq_n;
+    // dims at or beyond the head dimension load dims 0..7 and are zeroed after
     u32x4 w[kD / 16];
 #pragma unroll
-    for (int t = 0; t < kD / 16; ++t) w[t] = *(const u32x4*)(qrow + 16 * t + 8 * hl);
+    for (int t = 0; t < kD / 16; ++t) {
+      const int d0 = 16 * t + 8 * hl;
+      w[t] = *(const u32x4*)(qrow + (d0 < a.D ? d0 : 0));
+    }
     // Redefine Q^T here so the loop does not see it as an outstanding load: otherwise
     // every S = K Q^T block waits for all memory loads, including the staging loads
     // meant to land two sections later.
 #pragma unroll
     for (int t = 0; t < kD / 16; ++t) {
       asm volatile("" : "+v"(w[t]));
-      qreg[t] = row < a.Nq ? w[t] : u32x4{0, 0, 0, 0};
+      qreg[t] = (row < a.Nq && 16 * t + 8 * hl < a.D) ? w[t] : u32x4{0, 0, 0, 0};
     }
   }
   if (T > 0) {
@@ -944,7 +956,7 @@ void attn_pp_kernel(AttnArgs a) {
         u32x2 w;
         w[0] = E16<DT>::pack(o[db][4 * j + 0] * inv, o[db][4 * j + 1] * inv);
         w[1] = E16<DT>::pack(o[db][4 * j + 2] * inv, o[db][4 * j + 3] * inv);
-        *(u32x2*)(orow + db * 32 + 8 * j + 4 * hl) = w;
+        if (db * 32 + 8 * j + 4 * hl < a.D) *(u32x2*)(orow + db * 32 + 8 * j + 4 * hl) = w;
       }
   }
 }
@@ -1129,7 +1141,9 @@ static int fill_common(AttnArgs& a, const void* q, const void* k, const void* v,
                        const int64_t* st, float scale, const char* who) {
   DA_REQUIRE(q && k && v && out && st, "%s: null pointer", who);
   DA_REQUIRE(B > 0 && Hq > 0 && Hkv > 0 && Nq > 0 && Nk > 0, "%s: empty shape", who);
-  if (D != kD) return set_error(DA_ERR_UNSUPPORTED, "%s: head_dim must be 128 (got %lld)", who, (long long)D);
+  if (D <= 0 || D > kD || (D & 7))
+    return set_error(DA_ERR_UNSUPPORTED, "%s: head_dim must be a multiple of 8 in [8, 128] (got %lld)", who,
+                     (long long)D);
   DA_REQUIRE(Hq % Hkv == 0, "%s: Hq (%lld) must be a multiple of Hkv (%lld)", who, (long long)Hq, (long long)Hkv);
   DA_REQUIRE(Nq < (1ll << 30) && Nk < (1ll << 30), "%s: sequence too long", who);
   DA_REQUIRE(scale > 0.0f, "%s: scale must be positive", who);
@@ -1137,7 +1151,7 @@ static int fill_common(AttnArgs& a, const void* q, const void* k, const void* v,
     DA_REQUIRE((st[i] & 7) == 0, "%s: strides must be multiples of 8 elements (stride %d = %lld)", who, i, (long long)st[i]);
   DA_REQUIRE(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out), "%s: tensors must be 16-byte aligned", who);
   for (int i : {DA_STRIDE_K + 2, DA_STRIDE_V + 2})
-    DA_REQUIRE(st[i] >= kD && st[i] < (1ll << 24),
+    DA_REQUIRE(st[i] >= D && st[i] < (1ll << 24),
                "%s: key/value sequence strides must be in [head_dim, 2^24) (stride %d = %lld)", who, i, (long long)st[i]);
   a.q = (const uint16_t*)q; a.k = (const uint16_t*)k; a.v = (const uint16_t*)v; a.out = (uint16_t*)out;
   a.sq_b = st[DA_STRIDE_Q]; a.sq_h = st[DA_STRIDE_Q + 1]; a.sq_n = st[DA_STRIDE_Q + 2];
@@ -1146,6 +1160,7 @@ static int fill_common(AttnArgs& a, const void* q, const void* k, const void* v,
   a.so_b = st[DA_STRIDE_OUT]; a.so_h = st[DA_STRIDE_OUT + 1]; a.so_n = st[DA_STRIDE_OUT + 2];
   a.B = (int)B; a.Hq = (int)Hq; a.Hkv = (int)Hkv; a.G = (int)(Hq / Hkv);
   a.Nq = (int)Nq; a.Nk = (int)Nk;
+  a.D = (int)D;
   a.scale_log2 = scale * 1.4426950408889634f;
   a.hpw = (a.G % 4 == 0) ? 4 : (a.G % 2 == 0 ? 2 : 1);
   a.rows_per_wg = 32 * (4 / a.hpw);
@@ -1206,7 +1221,7 @@ extern "C" int da_hybrid_prefill(const void* q, const void* k, const void* v, co
   DA_REQUIRE(window >= 0 && window < (1ll << 30), "da_hybrid_prefill: window must be >= 0");
   DA_REQUIRE(aligned16(k_packed) && aligned16(v_packed), "da_hybrid_prefill: packed tensors must be 16-byte aligned");
   for (int i : {DA_STRIDE_KP + 2, DA_STRIDE_VP + 2})
-    DA_REQUIRE(strides[i] >= kD && strides[i] < (1ll << 24),
+    DA_REQUIRE(strides[i] >= D && strides[i] < (1ll << 24),
                "da_hybrid_prefill: packed sequence strides must be in [head_dim, 2^24) (stride %d = %lld)", i, (long long)strides[i]);
   DA_REQUIRE(strides[DA_STRIDE_TS + 2] == 1 && strides[DA_STRIDE_CNT + 2] == 1,
              "da_hybrid_prefill: timestamps and counts must be contiguous along the packed axis");

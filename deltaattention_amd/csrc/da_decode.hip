@@ -439,6 +439,9 @@ extern "C" int da_decode_attention(const void* q, int dtype, int64_t B, int64_t 
              "da_decode_attention: bad cache lengths");
   DA_REQUIRE(((sp_b | sp_h | sp_s | sx_b | sx_h | sx_s) & 7) == 0 && (((uintptr_t)k_packed | (uintptr_t)k_exact) & 15) == 0,
              "da_decode_attention: key rows must be 16-byte aligned");
+  // value rows are read 4 bytes per lane
+  DA_REQUIRE((((uintptr_t)v_packed | (uintptr_t)v_exact) & 3) == 0,
+             "da_decode_attention: value rows must be 4-byte aligned");
   if ((capacity + window + kDecSlice - 1) / kDecSlice > kDecMaxSlices)
     return set_error(DA_ERR_UNSUPPORTED, "da_decode_attention: cache longer than %d keys", kDecMaxSlices * kDecSlice);
   const int64_t need = da_decode_workspace_size(B, Hq, capacity, window);

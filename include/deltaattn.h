@@ -109,7 +109,8 @@ int da_pack(const int32_t* keep, const void* k, const void* v, int dtype, int64_
  * Logical schedule: 128-row query blocks x 128-anchor packed blocks exactly as
  * the reference (Phase 1 stops at the first packed block whose maximum
  * timestamp is >= start_m - W; Phase 2 starts at ((last+1)/128)*128).
- * D must be 128; Hq % Hkv == 0.
+ * D: a multiple of 8 in [8, 128] (the kernels zero-fill dims D..127, as the reference's
+ * BLOCK_D = next_pow2(D) masked loads do, deltaFlashAttention.py:39-42); Hq % Hkv == 0.
  */
 int64_t da_hybrid_workspace_size(int64_t B, int64_t Hkv, int64_t num_packed);
 int da_hybrid_prefill(const void* q, const void* k, const void* v, const void* k_packed,
@@ -124,7 +125,8 @@ int da_hybrid_prefill(const void* q, const void* k, const void* v, const void* k
  * Dense flash prefill (the uncompressed control).  Replaces _attn_fwd_flat and
  * triton_flash_attention (flashAttention.py:5-130) with GQA handled by head
  * indexing instead of repeat_kv.
- * q, out: [B, Hq, Nq, D]; k, v: [B, Hkv, Nk, D]; causal: mask j > i.
+ * q, out: [B, Hq, Nq, D]; k, v: [B, Hkv, Nk, D]; causal: mask j > i.  D as for
+ * da_hybrid_prefill (flashAttention.py:25-32 pads it the same way).
  */
 int da_dense_prefill(const void* q, const void* k, const void* v, void* out, int dtype,
                      int64_t B, int64_t Hq, int64_t Hkv, int64_t Nq, int64_t Nk, int64_t D,

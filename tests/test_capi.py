@@ -65,8 +65,10 @@ def test_attention_rejects_bad_shapes():
     fake = ctypes.c_void_p(1 << 20)
     st = _native.strides_array([0] * 24)
     f = ctypes.c_float(0.088)
-    # head_dim 64 is not supported by the attention kernels
-    assert lib.da_dense_prefill(fake, fake, fake, fake, 1, 1, 4, 2, 64, 64, 64, st, 1, f, None) == -2
+    # head_dim must be a multiple of 8 in [8, 128]
+    for D in (60, 136, 0):
+        assert lib.da_dense_prefill(fake, fake, fake, fake, 1, 1, 4, 2, 64, 64, D, st, 1, f, None) == -2
+        assert "head_dim" in _err()
     # Hq not a multiple of Hkv
     assert lib.da_dense_prefill(fake, fake, fake, fake, 1, 1, 6, 4, 64, 64, 128, st, 1, f, None) == -1
     # negative scale
@@ -88,6 +90,21 @@ def test_attention_rejects_bad_shapes():
     assert lib.da_hybrid_prefill(*args, 3, fake, 1, 1, 4, 2, 64, 64, 128, st3, 10, None, 0,
                                  f, 0, 0, fake, 1 << 20, None) == -1
     assert b"sequence strides" in lib.da_last_error()
+
+
+def test_decode_rejects_misaligned_values():
+    """Value rows are read 4 bytes per lane: misaligned v_packed / v_exact are refused."""
+    lib = _native.lib()
+    a = ctypes.c_void_p(1 << 20)
+    odd = ctypes.c_void_p((1 << 20) + 2)
+    f = ctypes.c_float(0.088)
+    D, cap, W = 128, 64, 16
+    st_p, st_x = (8 * cap * D, cap * D, D), (8 * W * D, W * D, D)
+    for vp, vx in ((odd, a), (a, odd)):
+        for fn, tail in ((lib.da_decode_attention, [a, 1 << 30, None]),):
+            rc = fn(a, 1, 1, 32, 8, D, 32 * D, D, a, vp, *st_p, a, 8 * cap, cap, a, cap, a, vx,
+                    *st_x, W, 0, f, a, 32 * D, D, *tail)
+            assert rc == -1 and "value rows" in _err()
 
 
 def test_workspace_sizes():

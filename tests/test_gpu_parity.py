@@ -126,19 +126,23 @@ def test_dense_vs_oracle(gpu, B, Hq, Hkv, N, causal):
 # --------------------------------------------------------------------------------------
 @pytest.mark.parametrize("case", ["A", "B", "C", "D"])
 @pytest.mark.parametrize("variant", ["hybrid", "sanity", "pure_phase1"])
-def test_hybrid_golden(gpu, case, variant):
-    """The golden inputs are bf16-exact with D=32; zero-padding D to 128 leaves every
-    score (and the selection) unchanged, the scale stays 32**-0.5, and the first 32
-    output dims are compared with the reference's interpreter outputs."""
+@pytest.mark.parametrize("native", [True, False], ids=["d32", "d32-padded"])
+def test_hybrid_golden(gpu, case, variant, native):
+    """The golden inputs are bf16-exact with D=32.  "d32" runs head_dim 32 natively (the
+    kernels zero-fill dims 32..127, like the reference's BLOCK_D masking); "d32-padded"
+    zero-pads D to 128 on the host, which leaves every score unchanged (scale 32**-0.5),
+    and compares the first 32 output dims.  Both against the reference's interpreter
+    outputs."""
     from deltaattention_amd import ops
     z = np.load(os.path.join(HERE, "golden", "hybrid_golden.npz"))
     g = lambda n: z[f"{case}/{n}"]
     q, k, v, keep = g("q"), g("k"), g("v"), g("keep")
     W, no_count = int(g("window")), bool(g("no_count"))
     D = q.shape[-1]
-    pad = lambda a: torch.from_numpy(np.pad(a, [(0, 0)] * 3 + [(0, 128 - D)])).to(torch.bfloat16).to(gpu)
+    width = D if native else 128
+    pad = lambda a: torch.from_numpy(np.pad(a, [(0, 0)] * 3 + [(0, width - D)])).to(torch.bfloat16).to(gpu)
     qg, kg, vg = pad(q), pad(k), pad(v)
-    announce(f"golden case {case} {variant}")
+    announce(f"golden case {case} {variant} {'native D' if native else 'padded to 128'}")
     packed = ops.pack(torch.from_numpy(keep).to(gpu), kg, vg)
     out = ops.hybrid_prefill(qg, kg, vg, packed.k_packed, packed.v_packed, packed.timestamps,
                              packed.counts, window=W, scale=D ** -0.5, variant=variant,
