@@ -12,7 +12,9 @@ native kernels.
   timings and the prefill -> HybridCompressedCache hand-off.  P stays on the device
   for the attention; only the bookkeeping and the hand-off read it back, as the
   reference does (:656, :695).
-* ``dense_prefill_attention`` restates PATH 2 (modeling_llama.py:778-803).
+* ``dense_prefill_attention`` restates PATH 2 (modeling_llama.py:778-803), and
+  ``delta_decode_handoff`` its ``delta_decode`` tail (:805-879): delta selection and
+  packing of the prefill keys into the HybridCompressedCache for compressed decoding.
 """
 from __future__ import annotations
 
@@ -23,7 +25,8 @@ import torch
 from . import globVR, ops, timing
 
 __all__ = ["forward_hybrid_flash", "forward_hybrid_flash_sanity", "forward_pure_phase1",
-           "delta_prefill_attention", "dense_prefill_attention", "keep_mask"]
+           "delta_prefill_attention", "dense_prefill_attention", "delta_decode_handoff",
+           "keep_mask"]
 
 
 def _wrapper(variant, q, k_dense, v_dense, k_packed, v_packed, packed_timestamps, packed_counts,
@@ -121,13 +124,37 @@ def delta_prefill_attention(query_states: torch.Tensor, key_states: torch.Tensor
                              num_packed_dev=packed.num_packed, out=out)
     timing.stop_event("time_delta_mm_pattern", ev)
     if past_key_value is not None and hasattr(past_key_value, "initialize_from_prefill"):
-        p = packed.trimmed()                                        # :762-773
-        tail = min(q_len, past_key_value.exact_window_size)
-        past_key_value.initialize_from_prefill(
-            layer_idx=layer_idx, k_packed=p.k_packed, v_packed=p.v_packed, counts=p.counts,
-            timestamps=p.timestamps, k_exact=key_states[:, :, -tail:, :],
-            v_exact=value_states[:, :, -tail:, :], original_q_len=q_len)
+        _handoff(past_key_value, layer_idx, packed, key_states, value_states)   # :762-773
     return out
+
+
+def _handoff(cache, layer_idx, packed, key_states, value_states):
+    """initialize_from_prefill with the P packed rows of every head and the last
+    min(N, W) prefill tokens (modeling_llama.py:762-773, 869-879)."""
+    q_len = key_states.shape[2]
+    p = packed.trimmed()
+    tail = min(q_len, cache.exact_window_size)
+    cache.initialize_from_prefill(
+        layer_idx=layer_idx, k_packed=p.k_packed, v_packed=p.v_packed, counts=p.counts,
+        timestamps=p.timestamps, k_exact=key_states[:, :, -tail:, :],
+        v_exact=value_states[:, :, -tail:, :], original_q_len=q_len)
+
+
+def delta_decode_handoff(key_states: torch.Tensor, value_states: torch.Tensor, layer_idx: int,
+                         past_key_value) -> None:
+    """PATH 2's ``delta_decode`` tail (modeling_llama.py:805-879): after a dense prefill,
+    delta-select and pack the post-RoPE keys with the globVR chunking, metric and
+    threshold (always delta mode, whatever ``packing_mode`` says, as the reference
+    launches chunked_eval_kernel directly), then hand the packed history and the exact
+    tail to the cache."""
+    fixed = getattr(globVR, "chunk_size", 0)                        # :809-816
+    divide_to = getattr(globVR, "divide_to", 0)
+    keep, _ = ops.select(key_states, getattr(globVR, "row_delta_threshold", 0.0),
+                         chunk_size=fixed if fixed > 0 else 0,
+                         divide_to=0 if fixed > 0 else divide_to,
+                         metric=getattr(globVR, "row_similarity_metric", "euclidean"))
+    packed = ops.pack(keep, key_states, value_states)               # :836-866
+    _handoff(past_key_value, layer_idx, packed, key_states, value_states)   # :868-879
 
 
 def dense_prefill_attention(query_states, key_states, value_states, scaling=None, out=None):

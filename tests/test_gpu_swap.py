@@ -2,6 +2,7 @@
 transformers, against transformers' own fp32 eager attention on the same weights."""
 import copy
 
+import numpy as np
 import pytest
 import torch
 
@@ -67,3 +68,123 @@ def test_delta_swap_keep_all_equals_dense(gpu):
     print(f"delta(keep all) vs dense: max-abs {err.max():.3e} mean-abs {err.mean():.3e}")
     assert err.max() <= 2e-2 * max(1.0, float(dense.abs().max()))
     assert err.mean() <= 1e-3 * max(1.0, float(dense.abs().mean()) * 10)
+
+
+def _spy_layer0(monkeypatch):
+    """Record layer 0's prefill key/value states, its decode-step keys/values and its
+    decode queries and attention outputs, while the real calls run."""
+    from deltaattention_amd import attention, deltaDecoding
+    from deltaattention_amd.deltaDecoding import HybridCompressedCache
+    rec = {"prefill": None, "kv": [], "attn": []}
+    real_prefill = attention.delta_prefill_attention
+    real_handoff = attention.delta_decode_handoff
+    real_update = HybridCompressedCache.update
+    real_decode = deltaDecoding.decode_attention
+
+    def prefill(q, k, v, layer_idx=0, **kw):
+        if layer_idx == 0:
+            rec["prefill"] = (k.detach().clone(), v.detach().clone())
+        return real_prefill(q, k, v, layer_idx=layer_idx, **kw)
+
+    def handoff(k, v, layer_idx, cache):
+        if layer_idx == 0:
+            rec["prefill"] = (k.detach().clone(), v.detach().clone())
+        return real_handoff(k, v, layer_idx, cache)
+
+    def update(self, k, v, layer_idx, cache_kwargs=None):
+        if layer_idx == 0 and k.shape[2] == 1:
+            rec["kv"].append((k.detach().clone(), v.detach().clone()))
+        return real_update(self, k, v, layer_idx, cache_kwargs)
+
+    def decode(q, cache, layer_idx, scaling=None):
+        out = real_decode(q, cache, layer_idx, scaling=scaling)
+        if layer_idx == 0:
+            rec["attn"].append((q.detach().clone(), out.detach().clone()))
+        return out
+
+    monkeypatch.setattr(attention, "delta_prefill_attention", prefill)
+    monkeypatch.setattr(attention, "delta_decode_handoff", handoff)
+    monkeypatch.setattr(HybridCompressedCache, "update", update)
+    monkeypatch.setattr(deltaDecoding, "decode_attention", decode)
+    return rec
+
+
+def _assert_cache_equals(cache, st, what):
+    n = int(st["lengths"].max())
+    assert np.array_equal(cache.packed_lengths[0].cpu().numpy(), st["lengths"]), what
+    assert np.array_equal(cache.packed_counts[0, :, :, :n].cpu().numpy(), st["counts"][:, :, :n]), what
+    assert np.array_equal(cache.packed_timestamps[0, :, :, :n].cpu().numpy(), st["timestamps"][:, :, :n]), what
+    assert np.array_equal(cache.k_packed[0, :, :, :n].float().cpu().numpy(), st["k_packed"][:, :, :n]), what
+    assert np.array_equal(cache.v_packed[0, :, :, :n].float().cpu().numpy(), st["v_packed"][:, :, :n]), what
+    assert np.array_equal(cache.k_exact[0].float().cpu().numpy(), st["k_exact"]), what
+    assert np.array_equal(cache.v_exact[0].float().cpu().numpy(), st["v_exact"]), what
+
+
+@pytest.mark.parametrize("impl", ["deltaattention", "deltaattention_dense"], ids=["path1", "path2"])
+def test_model_prefill_then_decode_compressed_cache(gpu, monkeypatch, impl):
+    """A 2-layer Llama-3-8B-shaped model (hidden 4096, 32 query / 8 KV heads, head_dim
+    128; vocab cut to 1024) prefills 2048 tokens into a HybridCompressedCache through
+    llama_swap.install's forward and decodes 64 tokens one at a time.  PATH 1 hands its
+    packed history to the cache (modeling_llama.py:761-773); PATH 2 packs after the dense
+    prefill when delta_decode is set (:805-879); every later token runs PATH 3: update,
+    then the compressed decode attention (:565-567, :453-518, :883-897).  Layer 0 is
+    replayed in the oracle from the keys and queries it saw: the cache after the hand-off
+    and after the last step is bit-exact, and every step's decode attention is within
+    tolerance."""
+    from oracle import delta_oracle as O
+    from oracle import select_oracle_c as OC
+    from test_gpu_dropin import _oracle_cache_from_prefill
+    from deltaattention_amd import globVR, llama_swap, timing
+    from deltaattention_amd.deltaDecoding import HybridCompressedCache
+    N, steps, W, tau = 2048, 64, 64, 20.5   # random-init keys: adjacent dist^2 ~ 420 +- 52
+    cfg = llama_swap.llama3_8b_config(impl, num_layers=2)
+    cfg.vocab_size = 1024
+    model = llama_swap.random_llama(cfg, gpu, seed=3)
+    for name, val in (("packing_mode", "delta"), ("chunk_size", 512), ("row_delta_threshold", tau),
+                      ("row_similarity_metric", "euclidean"), ("delta_decode", True),
+                      ("dense_window_size", 128), ("time_internal", True), ("kv_log_interval", 16),
+                      ("sanity", False), ("pure_phase1", False), ("no_count", False)):
+        monkeypatch.setattr(globVR, name, val, raising=False)
+    timing.reset()
+    rec = _spy_layer0(monkeypatch)
+    cache = HybridCompressedCache(cfg, 1, dtype=torch.bfloat16, exact_window_size=W,
+                                  initial_capacity=256, device="cuda")
+    ids = torch.randint(0, cfg.vocab_size, (1, N + steps), generator=torch.Generator().manual_seed(4)).cuda()
+    announce(f"model swap {impl}: prefill N={N} into HybridCompressedCache")
+    with torch.no_grad():
+        h = model.model(input_ids=ids[:, :N], past_key_values=cache, use_cache=True).last_hidden_state
+    assert torch.isfinite(h).all()
+    assert cache.get_seq_length(0) == N and cache.get_seq_length(1) == N
+    k0, v0 = (t.float().cpu().numpy() for t in rec["prefill"])
+    keep, _ = OC.select_delta(k0, tau, 512)
+    p = O.pack(k0, v0, keep)
+    st = _oracle_cache_from_prefill(p, k0, v0, W, cache.capacity + steps)
+    _assert_cache_equals(cache, st, "after the prefill hand-off")
+    print(f"{impl}: P={p['P']} anchors of {N} per head (max)", flush=True)
+    announce(f"model swap {impl}: {steps} decode steps")
+    worst = 0.0
+    with torch.no_grad():
+        for t in range(steps):
+            h = model.model(input_ids=ids[:, N + t:N + t + 1], past_key_values=cache,
+                            use_cache=True).last_hidden_state
+            assert h.shape == (1, 1, cfg.hidden_size) and torch.isfinite(h).all()
+            kt, vt = (x.float().cpu().numpy() for x in rec["kv"][t])
+            O.decode_update(st, kt, vt, tau)
+            q, out = rec["attn"][t]
+            want = O.decode_attention(q[:, :, 0].float().cpu().numpy(), st, scale=128 ** -0.5)
+            err = np.abs(out[:, :, 0].float().cpu().numpy() - want)
+            worst = max(worst, float(err.max()))
+            assert err.max() <= 2e-2 and err.mean() <= 1e-3, (t, err.max(), err.mean())
+    assert cache.get_seq_length(0) == N + steps
+    _assert_cache_equals(cache, st, "after the decode steps")
+    appended = int((st["lengths"] - p["P"]).sum())     # evicted tokens that became anchors
+    print(f"{impl}: {steps} steps, worst max-abs {worst:.3e}, packed length "
+          f"{int(st['lengths'].max())}, appended {appended} of {8 * steps} evictions", flush=True)
+    assert 0 < appended < 8 * steps     # the threshold both merges and appends
+    timing.resolve_latency_events()
+    stats = globVR.latency_stats
+    for key in ("time_prefill_forward_total", "time_decode_forward_total",
+                "time_delta_decode_cache_update", "time_delta_decode_attn_calc"):
+        assert stats.get(key, {}).get("calls", 0) > 0, key
+    assert len(globVR.kv_compression_samples) >= steps // 16
+    timing.reset()
