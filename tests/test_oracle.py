@@ -362,3 +362,79 @@ def test_decode_update_cosine_on_a_circle():
     n = int(st["lengths"][0])
     assert st["timestamps"][0, 0, :n].tolist() == list(range(0, T - W, 3))
     assert st["counts"][0, 0, :n].sum() == T - W
+
+
+# --------------------------------------------------------------------------------------
+# bf16 rounding (oracle.bf16_round) and the round_p paths that use it
+# --------------------------------------------------------------------------------------
+def test_bf16_round_matches_torch():
+    """bf16_round against torch's own float32 -> bfloat16 conversion (round to nearest,
+    ties to even) on values across the whole exponent range, exact ties with even and
+    odd bf16 mantissas, overflow to infinity, signed zeros, infinities, NaN and
+    subnormals.  A truncating or ties-away implementation fails the tie cases."""
+    torch = pytest.importorskip("torch")
+    rng = np.random.default_rng(0)
+    n = 200000
+    mant = rng.standard_normal(n)
+    with np.errstate(over="ignore"):  # a few land beyond the float32 range: +-inf
+        x = (mant * np.exp2(rng.integers(-150, 128, n).astype(np.float64))).astype(np.float32)
+    bits = rng.integers(0, 1 << 32, 50000, dtype=np.uint64).astype(np.uint32)
+    ties = ((bits & np.uint32(0xFFFF0000)) | np.uint32(0x8000)).view(np.float32)
+    near = ((bits & np.uint32(0xFFFF0000)) | np.uint32(0x7FFF)).view(np.float32)
+    special = np.array([1.00390625, 1.01171875, -1.00390625, -1.01171875, 0.0, -0.0, np.inf,
+                        -np.inf, np.nan, 1e-40, -1e-40, 1e-45, 3.3961776e38, -3.3961776e38,
+                        np.finfo(np.float32).max, np.finfo(np.float32).tiny, 0.7, 0.702],
+                       dtype=np.float32)
+    allv = np.concatenate([x, ties, near, special])
+    got = O.bf16_round(allv)
+    want = torch.from_numpy(allv.copy()).to(torch.bfloat16).float().numpy()
+    nan = np.isnan(want)
+    assert np.array_equal(np.isnan(got), nan)
+    assert np.array_equal(got[~nan].view(np.uint32), want[~nan].view(np.uint32))
+    # the tie cases really are ties and go both ways
+    r = O.bf16_round(ties[np.isfinite(ties)])
+    up = np.abs(r) > np.abs(ties[np.isfinite(ties)])
+    assert 0.3 < up.mean() < 0.7
+
+
+def _round_p_case():
+    """Two keys, scale 128**-0.5: row 1 scores key 0 at 0 and key 1 at ln(0.702), so
+    p = (1, 0.702 +- 1e-7); bf16(0.702) = 0.703125 (round to nearest, unambiguous: the
+    neighbours are 0.69921875 and 0.703125).  V = (0, 1) in dim 0."""
+    D = 128
+    scale = np.float32(D ** -0.5)
+    q = np.zeros((1, 1, 2, D), np.float32)
+    q[0, 0, 1, 0] = np.float32(np.log(0.702) / scale)
+    k = np.zeros((1, 1, 2, D), np.float32)
+    k[0, 0, 1, 0] = 1.0
+    v = np.zeros((1, 1, 2, D), np.float32)
+    v[0, 0, 1, 0] = 1.0
+    p1 = float(np.exp(np.float32(q[0, 0, 1, 0] * scale)))
+    return q, k, v, scale, p1
+
+
+def test_round_p_hybrid_closed_form():
+    """With round_p the P.V product takes bf16(p) while l keeps the fp32 p, as
+    deltaFlashAttention.py:86-98 (p.to(v.dtype)); without it, p itself."""
+    q, k, v, scale, p1 = _round_p_case()
+    ts = np.zeros((1, 1, 1), np.int32)
+    cnt = np.ones((1, 1, 1), np.int32)
+    kp, vp = k[:, :, :1], v[:, :, :1]
+    for round_p, num in ((True, 0.703125), (False, p1)):
+        out = O.hybrid_attention(q, k, v, kp, vp, ts, cnt, window=1000, scale=scale, round_p=round_p)
+        assert abs(out[0, 0, 1, 0] - num / (1.0 + p1)) < 1e-6, (round_p, out[0, 0, 1, 0])
+        assert out[0, 0, 0, 0] == 0.0
+
+
+def test_round_p_decode_closed_form():
+    """decode_attention's round_p: one query, a packed anchor with count 1 scoring 0 and a
+    ring key scoring ln(0.702)."""
+    q, k, v, scale, p1 = _round_p_case()
+    D = 128
+    st = {"k_packed": k[:, :, :1].copy(), "v_packed": v[:, :, :1].copy(),
+          "counts": np.ones((1, 1, 1), np.int32), "lengths": np.ones(1, np.int32),
+          "k_exact": k[:, :, 1:].copy(), "v_exact": v[:, :, 1:].copy(), "exact_len": 1, "window": 1}
+    for round_p, num in ((True, 0.703125), (False, p1)):
+        out = O.decode_attention(q[:, :, 1], st, scale=scale, round_p=round_p)
+        assert out.shape == (1, 1, D)
+        assert abs(out[0, 0, 0] - num / (1.0 + p1)) < 1e-6, (round_p, out[0, 0, 0])
