@@ -37,7 +37,12 @@ SIGNATURES = {
     "da_decode_workspace_size": (_L, [_L, _L, _L, _L]),
     "da_decode_attention": (_I, [_P, _I, _L, _L, _L, _L, _L, _L, _P, _P, _L, _L, _L, _P, _L, _L,
                                  _P, _L, _P, _P, _L, _L, _L, _L, _L, _F, _P, _L, _L, _P, _L, _P]),
+    "da_decode_attention_noalloc": (_I, [_P, _I, _L, _L, _L, _L, _L, _L, _P, _P, _L, _L, _L, _P, _L,
+                                         _L, _P, _L, _P, _P, _L, _L, _L, _L, _L, _F, _P, _L, _L,
+                                         _P]),
 }
+
+DA_DECODE_SCRATCH_BYTES = 32 << 20
 
 
 class NativeLibraryError(RuntimeError):

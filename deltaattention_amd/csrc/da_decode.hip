@@ -18,6 +18,8 @@
 // combine kernel merges the slices exactly (rescaling by exp(m_s - M)).  As in the
 // reference, P is rounded to the cache's 16-bit type before the P.V product while the
 // row sum stays fp32.  The cache is bf16 or fp16 (the E16 element type).
+#include <mutex>
+
 #include "da_common.hpp"
 
 namespace da {
@@ -419,6 +421,52 @@ extern "C" int64_t da_decode_workspace_size(int64_t B, int64_t Hq, int64_t capac
   return B * Hq * nslice * (kDecD + 2) * (int64_t)sizeof(float);
 }
 
+// Validation and launch shared by da_decode_attention and da_decode_attention_noalloc:
+// `part` is the slice-partials buffer (caller workspace or the static scratch).
+static int decode_attention_impl(const void* q, int dtype, int64_t B, int64_t Hq, int64_t Hkv,
+                                 int64_t sq_b, int64_t sq_h, const void* k_packed, const void* v_packed,
+                                 int64_t sp_b, int64_t sp_h, int64_t sp_s, const int32_t* counts,
+                                 int64_t sc_b, int64_t sc_h, const int32_t* lengths, int64_t capacity,
+                                 const void* k_exact, const void* v_exact, int64_t sx_b, int64_t sx_h,
+                                 int64_t sx_s, int64_t window, int64_t exact_len, float scale, void* out,
+                                 int64_t so_b, int64_t so_h, float* part, hipStream_t st) {
+  DecodeAttnArgs a = {};
+  a.q = (const uint16_t*)q; a.sq_b = sq_b; a.sq_h = sq_h;
+  a.kp = (const uint16_t*)k_packed; a.vp = (const uint16_t*)v_packed; a.sp_b = sp_b; a.sp_h = sp_h; a.sp_s = sp_s;
+  a.counts = counts; a.sc_b = sc_b; a.sc_h = sc_h; a.lengths = lengths; a.capacity = capacity;
+  a.kx = (const uint16_t*)k_exact; a.vx = (const uint16_t*)v_exact; a.sx_b = sx_b; a.sx_h = sx_h; a.sx_s = sx_s;
+  a.exact_len = (int)exact_len; a.scale = scale; a.out = (uint16_t*)out; a.so_b = so_b; a.so_h = so_h;
+  a.part = part;
+  a.nslice = (int)((capacity + window + kDecSlice - 1) / kDecSlice);
+  a.B = (int)B; a.Hq = (int)Hq; a.Hkv = (int)Hkv; a.G = (int)(Hq / Hkv);
+  const dim3 agrid((unsigned)(B * Hkv), (unsigned)a.nslice);
+  return dtype == DA_F16 ? launch_decode<DA_F16>(a, agrid, B * Hq, st) : launch_decode<DA_BF16>(a, agrid, B * Hq, st);
+}
+
+// Argument checks common to both decode attention entry points.
+static int decode_attention_check(const void* q, int dtype, int64_t B, int64_t Hq, int64_t Hkv, int64_t D,
+                                  const void* k_packed, const void* v_packed, int64_t sp_b, int64_t sp_h,
+                                  int64_t sp_s, const int32_t* counts, const int32_t* lengths,
+                                  int64_t capacity, const void* k_exact, const void* v_exact, int64_t sx_b,
+                                  int64_t sx_h, int64_t sx_s, int64_t window, int64_t exact_len, void* out,
+                                  const char* who) {
+  DA_REQUIRE(q && k_packed && v_packed && counts && lengths && k_exact && v_exact && out,
+             "%s: null pointer", who);
+  if (dtype != DA_BF16 && dtype != DA_F16)
+    return set_error(DA_ERR_UNSUPPORTED, "%s: the cache must be bf16 or fp16", who);
+  if (D != kDecD) return set_error(DA_ERR_UNSUPPORTED, "%s: head_dim must be 128", who);
+  DA_REQUIRE(B > 0 && Hq > 0 && Hkv > 0 && Hq % Hkv == 0, "%s: bad head counts", who);
+  if (Hq / Hkv > kDecMaxG) return set_error(DA_ERR_UNSUPPORTED, "%s: GQA group above %d", who, kDecMaxG);
+  DA_REQUIRE(window > 0 && exact_len >= 0 && exact_len <= window && capacity > 0, "%s: bad cache lengths", who);
+  // key rows are read 16 bytes at a time, value rows 4 bytes per lane
+  DA_REQUIRE(((sp_b | sp_h | sp_s | sx_b | sx_h | sx_s) & 7) == 0 && (((uintptr_t)k_packed | (uintptr_t)k_exact) & 15) == 0,
+             "%s: key rows must be 16-byte aligned", who);
+  DA_REQUIRE((((uintptr_t)v_packed | (uintptr_t)v_exact) & 3) == 0, "%s: value rows must be 4-byte aligned", who);
+  if ((capacity + window + kDecSlice - 1) / kDecSlice > kDecMaxSlices)
+    return set_error(DA_ERR_UNSUPPORTED, "%s: cache longer than %d keys", who, kDecMaxSlices * kDecSlice);
+  return DA_OK;
+}
+
 extern "C" int da_decode_attention(const void* q, int dtype, int64_t B, int64_t Hq, int64_t Hkv,
                                    int64_t D, int64_t sq_b, int64_t sq_h, const void* k_packed,
                                    const void* v_packed, int64_t sp_b, int64_t sp_h, int64_t sp_s,
@@ -428,35 +476,75 @@ extern "C" int da_decode_attention(const void* q, int dtype, int64_t B, int64_t 
                                    int64_t window, int64_t exact_len, float scale, void* out,
                                    int64_t so_b, int64_t so_h, void* workspace,
                                    int64_t workspace_bytes, void* stream) {
-  DA_REQUIRE(q && k_packed && v_packed && counts && lengths && k_exact && v_exact && out,
-             "da_decode_attention: null pointer");
-  if (dtype != DA_BF16 && dtype != DA_F16)
-    return set_error(DA_ERR_UNSUPPORTED, "da_decode_attention: the cache must be bf16 or fp16");
-  if (D != kDecD) return set_error(DA_ERR_UNSUPPORTED, "da_decode_attention: head_dim must be 128");
-  DA_REQUIRE(B > 0 && Hq > 0 && Hkv > 0 && Hq % Hkv == 0, "da_decode_attention: bad head counts");
-  if (Hq / Hkv > kDecMaxG) return set_error(DA_ERR_UNSUPPORTED, "da_decode_attention: GQA group above %d", kDecMaxG);
-  DA_REQUIRE(window > 0 && exact_len >= 0 && exact_len <= window && capacity > 0,
-             "da_decode_attention: bad cache lengths");
-  DA_REQUIRE(((sp_b | sp_h | sp_s | sx_b | sx_h | sx_s) & 7) == 0 && (((uintptr_t)k_packed | (uintptr_t)k_exact) & 15) == 0,
-             "da_decode_attention: key rows must be 16-byte aligned");
-  // value rows are read 4 bytes per lane
-  DA_REQUIRE((((uintptr_t)v_packed | (uintptr_t)v_exact) & 3) == 0,
-             "da_decode_attention: value rows must be 4-byte aligned");
-  if ((capacity + window + kDecSlice - 1) / kDecSlice > kDecMaxSlices)
-    return set_error(DA_ERR_UNSUPPORTED, "da_decode_attention: cache longer than %d keys", kDecMaxSlices * kDecSlice);
+  const char* who = "da_decode_attention";
+  if (int rc = decode_attention_check(q, dtype, B, Hq, Hkv, D, k_packed, v_packed, sp_b, sp_h, sp_s, counts,
+                                      lengths, capacity, k_exact, v_exact, sx_b, sx_h, sx_s, window, exact_len,
+                                      out, who))
+    return rc;
   const int64_t need = da_decode_workspace_size(B, Hq, capacity, window);
   if (!workspace || workspace_bytes < need)
-    return set_error(DA_ERR_WORKSPACE, "da_decode_attention: workspace of %lld bytes required", (long long)need);
-  DecodeAttnArgs a = {};
-  a.q = (const uint16_t*)q; a.sq_b = sq_b; a.sq_h = sq_h;
-  a.kp = (const uint16_t*)k_packed; a.vp = (const uint16_t*)v_packed; a.sp_b = sp_b; a.sp_h = sp_h; a.sp_s = sp_s;
-  a.counts = counts; a.sc_b = sc_b; a.sc_h = sc_h; a.lengths = lengths; a.capacity = capacity;
-  a.kx = (const uint16_t*)k_exact; a.vx = (const uint16_t*)v_exact; a.sx_b = sx_b; a.sx_h = sx_h; a.sx_s = sx_s;
-  a.exact_len = (int)exact_len; a.scale = scale; a.out = (uint16_t*)out; a.so_b = so_b; a.so_h = so_h;
-  a.part = (float*)workspace;
-  a.nslice = (int)((capacity + window + kDecSlice - 1) / kDecSlice);
-  a.B = (int)B; a.Hq = (int)Hq; a.Hkv = (int)Hkv; a.G = (int)(Hq / Hkv);
-  hipStream_t st = (hipStream_t)stream;
-  const dim3 agrid((unsigned)(B * Hkv), (unsigned)a.nslice);
-  return dtype == DA_F16 ? launch_decode<DA_F16>(a, agrid, B * Hq, st) : launch_decode<DA_BF16>(a, agrid, B * Hq, st);
+    return set_error(DA_ERR_WORKSPACE, "%s: workspace of %lld bytes required", who, (long long)need);
+  return decode_attention_impl(q, dtype, B, Hq, Hkv, sq_b, sq_h, k_packed, v_packed, sp_b, sp_h, sp_s, counts,
+                               sc_b, sc_h, lengths, capacity, k_exact, v_exact, sx_b, sx_h, sx_s, window,
+                               exact_len, scale, out, so_b, so_h, (float*)workspace, (hipStream_t)stream);
+}
+
+// ------------------------------------------------------------------------------------
+// Decode attention without any allocation: the slice partials live in `scratch`, a
+// file-scope device array (one copy per GPU, held until the process ends).  Host code
+// never passes the array's name to a kernel: on each device the first call looks up
+// the array's device address with hipGetSymbolAddress (with that device current) and
+// keeps it per device; kernels receive that address.  Every call on one GPU shares its
+// copy, so calls that overlap on one GPU (different streams, no ordering) race.
+// ------------------------------------------------------------------------------------
+static __device__ __align__(256) float scratch[DA_DECODE_SCRATCH_BYTES / sizeof(float)];
+
+constexpr int kMaxScratchDevices = 64;
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[kMaxScratchDevices] = {};
+
+// Device address of `scratch` on the current device (looked up once per device).
+static int scratch_for_current_device(void** ptr, const char* who) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return set_error(DA_ERR_HIP, "%s: hipGetDevice: %s", who, hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxScratchDevices)
+    return set_error(DA_ERR_UNSUPPORTED, "%s: device index %d above %d", who, dev, kMaxScratchDevices - 1);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return set_error(DA_ERR_HIP, "%s: hipGetSymbolAddress(scratch) on device %d: %s", who, dev,
+                       hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *ptr = g_scratch_ptr[dev];
+  return DA_OK;
+}
+
+extern "C" int da_decode_attention_noalloc(const void* q, int dtype, int64_t B, int64_t Hq, int64_t Hkv,
+                                           int64_t D, int64_t sq_b, int64_t sq_h, const void* k_packed,
+                                           const void* v_packed, int64_t sp_b, int64_t sp_h, int64_t sp_s,
+                                           const int32_t* counts, int64_t sc_b, int64_t sc_h,
+                                           const int32_t* lengths, int64_t capacity, const void* k_exact,
+                                           const void* v_exact, int64_t sx_b, int64_t sx_h, int64_t sx_s,
+                                           int64_t window, int64_t exact_len, float scale, void* out,
+                                           int64_t so_b, int64_t so_h, void* stream) {
+  const char* who = "da_decode_attention_noalloc";
+  if (int rc = decode_attention_check(q, dtype, B, Hq, Hkv, D, k_packed, v_packed, sp_b, sp_h, sp_s, counts,
+                                      lengths, capacity, k_exact, v_exact, sx_b, sx_h, sx_s, window, exact_len,
+                                      out, who))
+    return rc;
+  const int64_t need = da_decode_workspace_size(B, Hq, capacity, window);
+  if (need > (int64_t)DA_DECODE_SCRATCH_BYTES)
+    return set_error(DA_ERR_UNSUPPORTED,
+                     "%s: needs %lld bytes of scratch, above the static maximum of %lld "
+                     "(B * Hq * ceil((capacity + window) / 64) * 520 bytes); use da_decode_attention",
+                     who, (long long)need, (long long)DA_DECODE_SCRATCH_BYTES);
+  void* part = nullptr;
+  if (int rc = scratch_for_current_device(&part, who)) return rc;
+  return decode_attention_impl(q, dtype, B, Hq, Hkv, sq_b, sq_h, k_packed, v_packed, sp_b, sp_h, sp_s, counts,
+                               sc_b, sc_h, lengths, capacity, k_exact, v_exact, sx_b, sx_h, sx_s, window,
+                               exact_len, scale, out, so_b, so_h, (float*)part, (hipStream_t)stream);
 }

@@ -6,8 +6,9 @@
  * sizes, and a hipStream_t passed as void*.  Nothing allocates device memory:
  * scratch space comes in through a caller-provided workspace whose size the
  * matching *_workspace_size function returns.  Calls enqueue work on the given
- * stream and return without synchronising.  The library is stateless and
- * reentrant; the only per-thread state is the text of the last error.
+ * stream and return without synchronising.  The library is reentrant; the only
+ * per-thread state is the text of the last error, and the only device state is the
+ * static scratch array of da_decode_attention_noalloc.
  *
  * Return value: DA_OK (0) or a negative DA_ERR_* code; da_last_error() then
  * holds a message.
@@ -174,6 +175,28 @@ int da_decode_attention(const void* q, int dtype, int64_t B, int64_t Hq, int64_t
                         int64_t sx_s, int64_t window, int64_t exact_len, float scale, void* out,
                         int64_t so_b, int64_t so_h, void* workspace, int64_t workspace_bytes,
                         void* stream);
+
+/*
+ * da_decode_attention without a workspace and without any allocation.  No counterpart
+ * in the reference: it is for callers that cannot allocate device memory (code under
+ * HIP graph capture, serving loops, harnesses that forbid hipMalloc).  Arguments and
+ * results are those of da_decode_attention minus the workspace; the slice partials
+ * live in a static device array of DA_DECODE_SCRATCH_BYTES per GPU (held until the
+ * process ends), so da_decode_workspace_size(B, Hq, capacity, window) must not exceed
+ * DA_DECODE_SCRATCH_BYTES (DA_ERR_UNSUPPORTED otherwise; e.g. B = 1, Hq = 32 allows
+ * capacity + window up to 129024 keys).  The stream must belong to the current device.
+ * Every call on one GPU shares that GPU's array: calls that overlap on one GPU (on
+ * streams not ordered with each other) race.
+ */
+#define DA_DECODE_SCRATCH_BYTES (32ll << 20)
+int da_decode_attention_noalloc(const void* q, int dtype, int64_t B, int64_t Hq, int64_t Hkv,
+                                int64_t D, int64_t sq_b, int64_t sq_h, const void* k_packed,
+                                const void* v_packed, int64_t sp_b, int64_t sp_h, int64_t sp_s,
+                                const int32_t* counts, int64_t sc_b, int64_t sc_h,
+                                const int32_t* lengths, int64_t capacity, const void* k_exact,
+                                const void* v_exact, int64_t sx_b, int64_t sx_h, int64_t sx_s,
+                                int64_t window, int64_t exact_len, float scale, void* out,
+                                int64_t so_b, int64_t so_h, void* stream);
 
 /*
  * strides for da_hybrid_prefill / da_dense_prefill: int64[3 * 8] element strides

@@ -22,7 +22,8 @@ def test_header_declares_the_expected_entry_points():
     assert declared_symbols() == sorted([
         "da_last_error", "da_version", "da_select", "da_pack_workspace_size", "da_pack",
         "da_hybrid_workspace_size", "da_hybrid_prefill", "da_dense_prefill",
-        "da_decode_update", "da_decode_workspace_size", "da_decode_attention"])
+        "da_decode_update", "da_decode_workspace_size", "da_decode_attention",
+        "da_decode_attention_noalloc"])
 
 
 def test_library_exports_every_declared_symbol():
@@ -101,7 +102,8 @@ def test_decode_rejects_misaligned_values():
     D, cap, W = 128, 64, 16
     st_p, st_x = (8 * cap * D, cap * D, D), (8 * W * D, W * D, D)
     for vp, vx in ((odd, a), (a, odd)):
-        for fn, tail in ((lib.da_decode_attention, [a, 1 << 30, None]),):
+        for fn, tail in ((lib.da_decode_attention, [a, 1 << 30, None]),
+                         (lib.da_decode_attention_noalloc, [None])):
             rc = fn(a, 1, 1, 32, 8, D, 32 * D, D, a, vp, *st_p, a, 8 * cap, cap, a, cap, a, vx,
                     *st_x, W, 0, f, a, 32 * D, D, *tail)
             assert rc == -1 and "value rows" in _err()
