@@ -58,6 +58,11 @@ def parse_args():
                          "attention over the uncompressed cache")
     ap.add_argument("--decode-tokens", type=int, default=200)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-128k", action="store_true",
+                    help="config 1 only: skip the config-2 (N=131072, r=4) measurement that the "
+                         "default run adds to the JSON line as config2_r4")
+    ap.add_argument("--no-sdpa", action="store_true",
+                    help="skip timing torch's scaled_dot_product_attention as a second dense control")
     ap.add_argument("--cpu-sample-blocks", type=int, default=24,
                     help="query blocks (all heads) the CPU baseline runs")
     return ap.parse_args()
@@ -71,11 +76,29 @@ def log(msg):
     print(f"[bench] {msg}", file=sys.stderr, flush=True)
 
 
-def cpu_baseline(q, k, v, tau, window, alg_total, sample_blocks):
-    """Time the CPU restatement (oracle, a 'port' of the reference math) on a bounded
-    sample: full selection + packing, and the hybrid attention for ``sample_blocks``
-    evenly spaced query blocks of every head, extrapolated to the layer by the exact
-    algorithmic-FLOP ratio."""
+def _cpu_model() -> str:
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or platform.machine()
+
+
+def cpu_baseline(q, k, v, tau, window, alg_total, dense_total, sample_blocks):
+    """Time the CPU restatement of the reference math (the oracle, a 'port') on a bounded
+    sample of the layer, on the host cores of the GPU box:
+
+    * delta: selection + packing over every KV head in full, then the hybrid attention for
+      ``sample_blocks`` evenly spaced query blocks of every query head, extrapolated to
+      the layer by the exact algorithmic-FLOP ratio;
+    * dense: the blockwise eager attention (modeling_llama.py:235-276 without the N x N
+      matrix) on the same query blocks, extrapolated by the dense FLOP ratio.
+
+    The full layer would take about a minute of CPU time per leg; the sample keeps the
+    default benchmark run within a few minutes."""
     import numpy as np
     from threadpoolctl import threadpool_limits
     from oracle import delta_oracle as O
@@ -98,6 +121,9 @@ def cpu_baseline(q, k, v, tau, window, alg_total, sample_blocks):
         O.hybrid_attention(qf, kf, vf, p["k_packed"], p["v_packed"], p["timestamps"], p["counts"],
                            window, q_blocks=blocks)
         t_sample = time.perf_counter() - t0
+        t0 = time.perf_counter()
+        O.dense_attention(qf, kf, vf, True, q_blocks=blocks)
+        t_dense_sample = time.perf_counter() - t0
     # algorithmic FLOPs of the sampled blocks
     n_safe, last, ds = metrics.hybrid_schedule(p["timestamps"], p["P"], N, N, window)
     G = Hq // kf.shape[1]
@@ -107,24 +133,38 @@ def cpu_baseline(q, k, v, tau, window, alg_total, sample_blocks):
     pairs = rows * np.minimum(n_safe * 128, c) + rows * (start - ds + 1) + rows * (rows - 1) // 2
     sample_flops = 4.0 * D * float(pairs[:, :, blocks].sum() * G)
     t_attn = t_sample * alg_total / sample_flops
+    st = np.asarray(blocks) * 128
+    rb = np.minimum(128, N - st)
+    dense_sample_flops = 4.0 * D * float((rb * st + rb * (rb + 1) // 2).sum()) * B * Hq
+    t_dense = t_dense_sample * dense_total / dense_sample_flops
     ms = 1e3 * (t_compress + t_attn)
     return {"value": round(ms, 1), "unit": "ms/layer", "cores": cores, "kind": "port",
-            "sample": (f"oracle select+pack over all {B * kf.shape[1]} KV heads "
+            "dense_value": round(1e3 * t_dense, 1),
+            "host_cpu_count": os.cpu_count(), "host_cpu": _cpu_model(),
+            "sample": (f"oracle select+pack over all {B * kf.shape[1]} KV heads in full "
                        f"({1e3 * t_compress:.0f} ms) + hybrid attention for {len(blocks)} of {nqb} "
                        f"query blocks x {Hq} heads ({t_sample:.1f} s), extrapolated by the "
-                       f"algorithmic-FLOP ratio; BLAS threads={cores}, host {platform.processor() or platform.machine()}")}
+                       f"algorithmic-FLOP ratio; dense_value: blockwise dense attention on the same "
+                       f"blocks ({t_dense_sample:.1f} s), extrapolated by the dense FLOP ratio; "
+                       f"numpy/BLAS threads={cores}")}
 
 
-def traffic_bytes(args, N, r_real):
+def traffic_bytes(args, N, r_real, ratio):
     """HBM bytes per launch of the hybrid attention kernel, from the committed rocprofv3
-    FETCH_SIZE / WRITE_SIZE runs (profiles/attn_pp_hybrid_config1_traffic.txt); None for
-    a workload those runs do not cover."""
-    if args.config != 1 or N != 32768 or abs(r_real - 4.0) > 0.05 or args.window != 128:
+    FETCH_SIZE / WRITE_SIZE runs (profiles/traffic_config*.json); None for a workload
+    (sequence length, ratio, window, dtype) those runs do not cover."""
+    if args.dtype != "bf16" or args.window != 128 or abs(r_real - ratio) > 0.05 * ratio:
         return None
-    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic_config1.json")
+    name = {32768: "traffic_config1.json", 131072: f"traffic_config2_r{int(ratio)}.json"}.get(N)
+    if name is None:
+        return None
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", name)
     try:
         with open(path) as f:
-            return int(json.load(f)["bytes_per_launch"])
+            rec = json.load(f)
+        if abs(float(rec.get("ratio", 4.0)) - ratio) > 1e-6:
+            return None
+        return int(rec["bytes_per_launch"])
     except (OSError, ValueError, KeyError):
         return None
 
@@ -403,37 +443,85 @@ def main():
     if args.decode:
         run_decode(args)
         return
-    import numpy as np
-    import torch
-    from deltaattention_amd import metrics, ops, synth
-
-    dev = torch.device("cuda:0")
+    if args.only:
+        run_only(args)
+        return
     N = args.seq or (32768 if args.config == 1 else 131072)
-    B, Hq, Hkv, D = 1, 32, 8, 128
-    W = args.window
-    log(f"config {args.config}: N={N} r={args.ratio} W={W}")
-    q, k, v = synth.make_layer_inputs(B, Hq, Hkv, N, D, rope_base=500000.0, seed=args.seed,
+    head = measure_layer(args, N, args.ratio, headline=True)
+    rec = head.pop("record")
+    if args.config == 1 and not args.no_128k and not args.seq:
+        log("config 2 (N=131072, r=4) ...")
+        extra = measure_layer(args, 131072, 4.0, headline=False)
+        extra.pop("record", None)
+        rec["config2_r4"] = extra
+    print(json.dumps(rec), flush=True)
+
+
+def layer_inputs(args, N):
+    import torch
+    from deltaattention_amd import synth
+    dev = torch.device("cuda:0")
+    q, k, v = synth.make_layer_inputs(1, 32, 8, N, 128, rope_base=500000.0, seed=args.seed,
                                       device=dev, qv_on_device=True,
                                       dtype=torch.float16 if args.dtype == "fp16" else torch.bfloat16)
     torch.cuda.synchronize()
-    tau, r_real = synth.calibrate_threshold(k, args.ratio)
+    return q, k, v
+
+
+def time_loop(fn, iters):
+    """Average ms per call of ``fn``, with HIP events on the stream the kernels run on."""
+    import torch
+    st = torch.cuda.current_stream()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    e0.record(st)
+    for _ in range(iters):
+        fn()
+    e1.record(st)
+    e1.synchronize()
+    return e0.elapsed_time(e1) / iters
+
+
+def sdpa_ms(q, k, v, iters):
+    """torch's scaled_dot_product_attention (causal) on the same inputs, flash / memory-
+    efficient backends only (the math backend would materialise N x N), K/V expanded to
+    the query heads; None when no such backend runs these shapes."""
+    import torch
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+    G = q.shape[1] // k.shape[1]
+    ke = k.repeat_interleave(G, dim=1).contiguous()
+    ve = v.repeat_interleave(G, dim=1).contiguous()
+    try:
+        with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+            fn = lambda: torch.nn.functional.scaled_dot_product_attention(q, ke, ve, is_causal=True)
+            fn()
+            torch.cuda.synchronize()
+            return time_loop(fn, iters)
+    except RuntimeError as e:
+        log(f"sdpa unavailable: {e}")
+        return None
+    finally:
+        del ke, ve
+
+
+def measure_layer(args, N, ratio, headline):
+    """One Llama-3-8B attention layer (B=1, Hq=32, Hkv=8, D=128) at N tokens and
+    compression r: the contract's timed steps of the full delta step (select -> pack ->
+    hybrid) when ``headline``, then per-part HIP-event timings of the hybrid, dense,
+    compression and torch SDPA launches, the roofline of the hybrid kernel and (headline
+    only) the CPU baseline.  Returns a dict; ``record`` holds the JSON line's fields."""
+    import torch
+    from deltaattention_amd import metrics, ops, synth
+    W = args.window
+    B, Hq, Hkv, D = 1, 32, 8, 128
+    log(f"layer: N={N} r={ratio} W={W}")
+    q, k, v = layer_inputs(args, N)
+    tau, r_real = synth.calibrate_threshold(k, ratio)
     log(f"calibrated tau={tau:.4f} realised r={r_real:.3f}")
 
     def step():
         return ops.delta_prefill(q, k, v, tau, 512, window=W)
-
-    # ---- per-part timing helpers (HIP events on the launch stream) ----
-    def time_loop(fn, iters):
-        st = torch.cuda.current_stream()
-        e0 = torch.cuda.Event(enable_timing=True)
-        e1 = torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
-        e0.record(st)
-        for _ in range(iters):
-            fn()
-        e1.record(st)
-        e1.synchronize()
-        return e0.elapsed_time(e1) / iters
 
     keep, _ = ops.select(k, tau, 512)
     packed = ops.pack(keep, k, v)
@@ -455,54 +543,59 @@ def main():
         kk, _ = ops.select(k, tau, 512)
         ops.pack(kk, k, v, out=packed)
 
-    copy_src = copy_dst = None
-    if args.only == "copy":
-        copy_src = torch.ones(1 << 29, dtype=torch.int16, device=dev)  # 1 GiB
-        copy_dst = torch.empty_like(copy_src)
-
-    def copy_only():
-        copy_dst.copy_(copy_src)
-
-    if args.only:
-        fn = {"delta": step, "hybrid": hybrid_only, "dense": dense_only, "compress": compress_only,
-              "copy": copy_only}[args.only]
-        for _ in range(args.warmup):
-            fn()
-        ms = time_loop(fn, args.steps)
-        print(f"only={args.only} N={N} r={r_real:.3f} steps={args.steps} ms/launch={ms:.4f}", flush=True)
-        return
-
-    # ---- the contract's timed region: K full steps ----
+    steps = args.steps if headline else max(3, min(args.steps, 10))
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for _ in range(args.steps):
+    for _ in range(steps):
         step()
     torch.cuda.synchronize()
-    ms_step = 1e3 * (time.perf_counter() - t0) / args.steps
+    ms_step = 1e3 * (time.perf_counter() - t0) / steps
     log(f"delta step {ms_step:.3f} ms")
 
-    iters = max(3, args.steps)
+    iters = max(3, steps)
     for _ in range(2):
         hybrid_only(); dense_only(); compress_only()
     ms_hybrid = time_loop(hybrid_only, iters)
     ms_dense = time_loop(dense_only, iters)
     ms_compress = time_loop(compress_only, iters)
-    log(f"hybrid {ms_hybrid:.3f} ms  dense {ms_dense:.3f} ms  compress {ms_compress:.4f} ms")
+    ms_sdpa = sdpa_ms(q, k, v, max(3, iters // 3)) if not args.no_sdpa else None
+    log(f"hybrid {ms_hybrid:.3f} ms  dense {ms_dense:.3f} ms  compress {ms_compress:.4f} ms  "
+        f"sdpa {ms_sdpa if ms_sdpa is None else round(ms_sdpa, 3)} ms")
 
     fl = metrics.hybrid_flops(ts_h, c_h, P, N, Hq, D, W)
     dense_fl = metrics.dense_flops(B, Hq, N, D)
     cbytes = metrics.compression_bytes(N, D, c_h)
     hyb_tflops = fl["algorithmic"] / (ms_hybrid * 1e-3) / 1e12
     dense_tflops = dense_fl / (ms_dense * 1e-3) / 1e12
-
+    best_dense = min(ms_dense, ms_sdpa) if ms_sdpa else ms_dense
+    res = {
+        "seq_len": N, "ratio": ratio, "realised_ratio": round(r_real, 3), "tau": round(tau, 4),
+        "delta_ms_per_layer": round(ms_step, 4),
+        "speedup_vs_dense": round(ms_dense / ms_step, 3),
+        "kernel_speedup_vs_dense": round(ms_dense / ms_hybrid, 3),
+        "dense_ms_per_layer": round(ms_dense, 4),
+        "sdpa_ms_per_layer": None if ms_sdpa is None else round(ms_sdpa, 4),
+        "speedup_vs_best_dense": round(best_dense / ms_step, 3),
+        "hybrid_kernel_ms": round(ms_hybrid, 4),
+        "compress_ms": round(ms_compress, 4),
+        "compress_gbs": round(cbytes / (ms_compress * 1e-3) / 1e9, 1),
+        "compress_hbm_frac": round(cbytes / (ms_compress * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "hybrid_tflops": round(hyb_tflops, 1),
+        "hybrid_mfma_frac": round(hyb_tflops / BF16_PEAK_TFLOPS, 4),
+        "dense_tflops": round(dense_tflops, 1),
+        "dense_mfma_frac": round(dense_tflops / BF16_PEAK_TFLOPS, 4),
+    }
+    if not headline:
+        res["traffic"] = traffic_bytes(args, N, r_real, ratio)
+        return res
     rec = {
         "metric": "prefill attn ms/layer + speedup vs dense FA at 32K/128K, Llama-3-8B GQA",
         "value": round(ms_step, 4),
         "unit": "ms/layer",
         "n_gpus": 1,
-        "steps": args.steps,
+        "steps": steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms_step, 4),
         "higher_is_better": False,
@@ -510,31 +603,54 @@ def main():
         "vs_baseline": None,
         "dtype": args.dtype,
         "data": (f"synthetic: AR(1) keys rho=0.9 sigma=0.44 + RoPE base 5e5, Gaussian Q/V, "
-                 f"seed {args.seed}; Euclidean tau={tau:.4f} calibrated to r={args.ratio:g} "
+                 f"seed {args.seed}; Euclidean tau={tau:.4f} calibrated to r={ratio:g} "
                  f"(realised {r_real:.3f}), chunk 512, W={W}"),
         "config": {"workload": (f"config{args.config}: delta prefill attention, one layer, "
-                                f"B={B} Hq={Hq} Hkv={Hkv} D={D} N={N} {args.dtype} causal r={args.ratio:g}"),
+                                f"B={B} Hq={Hq} Hkv={Hkv} D={D} N={N} {args.dtype} causal r={ratio:g}"),
                    "seq_len": N, "global_batch": B, "parallelism": "none (1 GPU)"},
-        "speedup_vs_dense": round(ms_dense / ms_step, 3),
-        "kernel_speedup_vs_dense": round(ms_dense / ms_hybrid, 3),
-        "dense_ms_per_layer": round(ms_dense, 4),
-        "hybrid_kernel_ms": round(ms_hybrid, 4),
-        "compress_ms": round(ms_compress, 4),
-        "compress_gbs": round(cbytes / (ms_compress * 1e-3) / 1e9, 1),
-        "hybrid_tflops": round(hyb_tflops, 1),
-        "dense_tflops": round(dense_tflops, 1),
-        "dense_mfma_frac": round(dense_tflops / BF16_PEAK_TFLOPS, 4),
-        "realised_ratio": round(r_real, 3),
         "roofline": {"bound": "mfma", "achieved": round(hyb_tflops, 2), "peak": BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(hyb_tflops / BF16_PEAK_TFLOPS, 4),
-                     "traffic": traffic_bytes(args, N, r_real),
+                     "traffic": traffic_bytes(args, N, r_real, ratio),
                      "kernel": "attn_pp_kernel<hybrid> (da_hybrid_prefill)",
                      "algorithmic_flops": fl["algorithmic"]},
     }
+    rec.update({k2: v2 for k2, v2 in res.items() if k2 not in ("seq_len",)})
     if not args.no_cpu_baseline:
         log("cpu baseline (oracle sample) ...")
-        rec["cpu_baseline"] = cpu_baseline(q, k, v, tau, W, fl["algorithmic"], args.cpu_sample_blocks)
-    print(json.dumps(rec), flush=True)
+        rec["cpu_baseline"] = cpu_baseline(q, k, v, tau, W, fl["algorithmic"], dense_fl,
+                                           args.cpu_sample_blocks)
+    res["record"] = rec
+    return res
+
+
+def run_only(args):
+    """``--only``: one part of the config-1/2 layer for K launches (rocprofv3 captures)."""
+    import torch
+    from deltaattention_amd import ops, synth
+    N = args.seq or (32768 if args.config == 1 else 131072)
+    W = args.window
+    q, k, v = layer_inputs(args, N)
+    tau, r_real = synth.calibrate_threshold(k, args.ratio)
+    keep, _ = ops.select(k, tau, 512)
+    packed = ops.pack(keep, k, v)
+    out = torch.empty_like(q)
+    fns = {
+        "delta": lambda: ops.delta_prefill(q, k, v, tau, 512, window=W),
+        "hybrid": lambda: ops.hybrid_prefill(q, k, v, packed.k_packed, packed.v_packed,
+                                             packed.timestamps, packed.counts, window=W,
+                                             num_packed_dev=packed.num_packed, out=out),
+        "dense": lambda: ops.dense_prefill(q, k, v, causal=True, out=out),
+        "compress": lambda: ops.pack(ops.select(k, tau, 512)[0], k, v, out=packed),
+    }
+    if args.only == "copy":
+        src = torch.ones(1 << 29, dtype=torch.int16, device=q.device)  # 1 GiB
+        dst = torch.empty_like(src)
+        fns["copy"] = lambda: dst.copy_(src)
+    fn = fns[args.only]
+    for _ in range(args.warmup):
+        fn()
+    ms = time_loop(fn, args.steps)
+    print(f"only={args.only} N={N} r={r_real:.3f} steps={args.steps} ms/launch={ms:.4f}", flush=True)
 
 
 if __name__ == "__main__":
