@@ -17,6 +17,8 @@ DA_F16 = 2
 DA_I32 = 3
 DA_F32 = 4
 DA_VARIANT = {"hybrid": 0, "sanity": 1, "pure_phase1": 2}
+DA_SELECT_COSINE = 1
+DA_SELECT_ARITH16 = 2
 DA_NUM_STRIDES = 24
 
 # (name, restype, argtypes) for every symbol of include/deltaattn.h

@@ -86,7 +86,8 @@ def keep_mask(key_states: torch.Tensor):
     keep, chunk_counts = ops.select(key_states, getattr(globVR, "row_delta_threshold", 0.0),
                                     chunk_size=fixed if fixed > 0 else 0,
                                     divide_to=0 if fixed > 0 else divide_to,
-                                    metric=getattr(globVR, "row_similarity_metric", "euclidean"))
+                                    metric=getattr(globVR, "row_similarity_metric", "euclidean"),
+                                    arith=getattr(globVR, "row_delta_arith", "fp32"))
     return keep, chunk_counts.sum(dim=-1, dtype=torch.int32)
 
 
@@ -152,7 +153,8 @@ def delta_decode_handoff(key_states: torch.Tensor, value_states: torch.Tensor, l
     keep, _ = ops.select(key_states, getattr(globVR, "row_delta_threshold", 0.0),
                          chunk_size=fixed if fixed > 0 else 0,
                          divide_to=0 if fixed > 0 else divide_to,
-                         metric=getattr(globVR, "row_similarity_metric", "euclidean"))
+                         metric=getattr(globVR, "row_similarity_metric", "euclidean"),
+                         arith=getattr(globVR, "row_delta_arith", "fp32"))
     packed = ops.pack(keep, key_states, value_states)               # :836-866
     _handoff(past_key_value, layer_idx, packed, key_states, value_states)   # :868-879
 

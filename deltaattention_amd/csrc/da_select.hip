@@ -14,6 +14,12 @@
 // (r0 + r1) + (r2 + r3).  No multiply-add is fused, so the result is bit-identical
 // to the CPU restatement of the same tree.
 //
+// With A16 (DA_SELECT_ARITH16) the Euclidean distance rounds every difference, square
+// and tree addition to the keys' 16-bit type, as the reference's Triton code evaluates
+// curr - ref, diff * diff and tl.sum on 16-bit tensors (tritonModules.py:55-58); only
+// the reduction order stays the fixed tree.  The cosine test is fp32 either way (the
+// reference upcasts it, :48-54).
+//
 // Rows are prefetched 32 at a time one batch ahead, since loads never depend on
 // the decisions.  The distance reaches every lane through v_permlane16/32_swap (no
 // scalar round trip), the anchor update is a select, and a batch's decisions collect
@@ -24,9 +30,30 @@ namespace da {
 
 constexpr int kSelBatch = 32;
 
+// x rounded to the 16-bit type DT (nearest even) and widened back to fp32.
+template <int DT>
+__device__ __forceinline__ float round16(float x) {
+  return E16<DT>::one(E16<DT>::bits(x));
+}
+
+// wave_tree_sum_all with every addition rounded to DT: the same pairing (DPP lane^1,
+// lane^2, 8-lane and 16-lane mirror, then (r0 + r1) + (r2 + r3)).
+template <int DT>
+__device__ __forceinline__ float wave_tree_sum_all_r16(float t) {
+#pragma clang fp contract(off)
+  t = round16<DT>(t + dpp_f32<kDppXor1>(t));
+  t = round16<DT>(t + dpp_f32<kDppXor2>(t));
+  t = round16<DT>(t + dpp_f32<kDppHalfMirror>(t));
+  t = round16<DT>(t + dpp_f32<kDppMirror>(t));
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(t), __float_as_uint(t), false, false);
+  const float u = round16<DT>(__uint_as_float(r[0]) + __uint_as_float(r[1]));
+  const auto q = __builtin_amdgcn_permlane32_swap(__float_as_uint(u), __float_as_uint(u), false, false);
+  return round16<DT>(__uint_as_float(q[0]) + __uint_as_float(q[1]));
+}
+
 // One key of the walk: the decision and the anchor update without a branch (the
 // decision is the same in every lane).
-template <bool COS, int DT>
+template <bool COS, bool A16, int DT>
 __device__ __forceinline__ bool select_step(uint32_t xb, float& a0, float& a1, float& a_norm,
                                             float thr) {
 #pragma clang fp contract(off)
@@ -39,6 +66,10 @@ __device__ __forceinline__ bool select_step(uint32_t xb, float& a0, float& a1, f
     x_norm = __fsqrt_rn(wave_tree_sum_all(pair_dot(x0, x1, x0, x1)) + eps);
     const float sim = __fdiv_rn(dot, x_norm * a_norm);
     kp = sim < thr;
+  } else if (A16) {  // tritonModules.py:55-58 in the keys' 16-bit arithmetic
+    const float d0 = round16<DT>(x0 - a0), d1 = round16<DT>(x1 - a1);
+    const float p0 = round16<DT>(d0 * d0), p1 = round16<DT>(d1 * d1);
+    kp = wave_tree_sum_all_r16<DT>(round16<DT>(p0 + p1)) > thr;
   } else {  // tritonModules.py:55-58
     const float d0 = x0 - a0, d1 = x1 - a1;
     kp = wave_tree_sum_all(pair_dot(d0, d1, d0, d1)) > thr;
@@ -49,7 +80,7 @@ __device__ __forceinline__ bool select_step(uint32_t xb, float& a0, float& a1, f
   return kp;
 }
 
-template <bool COS, int DT>
+template <bool COS, bool A16, int DT>
 __global__ __launch_bounds__(256) void select_kernel(
     const uint16_t* __restrict__ k, int64_t sk_b, int64_t sk_h, int64_t sk_n, int H, int64_t N,
     int D, int64_t cs, int64_t nc, int64_t total_chunks, float thr, int32_t* __restrict__ keep,
@@ -94,11 +125,11 @@ __global__ __launch_bounds__(256) void select_kernel(
     if (i0 + kSelBatch <= e) {
 #pragma unroll
       for (int j = 0; j < kSelBatch; ++j)
-        bb |= (uint32_t)select_step<COS, DT>(cur[j], a0, a1, a_norm, thr) << j;
+        bb |= (uint32_t)select_step<COS, A16, DT>(cur[j], a0, a1, a_norm, thr) << j;
     } else {
 #pragma unroll
       for (int j = 0; j < kSelBatch; ++j)
-        if (i0 + j < e) bb |= (uint32_t)select_step<COS, DT>(cur[j], a0, a1, a_norm, thr) << j;
+        if (i0 + j < e) bb |= (uint32_t)select_step<COS, A16, DT>(cur[j], a0, a1, a_norm, thr) << j;
     }
     count += __builtin_popcount(bb);  // tritonModules.py:68
     if (lane < kSelBatch && i0 + lane < e) keep_row[i0 + lane] = (int32_t)((bb >> lane) & 1u);
@@ -113,10 +144,13 @@ __global__ __launch_bounds__(256) void select_kernel(
 using namespace da;
 
 extern "C" int da_select(const void* k, int dtype, int64_t B, int64_t Hkv, int64_t N, int64_t D,
-                         int64_t sk_b, int64_t sk_h, int64_t sk_n, float threshold, int use_cosine,
+                         int64_t sk_b, int64_t sk_h, int64_t sk_n, float threshold, int flags,
                          int64_t chunk_size, int64_t num_chunks, int32_t* keep,
                          int32_t* chunk_counts, void* stream) {
   DA_REQUIRE(k && keep && chunk_counts, "da_select: null pointer");
+  DA_REQUIRE((flags & ~(DA_SELECT_COSINE | DA_SELECT_ARITH16)) == 0, "da_select: unknown flags 0x%x", flags);
+  const bool use_cosine = flags & DA_SELECT_COSINE;
+  const bool a16 = !use_cosine && (flags & DA_SELECT_ARITH16);
   if (dtype != DA_BF16 && dtype != DA_F16)
     return set_error(DA_ERR_UNSUPPORTED, "da_select: keys must be bf16 or fp16");
   DA_REQUIRE(B > 0 && Hkv > 0 && N > 0 && D > 0, "da_select: empty shape");
@@ -129,16 +163,18 @@ extern "C" int da_select(const void* k, int dtype, int64_t B, int64_t Hkv, int64
   const int64_t blocks = (total + 3) / 4;
   DA_REQUIRE(blocks < (1ll << 31), "da_select: too many chunks");
   hipStream_t st = (hipStream_t)stream;
-#define DA_SELECT_LAUNCH(COS, DT)                                                                       \
-  hipLaunchKernelGGL((select_kernel<COS, DT>), dim3((unsigned)blocks), dim3(256), 0, st, (const uint16_t*)k, \
+#define DA_SELECT_LAUNCH(COS, A16, DT)                                                                       \
+  hipLaunchKernelGGL((select_kernel<COS, A16, DT>), dim3((unsigned)blocks), dim3(256), 0, st, (const uint16_t*)k, \
                      sk_b, sk_h, sk_n, (int)Hkv, N, (int)D, chunk_size, num_chunks, total, threshold, keep,  \
                      chunk_counts)
   if (dtype == DA_F16) {
-    if (use_cosine) DA_SELECT_LAUNCH(true, DA_F16);
-    else DA_SELECT_LAUNCH(false, DA_F16);
+    if (use_cosine) DA_SELECT_LAUNCH(true, false, DA_F16);
+    else if (a16) DA_SELECT_LAUNCH(false, true, DA_F16);
+    else DA_SELECT_LAUNCH(false, false, DA_F16);
   } else {
-    if (use_cosine) DA_SELECT_LAUNCH(true, DA_BF16);
-    else DA_SELECT_LAUNCH(false, DA_BF16);
+    if (use_cosine) DA_SELECT_LAUNCH(true, false, DA_BF16);
+    else if (a16) DA_SELECT_LAUNCH(false, true, DA_BF16);
+    else DA_SELECT_LAUNCH(false, false, DA_BF16);
   }
 #undef DA_SELECT_LAUNCH
   return check_launch("da_select");

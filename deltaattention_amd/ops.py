@@ -58,15 +58,30 @@ def chunking(seq_len: int, chunk_size: int = 0, divide_to: int = 0) -> Tuple[int
     return (seq_len + parts - 1) // parts, parts
 
 
+SELECT_ARITH = ("fp32", "native")
+
+
+def _select_flags(metric: str, arith: str) -> int:
+    if arith not in SELECT_ARITH:
+        raise ValueError(f"arith must be one of {SELECT_ARITH}, got {arith!r}")
+    if metric == "cosine":
+        return _native.DA_SELECT_COSINE
+    return _native.DA_SELECT_ARITH16 if arith == "native" else 0
+
+
 def select(k: torch.Tensor, threshold: float, chunk_size: int = 512, divide_to: int = 0,
            metric: str = "euclidean", keep: Optional[torch.Tensor] = None,
-           chunk_counts: Optional[torch.Tensor] = None) -> Tuple[torch.Tensor, torch.Tensor]:
+           chunk_counts: Optional[torch.Tensor] = None,
+           arith: str = "fp32") -> Tuple[torch.Tensor, torch.Tensor]:
     """Delta-mode anchor selection (tritonModules.py:7-69 via modeling_llama.py:634-653).
 
     ``metric == "cosine"`` selects the cosine test (keep iff cos < threshold); every
     other string is Euclidean (keep iff ||k - anchor||^2 > threshold^2), exactly as
-    modeling_llama.py:639-642.  Returns keep [B, Hkv, N] int32 and chunk counts
-    [B, Hkv, num_chunks] int32.
+    modeling_llama.py:639-642.  ``arith="native"`` evaluates the Euclidean distance in
+    the keys' own 16-bit arithmetic (every difference, square and tree addition rounded,
+    as the reference's Triton code does on bf16 / fp16 keys, tritonModules.py:55-58);
+    the default "fp32" keeps them in fp32.  Both reduce over the same fixed tree.
+    Returns keep [B, Hkv, N] int32 and chunk counts [B, Hkv, num_chunks] int32.
     """
     _require_device(k)
     dt = _require_half(k)
@@ -80,7 +95,7 @@ def select(k: torch.Tensor, threshold: float, chunk_size: int = 512, divide_to: 
     if chunk_counts is None:
         chunk_counts = torch.empty((B, H, nc), dtype=torch.int32, device=k.device)
     rc = lib().da_select(k.data_ptr(), dt, B, H, N, D, k.stride(0), k.stride(1), k.stride(2),
-                         ctypes.c_float(thr), 1 if use_cos else 0, cs, nc, keep.data_ptr(),
+                         ctypes.c_float(thr), _select_flags(metric, arith), cs, nc, keep.data_ptr(),
                          chunk_counts.data_ptr(), _stream())
     check(rc, "da_select")
     return keep, chunk_counts
@@ -233,14 +248,15 @@ def delta_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, threshold: 
                   chunk_size: int = 512, divide_to: int = 0, metric: str = "euclidean",
                   window: int = 128, scale: Optional[float] = None, variant: str = "hybrid",
                   no_count: bool = False, keep: Optional[torch.Tensor] = None,
-                  return_packed: bool = False, out: Optional[torch.Tensor] = None):
+                  return_packed: bool = False, out: Optional[torch.Tensor] = None,
+                  arith: str = "fp32"):
     """select -> pack -> hybrid prefill with P kept on the device (no host sync).
 
     Restates PATH 1 of LlamaAttention.forward (modeling_llama.py:600-749) for the delta
     packing mode; pass ``keep`` to use a mask from another packing mode.
     """
     if keep is None:
-        keep, _ = select(k, threshold, chunk_size, divide_to, metric)
+        keep, _ = select(k, threshold, chunk_size, divide_to, metric, arith=arith)
     packed = pack(keep, k, v)
     out = hybrid_prefill(q, k, v, packed.k_packed, packed.v_packed, packed.timestamps,
                          packed.counts, window=window, scale=scale, variant=variant,

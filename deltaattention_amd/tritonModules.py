@@ -49,9 +49,19 @@ class _ChunkedEval(KernelLauncher):
             raise ValueError("chunk_counts must be a contiguous [B, H, num_chunks] tensor")
         rc = lib().da_select(k.data_ptr(), dtype_code(k), B, H, N, D, int(a["stride_in_b"]),
                              int(a["stride_in_h"]), int(a["stride_in_s"]),
-                             ctypes.c_float(float(a["threshold_sq"])), 1 if a["USE_COSINE"] else 0,
+                             ctypes.c_float(float(a["threshold_sq"])), _flags(bool(a["USE_COSINE"])),
                              int(a["chunk_size"]), nc, keep.data_ptr(), cc.data_ptr(), _stream())
         check(rc, "chunked_eval_kernel")
+
+
+def _flags(use_cosine: bool) -> int:
+    """da_select flags: the cosine test, or the Euclidean distance in fp32 or (with
+    globVR.row_delta_arith == "native") in the keys' 16-bit arithmetic."""
+    from . import globVR
+    from ._native import DA_SELECT_ARITH16, DA_SELECT_COSINE
+    if use_cosine:
+        return DA_SELECT_COSINE
+    return DA_SELECT_ARITH16 if getattr(globVR, "row_delta_arith", "fp32") == "native" else 0
 
 
 class _ScatterPack(KernelLauncher):

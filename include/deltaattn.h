@@ -55,15 +55,22 @@ int da_version(void);
  * k: [B, Hkv, N, D] bf16 or fp16 (dtype DA_BF16 / DA_F16), strides (sk_b, sk_h, sk_n),
  * D even and <= 128.
  * threshold: tau^2 for Euclidean, tau for cosine (modeling_llama.py:641-642).
+ * flags: DA_SELECT_COSINE selects the cosine test (keep iff cos < tau, else Euclidean
+ *   keep iff dist^2 > tau^2); DA_SELECT_ARITH16 evaluates the Euclidean distance in the
+ *   keys' 16-bit arithmetic (every difference, square and tree addition rounded to
+ *   bf16 / fp16, as the reference's Triton code does on 16-bit keys,
+ *   tritonModules.py:55-58); without it the distance is fp32.
  * chunk_size / num_chunks: from the chunking rule of modeling_llama.py:602-610.
  * keep: [B, Hkv, N] int32 contiguous, 1 for anchors and 0 otherwise (rows of
  *   chunks that start at or beyond N are not written).
  * chunk_counts: [B, Hkv, num_chunks] int32 contiguous (0 for empty chunks).
- * The squared distance (or cosine) is fp32 over a fixed pairwise reduction
- * tree, so the result is deterministic and bit-identical to the CPU oracle.
+ * The squared distance (or cosine) is reduced over a fixed pairwise tree, so the
+ * result is deterministic and bit-identical to the CPU oracle.
  */
+#define DA_SELECT_COSINE 1
+#define DA_SELECT_ARITH16 2
 int da_select(const void* k, int dtype, int64_t B, int64_t Hkv, int64_t N, int64_t D,
-              int64_t sk_b, int64_t sk_h, int64_t sk_n, float threshold, int use_cosine,
+              int64_t sk_b, int64_t sk_h, int64_t sk_n, float threshold, int flags,
               int64_t chunk_size, int64_t num_chunks, int32_t* keep, int32_t* chunk_counts,
               void* stream);
 

@@ -32,7 +32,7 @@ __all__ = [
     "BLOCK_M", "BLOCK_N", "chunking", "tree_sum", "select_delta", "select_periodic",
     "index_map", "pack", "hybrid_schedule", "hybrid_attention", "hybrid_bruteforce",
     "dense_attention", "dense_bruteforce", "decode_update", "decode_attention",
-    "to_bf16", "bf16_round",
+    "to_bf16", "bf16_round", "f16_round",
 ]
 
 
@@ -79,17 +79,34 @@ def _tree_width(d: int) -> int:
     return w
 
 
-def tree_sum(x: np.ndarray) -> np.ndarray:
+def f16_round(x: np.ndarray) -> np.ndarray:
+    """Round float32 values to the nearest IEEE binary16 (ties to even, beyond 65504 to
+    infinity); returns float32."""
+    with np.errstate(over="ignore"):
+        return np.asarray(x, dtype=np.float32).astype(np.float16).astype(np.float32)
+
+
+def round16(x: np.ndarray, arith: str) -> np.ndarray:
+    """x rounded to the 16-bit type named by ``arith`` ("bf16", "fp16"); "fp32" keeps it."""
+    if arith == "bf16":
+        return bf16_round(x)
+    if arith == "fp16":
+        return f16_round(x)
+    return np.asarray(x, dtype=np.float32)
+
+
+def tree_sum(x: np.ndarray, arith: str = "fp32") -> np.ndarray:
     """Perfect pairwise fp32 tree sum over the last axis, zero-padded to 128 slots
     (or the next power of two above 128).  This is the build's fixed reduction
-    order for the selection distance (see module docstring)."""
+    order for the selection distance (see module docstring).  With ``arith`` "bf16" /
+    "fp16" every addition is rounded to that type."""
     x = np.asarray(x, dtype=np.float32)
     d = x.shape[-1]
     w = _tree_width(d)
     t = np.zeros(x.shape[:-1] + (w,), dtype=np.float32)
     t[..., :d] = x
     while t.shape[-1] > 1:
-        t = t[..., 0::2] + t[..., 1::2]
+        t = round16(t[..., 0::2] + t[..., 1::2], arith)
     return t[..., 0]
 
 
@@ -102,12 +119,16 @@ def select_threshold(threshold: float, metric: str) -> np.float32:
 
 
 def select_delta(k: np.ndarray, threshold: float, chunk_size: int = 512, divide_to: int = 0,
-                 metric: str = "euclidean") -> Tuple[np.ndarray, np.ndarray]:
+                 metric: str = "euclidean", arith: str = "fp32") -> Tuple[np.ndarray, np.ndarray]:
     """Delta-mode anchor selection (tritonModules.py:7-69, launch modeling_llama.py:634-653).
 
     Returns keep [B,H,N] int32 and chunk_counts [B,H,nc] int32.  Only the exact string
     "cosine" selects the cosine metric (modeling_llama.py:639-640); every other string is
-    Euclidean.  Pure numpy loop; use ``select_oracle_c.select_delta`` for large inputs.
+    Euclidean.  ``arith`` "bf16" / "fp16" rounds the Euclidean distance's differences,
+    squares and tree additions to that type, as the reference's Triton code computes
+    curr - ref, diff * diff and tl.sum on 16-bit keys (tritonModules.py:55-58; the cosine
+    branch upcasts to fp32 there, :48-54, and stays fp32 here).  Pure numpy loop; use
+    ``select_oracle_c.select_delta`` for large inputs.
     """
     k32 = np.asarray(k, dtype=np.float32)
     B, H, N, D = k32.shape
@@ -136,8 +157,8 @@ def select_delta(k: np.ndarray, threshold: float, chunk_size: int = 512, divide_
                         sim = np.float32(dot / np.float32(nx * a_norm))
                         kp = bool(sim < thr)
                     else:                       # tritonModules.py:55-58
-                        diff = x - a
-                        kp = bool(tree_sum(diff * diff) > thr)
+                        diff = round16(x - a, arith)
+                        kp = bool(tree_sum(round16(diff * diff, arith), arith) > thr)
                     if kp:                      # tritonModules.py:60-63
                         keep[b, h, i] = 1
                         a = x

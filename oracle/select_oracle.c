@@ -11,10 +11,51 @@
  * order; oracle/delta_oracle.py restates the same definition in numpy and the HIP
  * kernel computes the same tree.  Build with -ffp-contract=off so that no
  * multiply-add is fused.
+ *
+ * With arith16 = 1 (bf16) or 2 (fp16) the Euclidean distance rounds every elementwise
+ * difference, square and tree addition to the keys' 16-bit type, as the reference's
+ * Triton code does when it evaluates curr - ref, diff * diff and tl.sum on 16-bit
+ * tensors (tritonModules.py:55-58); only the reduction order stays the build's tree.
  */
 #include <math.h>
 #include <stdint.h>
 #include <string.h>
+
+/* round-to-nearest-even to bf16, returned as float (inf and NaN pass through) */
+static float bf16r(float x) {
+  uint32_t u;
+  memcpy(&u, &x, 4);
+  if ((u & 0x7f800000u) == 0x7f800000u) return x;
+  u = (u + 0x7fffu + ((u >> 16) & 1u)) & 0xffff0000u;
+  memcpy(&x, &u, 4);
+  return x;
+}
+
+/* round-to-nearest-even to IEEE binary16, returned as float */
+static float f16r(float x) {
+  uint32_t u;
+  memcpy(&u, &x, 4);
+  const uint32_t sign = u & 0x80000000u;
+  uint32_t a = u & 0x7fffffffu;
+  if (a >= 0x7f800000u) return x;                 /* inf, NaN */
+  if (a >= 0x477ff000u) {                         /* >= 65520 rounds to infinity */
+    u = sign | 0x7f800000u;
+    memcpy(&x, &u, 4);
+    return x;
+  }
+  if (a < 0x38800000u) {                          /* below 2^-14: quantum 2^-24 */
+    const float q = nearbyintf(fabsf(x) * 16777216.0f) / 16777216.0f;
+    return sign ? -q : q;
+  }
+  a = (a + 0xfffu + ((a >> 13) & 1u)) & ~0x1fffu; /* keep 10 mantissa bits */
+  u = sign | a;
+  memcpy(&x, &u, 4);
+  return x;
+}
+
+static float round16(float x, int arith16) {
+  return arith16 == 1 ? bf16r(x) : (arith16 == 2 ? f16r(x) : x);
+}
 
 static int tree_width(int d) {
   int w = 128;
@@ -22,42 +63,44 @@ static int tree_width(int d) {
   return w;
 }
 
-/* pairwise tree sum of t[0..w), destroys t */
-static float tree_reduce(float* t, int w) {
+/* pairwise tree sum of t[0..w), destroys t; every addition rounded per arith16 */
+static float tree_reduce(float* t, int w, int arith16) {
   while (w > 1) {
-    for (int j = 0; j < w / 2; ++j) t[j] = t[2 * j] + t[2 * j + 1];
+    for (int j = 0; j < w / 2; ++j) t[j] = round16(t[2 * j] + t[2 * j + 1], arith16);
     w /= 2;
   }
   return t[0];
 }
 
-static float sq_dist(const float* x, const float* a, int d, int w, float* t) {
+static float sq_dist(const float* x, const float* a, int d, int w, float* t, int arith16) {
   for (int j = 0; j < w; ++j) {
     if (j < d) {
-      float df = x[j] - a[j];
-      t[j] = df * df;
+      float df = round16(x[j] - a[j], arith16);
+      t[j] = round16(df * df, arith16);
     } else {
       t[j] = 0.0f;
     }
   }
-  return tree_reduce(t, w);
+  return tree_reduce(t, w, arith16);
 }
 
 static float dotp(const float* x, const float* a, int d, int w, float* t) {
   for (int j = 0; j < w; ++j) t[j] = (j < d) ? x[j] * a[j] : 0.0f;
-  return tree_reduce(t, w);
+  return tree_reduce(t, w, 0);
 }
 
 /*
  * k: float32 [B, H, N, D] contiguous.  thr: tau^2 (Euclidean) or tau (cosine) as fp32.
  * keep: int32 [B, H, N] (written for every row of every non-empty chunk; rows of
  * empty chunks are left untouched, as in the reference), counts: int32 [B, H, nc].
- * Returns 0, or -1 for an unsupported head_dim.
+ * arith16: 0 fp32 distance, 1 / 2 Euclidean distance in bf16 / fp16 arithmetic (the
+ * cosine test is always fp32: the reference upcasts it, tritonModules.py:48-54).
+ * Returns 0, or -1 for an unsupported head_dim or arith16.
  */
 int oracle_select_delta(const float* k, int64_t B, int64_t H, int64_t N, int64_t D,
-                        float thr, int64_t cs, int64_t nc, int use_cos,
+                        float thr, int64_t cs, int64_t nc, int use_cos, int arith16,
                         int32_t* keep, int32_t* counts) {
-  if (D <= 0 || D > 1024) return -1;
+  if (D <= 0 || D > 1024 || arith16 < 0 || arith16 > 2) return -1;
   int w = tree_width((int)D);
   float t[1024];
   const float eps = 1e-8f;
@@ -83,7 +126,7 @@ int oracle_select_delta(const float* k, int64_t B, int64_t H, int64_t N, int64_t
           float sim = dot / prod;
           kp_i = sim < thr;
         } else {                                 /* :55-58 */
-          kp_i = sq_dist(x, a, (int)D, w, t) > thr;
+          kp_i = sq_dist(x, a, (int)D, w, t, arith16) > thr;
         }
         if (kp_i) {                              /* :60-63 */
           kp[i] = 1;

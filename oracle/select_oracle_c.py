@@ -34,15 +34,22 @@ def _load():
         lib.oracle_select_delta.restype = ctypes.c_int
         lib.oracle_select_delta.argtypes = [
             ctypes.c_void_p, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64, ctypes.c_int64,
-            ctypes.c_float, ctypes.c_int64, ctypes.c_int64, ctypes.c_int,
+            ctypes.c_float, ctypes.c_int64, ctypes.c_int64, ctypes.c_int, ctypes.c_int,
             ctypes.c_void_p, ctypes.c_void_p]
         _lib = lib
     return _lib
 
 
+ARITH = {"fp32": 0, "bf16": 1, "fp16": 2}
+
+
 def select_delta(k: np.ndarray, threshold: float, chunk_size: int = 512, divide_to: int = 0,
-                 metric: str = "euclidean") -> Tuple[np.ndarray, np.ndarray]:
-    """keep [B,H,N] int32, chunk_counts [B,H,nc] int32 (see delta_oracle.select_delta)."""
+                 metric: str = "euclidean", arith: str = "fp32") -> Tuple[np.ndarray, np.ndarray]:
+    """keep [B,H,N] int32, chunk_counts [B,H,nc] int32 (see delta_oracle.select_delta).
+
+    ``arith`` "bf16" / "fp16" rounds every difference, square and tree addition of the
+    Euclidean distance to that type (the reference's 16-bit Triton arithmetic,
+    tritonModules.py:55-58); "fp32" is the build's default definition."""
     k32 = np.ascontiguousarray(k, dtype=np.float32)
     B, H, N, D = k32.shape
     cs, nc = chunking(N, chunk_size, divide_to)
@@ -51,7 +58,7 @@ def select_delta(k: np.ndarray, threshold: float, chunk_size: int = 512, divide_
     counts = np.zeros((B, H, nc), dtype=np.int32)
     rc = _load().oracle_select_delta(
         k32.ctypes.data, B, H, N, D, ctypes.c_float(float(thr)), cs, nc,
-        1 if metric == "cosine" else 0, keep.ctypes.data, counts.ctypes.data)
+        1 if metric == "cosine" else 0, ARITH[arith], keep.ctypes.data, counts.ctypes.data)
     if rc != 0:
         raise ValueError(f"oracle_select_delta failed ({rc}) for head_dim {D}")
     return keep, counts

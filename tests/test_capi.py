@@ -49,6 +49,9 @@ def test_select_rejects_null_and_dtype():
     assert "head_dim" in _err()
     assert lib.da_select(fake, 1, 1, 1, 8, 128, 0, 0, 129, f, 0, 8, 1, fake, fake, None) == -1
     assert lib.da_select(fake, 1, 1, 1, 8, 128, 0, 0, 128, f, 0, 0, 1, fake, fake, None) == -1
+    # flags: DA_SELECT_COSINE | DA_SELECT_ARITH16 only
+    assert lib.da_select(fake, 1, 1, 1, 8, 128, 0, 0, 128, f, 4, 8, 1, fake, fake, None) == -1
+    assert "flags" in _err()
 
 
 def test_pack_rejects_small_workspace():

@@ -71,6 +71,24 @@ def test_select_bitexact_config1_shape(gpu):
         assert (keep.cpu().numpy() == ok).all()
 
 
+@pytest.mark.parametrize("dtype,oracle_arith", [(torch.bfloat16, "bf16"), (torch.float16, "fp16")])
+def test_select_native_arith_bitexact(gpu, dtype, oracle_arith):
+    """arith="native": the Euclidean distance in the keys' 16-bit arithmetic, bit-exact
+    against the oracle's 16-bit mode, at N=3000 (chunk 512 and divide_to) and at the
+    config-1 key shape; the two definitions differ on some rows."""
+    from deltaattention_amd import ops, synth
+    k = _bf16_inputs(2, 2, 2, 3000, 128, seed=12)[1].to(dtype)
+    kc = synth.make_layer_inputs(1, 8, 8, 32768, 128, seed=0)[1].to(dtype)
+    for kk, tau, chunk, div in ((k, 9.0, 512, 0), (k, 8.0, 0, 3), (kc, 10.3327, 512, 0)):
+        announce(f"select native arith {dtype} N={kk.shape[2]} tau={tau}")
+        keep, cc = ops.select(kk.to(gpu), tau, chunk, div, arith="native")
+        ok, occ = OC.select_delta(kk.float().numpy(), tau, chunk, div, arith=oracle_arith)
+        assert np.array_equal(cc.cpu().numpy(), occ)
+        assert np.array_equal(keep.cpu().numpy(), ok)
+    k32, _ = OC.select_delta(kc.float().numpy(), 10.3327, 512)
+    assert not np.array_equal(k32, ok)
+
+
 @pytest.mark.parametrize("N,tau", [(3000, 10.0), (777, 7.0), (4096, 0.0)])
 def test_pack_exact(gpu, N, tau):
     from deltaattention_amd import ops
