@@ -356,8 +356,9 @@ def run_decode(args):
 def run_config4(args):
     """Config 4: a packed ragged batch of 8 sequences with N_b ~ U[4096, 32768] tokens,
     AR(1) keys with rho ~ U[0.6, 0.95] per (sequence, KV head), one tau calibrated to r
-    on the whole batch; each sequence is a B = 1 delta prefill (ops.delta_prefill_varlen)
-    against the dense varlen prefill.  Prints one JSON line."""
+    on the whole batch.  ops.delta_prefill_varlen runs every sequence as a B = 1 delta
+    prefill with one launch per stage over the whole batch (cu_seqlens on the device),
+    against the dense varlen prefill (one launch).  Prints one JSON line."""
     import numpy as np
     import torch
     from deltaattention_amd import ops, synth
@@ -379,17 +380,15 @@ def run_config4(args):
     T = cu[-1]
     log(f"config 4: lens {lens}, {T} tokens")
     tau, _ = synth.calibrate_threshold(k.permute(1, 0, 2).unsqueeze(0), args.ratio)
-    kept = 0
-    for s0, e0 in zip(cu[:-1], cu[1:]):
-        keep, _ = ops.select(k[s0:e0].permute(1, 0, 2).unsqueeze(0), tau, 512)
-        kept += int(keep.sum().item())
-    r_real = T * Hkv / kept
+    vb = ops.varlen_batch(cu, T, dev)
+    keep, _ = ops.select_varlen(k, vb, tau, 512)
+    r_real = T * Hkv / int(keep.sum().item())
 
     def delta():
-        return ops.delta_prefill_varlen(q, k, v, cu, tau, 512, window=args.window)
+        return ops.delta_prefill_varlen(q, k, v, vb, tau, 512, window=args.window)
 
     def dense():
-        return ops.dense_prefill_varlen(q, k, v, cu)
+        return ops.dense_prefill_varlen(q, k, v, vb)
 
     res = {}
     for name, fn in (("delta", delta), ("dense", dense)):

@@ -34,6 +34,15 @@ SIGNATURES = {
     "da_hybrid_prefill": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _P, _I, _L, _L, _L, _L, _L, _L, _P,
                                _L, _P, _L, _F, _I, _I, _P, _L, _P]),
     "da_dense_prefill": (_I, [_P, _P, _P, _P, _I, _L, _L, _L, _L, _L, _L, _P, _I, _F, _P]),
+    "da_select_varlen": (_I, [_P, _I, _L, _L, _L, _L, _L, _L, _P, _L, _F, _I, _L, _L, _P, _P, _L, _P]),
+    "da_pack_varlen_workspace_size": (_L, [_L, _L, _L]),
+    "da_pack_varlen": (_I, [_P, _P, _P, _I, _L, _L, _L, _L, _L, _L, _L, _L, _P, _L, _P, _P, _P, _P,
+                            _P, _P, _P, _L, _P]),
+    "da_hybrid_varlen_workspace_size": (_L, [_L, _L, _L]),
+    "da_hybrid_prefill_varlen": (_I, [_P, _P, _P, _P, _P, _P, _P, _I, _P, _I, _L, _L, _L, _L, _L,
+                                      _P, _P, _L, _P, _L, _F, _I, _I, _P, _L, _P]),
+    "da_dense_prefill_varlen": (_I, [_P, _P, _P, _P, _I, _L, _L, _L, _L, _L, _P, _P, _L, _I, _F,
+                                     _P]),
     "da_decode_update": (_I, [_P, _P, _I, _L, _L, _L, _L, _L, _P, _P, _L, _L, _L, _P, _P, _L, _L,
                               _L, _P, _P, _L, _L, _P, _L, _L, _L, _L, _F, _I, _P]),
     "da_decode_workspace_size": (_L, [_L, _L, _L, _L]),

@@ -78,9 +78,10 @@ struct AttnArgs {
   int64_t sts_b, sts_h;
   int64_t scnt_b, scnt_h;
   int B, Hq, Hkv, G, Nq, Nk;
+  SeqMap seq;  // ragged batch (varlen): every sequence has Nq = Nk = seq.len(b)
   int D;  // head dimension: a multiple of 8, at most 128 (dims D..127 are zero-filled)
   int P_host;
-  const int32_t* P_dev;
+  const int32_t* P_dev;  // P on the device ([B], one per sequence, for a ragged batch)
   int window;
   float scale_log2;  // softmax scale * log2(e)
   int no_count;
@@ -232,8 +233,7 @@ __device__ __forceinline__ void safe_prefix(const int32_t* __restrict__ bmax, co
 }
 
 template <int VARIANT, int DT>
-__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
-void attn_kernel(AttnArgs a) {
+__device__ __forceinline__ void attn_body(const AttnArgs& a) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar)
@@ -244,28 +244,38 @@ void attn_kernel(AttnArgs a) {
   const int wg = blockIdx.x;
   int unit, rg;
   if ((a.units & 7) == 0) {
+    // workgroup i runs on XCD i mod 8; each XCD takes whole units (a KV head of one
+    // sequence) and runs them one after another, every unit's row groups longest first,
+    // so the 32 CUs of an XCD share one unit's K/V in their L2
     const int xcd = wg & 7, idx = wg >> 3, upx = a.units >> 3;
-    unit = xcd * upx + idx % upx;
-    rg = a.n_row_groups - 1 - idx / upx;
+    unit = xcd * upx + idx / a.n_row_groups;
+    rg = a.n_row_groups - 1 - idx % a.n_row_groups;
   } else {
     unit = wg % a.units;
     rg = a.n_row_groups - 1 - wg / a.units;
   }
+  // units are KV-head major, so that the XCD mapping above gives each XCD whole KV
+  // heads of every sequence (balanced when the sequences of a batch differ in length)
   const int hunits = a.G / a.hpw;
-  const int bg = unit / hunits;  // b * Hkv + g
-  const int hu = unit - bg * hunits;
-  const int b = bg / a.Hkv, g = bg - (bg / a.Hkv) * a.Hkv;
+  const int gb = unit / hunits;  // g * B + b
+  const int hu = unit - gb * hunits;
+  const int g = gb / a.B, b = gb - (gb / a.B) * a.B;
+  const int bg = b * a.Hkv + g;
   const int h = g * a.G + hu * a.hpw + (wid % a.hpw);
   const int R0 = rg * a.rows_per_wg;
+  const int Nq = a.seq.cu ? a.seq.len(b) : a.Nq;
+  const int Nk = a.seq.cu ? a.seq.len(b) : a.Nk;
+  if (R0 >= Nq) return;  // a row group past the end of a shorter sequence (whole workgroup)
   const int r0w = R0 + (wid / a.hpw) * 32;  // first row of this wave
   const int wg_end = R0 + a.rows_per_wg;    // one past the last row of the workgroup
   const int start_m = (R0 / kBlock) * kBlock;
 
   // ---- schedule ----
   int P = a.P_host;
-  if (a.P_dev) P = min(*a.P_dev, a.P_host);
+  if (a.P_dev) P = min(a.seq.cu ? a.P_dev[b] : *a.P_dev, a.P_host);
+  if (a.seq.cu) P = min(P, Nk);  // a sequence's packed rows lie inside its own tokens
   int n1 = 0, ds = 0;
-  int kend = a.causal ? min(a.Nk, wg_end) : a.Nk;
+  int kend = a.causal ? min(Nk, wg_end) : Nk;
   if (VARIANT == kHybrid || VARIANT == kSanity) {
     const int nblk = (P + kBlock - 1) / kBlock;
     const int32_t* bmax = a.sched + (int64_t)bg * 2 * a.nblk_cap;
@@ -274,7 +284,7 @@ void attn_kernel(AttnArgs a) {
     safe_prefix(bmax, pmax, nblk, start_m - a.window, n_safe, last);
     ds = max(0, ((last + 1) / kBlock) * kBlock);
     if (VARIANT == kHybrid) n1 = n_safe * (kBlock / kTileN);
-    kend = min(a.Nk, wg_end);
+    kend = min(Nk, wg_end);
   } else if (VARIANT == kPure) {
     n1 = (P + kTileN - 1) / kTileN;
     kend = 0;
@@ -282,22 +292,22 @@ void attn_kernel(AttnArgs a) {
   const int n2 = kend > ds ? (kend - ds + kTileN - 1) / kTileN : 0;
   const int ntiles = n1 + n2;
 
-  const uint16_t* kp_base = a.kp + (int64_t)b * a.skp_b + (int64_t)g * a.skp_h;
-  const uint16_t* vp_base = a.vp + (int64_t)b * a.svp_b + (int64_t)g * a.svp_h;
-  const uint16_t* k_base = a.k + (int64_t)b * a.sk_b + (int64_t)g * a.sk_h;
-  const uint16_t* v_base = a.v + (int64_t)b * a.sv_b + (int64_t)g * a.sv_h;
-  const int32_t* ts_row = a.ts ? a.ts + (int64_t)b * a.sts_b + (int64_t)g * a.sts_h : nullptr;
-  const char* cnt_row = a.cnt ? (const char*)a.cnt + ((int64_t)b * a.scnt_b + (int64_t)g * a.scnt_h) * 4 : nullptr;
+  const uint16_t* kp_base = a.kp + a.seq.base(b, a.skp_b, a.skp_n) + (int64_t)g * a.skp_h;
+  const uint16_t* vp_base = a.vp + a.seq.base(b, a.svp_b, a.svp_n) + (int64_t)g * a.svp_h;
+  const uint16_t* k_base = a.k + a.seq.base(b, a.sk_b, a.sk_n) + (int64_t)g * a.sk_h;
+  const uint16_t* v_base = a.v + a.seq.base(b, a.sv_b, a.sv_n) + (int64_t)g * a.sv_h;
+  const int32_t* ts_row = a.ts ? a.ts + a.seq.base(b, a.sts_b, 1) + (int64_t)g * a.sts_h : nullptr;
+  const char* cnt_row = a.cnt ? (const char*)a.cnt + (a.seq.base(b, a.scnt_b, 1) + (int64_t)g * a.scnt_h) * 4 : nullptr;
   const bool meta = (VARIANT == kHybrid || VARIANT == kPure);
 
   // ---- Q^T in registers (B operand): lane (ql, hl) holds dims 16t + 8hl .. +7 ----
   u32x4 qreg[kD / 16];
   {
     const int row = r0w + ql;
-    const uint16_t* qrow = a.q + (int64_t)b * a.sq_b + (int64_t)h * a.sq_h + (int64_t)row * a.sq_n;
+    const uint16_t* qrow = a.q + a.seq.base(b, a.sq_b, a.sq_n) + (int64_t)h * a.sq_h + (int64_t)row * a.sq_n;
 #pragma unroll
     for (int t = 0; t < kD / 16; ++t)
-      qreg[t] = (row < a.Nq && 16 * t + 8 * hl < a.D) ? *(const u32x4*)(qrow + 16 * t + 8 * hl)
+      qreg[t] = (row < Nq && 16 * t + 8 * hl < a.D) ? *(const u32x4*)(qrow + 16 * t + 8 * hl)
                                                        : u32x4{0, 0, 0, 0};
   }
 
@@ -314,7 +324,7 @@ void attn_kernel(AttnArgs a) {
     if (ph1) {
       kb = kp_base; vb = vp_base; skn = a.skp_n; svn = a.svp_n; key0 = t * kTileN; limit = P;
     } else {
-      kb = k_base; vb = v_base; skn = a.sk_n; svn = a.sv_n; key0 = ds + (t - n1) * kTileN; limit = a.Nk;
+      kb = k_base; vb = v_base; skn = a.sk_n; svn = a.sv_n; key0 = ds + (t - n1) * kTileN; limit = Nk;
     }
   };
 
@@ -322,7 +332,7 @@ void attn_kernel(AttnArgs a) {
     const uint16_t *kb, *vb; int64_t skn, svn; int key0, limit; bool ph1;
     tile_src(0, kb, vb, skn, svn, key0, limit, ph1);
     load_tile(regs, kb, vb, skn, svn, key0, limit, a.D, tid, meta && ph1, ts_row, cnt_row,
-              a.cnt_is_float, a.no_count, P, a.Nk + 1);
+              a.cnt_is_float, a.no_count, P, Nk + 1);
     store_tile(regs, smem, tid, meta && ph1);
   }
   __syncthreads();
@@ -335,7 +345,7 @@ void attn_kernel(AttnArgs a) {
       const uint16_t *kb, *vb; int64_t skn, svn; int key0, limit;
       tile_src(t + 1, kb, vb, skn, svn, key0, limit, next_ph1);
       load_tile(regs, kb, vb, skn, svn, key0, limit, a.D, tid, meta && next_ph1, ts_row, cnt_row,
-                a.cnt_is_float, a.no_count, P, a.Nk + 1);
+                a.cnt_is_float, a.no_count, P, Nk + 1);
     }
 
     const bool ph1 = t < n1;
@@ -368,14 +378,14 @@ void attn_kernel(AttnArgs a) {
             if (!ok) s[kb2][r] = -INFINITY;
           }
       } else if (!ph1) {
-        const bool need = (a.causal && key0 + kTileN - 1 > r0w) || key0 + kTileN > a.Nk;
+        const bool need = (a.causal && key0 + kTileN - 1 > r0w) || key0 + kTileN > Nk;
         if (need) {
 #pragma unroll
           for (int kb2 = 0; kb2 < 2; ++kb2)
 #pragma unroll
             for (int r = 0; r < 16; ++r) {
               const int key = key0 + kb2 * 32 + 8 * (r >> 2) + 4 * hl + (r & 3);
-              const bool ok = key < a.Nk && (!a.causal || key <= row);
+              const bool ok = key < Nk && (!a.causal || key <= row);
               if (!ok) s[kb2][r] = -INFINITY;
             }
         }
@@ -443,8 +453,8 @@ void attn_kernel(AttnArgs a) {
   else
     inv = 1.0f / l_tot;
   const int row = r0w + ql;
-  if (row < a.Nq) {
-    uint16_t* orow = a.out + (int64_t)b * a.so_b + (int64_t)h * a.so_h + (int64_t)row * a.so_n;
+  if (row < Nq) {
+    uint16_t* orow = a.out + a.seq.base(b, a.so_b, a.so_n) + (int64_t)h * a.so_h + (int64_t)row * a.so_n;
 #pragma unroll
     for (int db = 0; db < 4; ++db)
 #pragma unroll
@@ -455,6 +465,21 @@ void attn_kernel(AttnArgs a) {
         if (db * 32 + 8 * j + 4 * hl < a.D) *(u32x2*)(orow + db * 32 + 8 * j + 4 * hl) = w;
       }
   }
+}
+
+// Per-head kernel entry points.  Dense, hybrid and sanity fit two waves per SIMD
+// (<= 256 registers).  The pure-Phase-1 body needs more: capped at 256 it spills, and that
+// build gave wrong pure-Phase-1 outputs on every row while the same source without the
+// cap (no spills) matches the oracle, so it runs at one wave per SIMD.
+template <int VARIANT, int DT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void attn_kernel(AttnArgs a) {
+  attn_body<VARIANT, DT>(a);
+}
+template <int DT>
+__global__ __launch_bounds__(256) __attribute__((amdgpu_waves_per_eu(1, 2)))
+void attn_kernel_pure(AttnArgs a) {
+  attn_body<kPure, DT>(a);
 }
 
 // ====================================================================================
@@ -605,19 +630,27 @@ void attn_pp_kernel(AttnArgs a) {
   const int wg = blockIdx.x;
   int unit, rg;
   if ((a.units & 7) == 0) {
+    // workgroup i runs on XCD i mod 8; each XCD takes whole units (a KV head of one
+    // sequence) and runs them one after another, every unit's row groups longest first,
+    // so the 32 CUs of an XCD share one unit's K/V in their L2
     const int xcd = wg & 7, idx = wg >> 3, upx = a.units >> 3;
-    unit = xcd * upx + idx % upx;
-    rg = a.n_row_groups - 1 - idx / upx;
+    unit = xcd * upx + idx / a.n_row_groups;
+    rg = a.n_row_groups - 1 - idx % a.n_row_groups;
   } else {
     unit = wg % a.units;
     rg = a.n_row_groups - 1 - wg / a.units;
   }
+  // KV-head-major units (see attn_kernel)
   const int hunits = a.G >> 2;
-  const int bg = unit / hunits;
-  const int hu = unit - bg * hunits;
-  const int b = bg / a.Hkv, g = bg - (bg / a.Hkv) * a.Hkv;
+  const int gb = unit / hunits;  // g * B + b
+  const int hu = unit - gb * hunits;
+  const int g = gb / a.B, b = gb - (gb / a.B) * a.B;
+  const int bg = b * a.Hkv + g;
   const int h = g * a.G + hu * 4 + hw;
   const int R0 = rg * 64;
+  const int Nq = a.seq.cu ? a.seq.len(b) : a.Nq;
+  const int Nk = a.seq.cu ? a.seq.len(b) : a.Nk;
+  if (R0 >= Nq) return;  // a row group past the end of a shorter sequence (whole workgroup)
   const int r0w = R0 + grp * 32;
   const int wg_end = R0 + 64;
   const int start_m = (R0 / kBlock) * kBlock;
@@ -625,9 +658,10 @@ void attn_pp_kernel(AttnArgs a) {
 
   // ---- schedule (identical to attn_kernel) ----
   int P = a.P_host;
-  if (a.P_dev) P = min(*a.P_dev, a.P_host);
+  if (a.P_dev) P = min(a.seq.cu ? a.P_dev[b] : *a.P_dev, a.P_host);
+  if (a.seq.cu) P = min(P, Nk);  // a sequence's packed rows lie inside its own tokens
   int n1 = 0, ds = 0;
-  int kend = a.causal ? min(a.Nk, wg_end) : a.Nk;
+  int kend = a.causal ? min(Nk, wg_end) : Nk;
   if (VARIANT == kHybrid || VARIANT == kSanity) {
     const int nblk = (P + kBlock - 1) / kBlock;
     const int32_t* bmax = a.sched + (int64_t)bg * 2 * a.nblk_cap;
@@ -636,7 +670,7 @@ void attn_pp_kernel(AttnArgs a) {
     safe_prefix(bmax, pmax, nblk, start_m - a.window, n_safe, last);
     ds = max(0, ((last + 1) / kBlock) * kBlock);
     if (VARIANT == kHybrid) n1 = n_safe * (kBlock / kTileN);
-    kend = min(a.Nk, wg_end);
+    kend = min(Nk, wg_end);
   } else if (VARIANT == kPure) {
     n1 = (P + kTileN - 1) / kTileN;
     kend = 0;
@@ -644,10 +678,10 @@ void attn_pp_kernel(AttnArgs a) {
   const int n2 = kend > ds ? (kend - ds + kTileN - 1) / kTileN : 0;
   const int T = n1 + n2;
 
-  const uint16_t* kp_base = a.kp + (int64_t)b * a.skp_b + (int64_t)g * a.skp_h;
-  const uint16_t* vp_base = a.vp + (int64_t)b * a.svp_b + (int64_t)g * a.svp_h;
-  const uint16_t* k_base = a.k + (int64_t)b * a.sk_b + (int64_t)g * a.sk_h;
-  const uint16_t* v_base = a.v + (int64_t)b * a.sv_b + (int64_t)g * a.sv_h;
+  const uint16_t* kp_base = a.kp + a.seq.base(b, a.skp_b, a.skp_n) + (int64_t)g * a.skp_h;
+  const uint16_t* vp_base = a.vp + a.seq.base(b, a.svp_b, a.svp_n) + (int64_t)g * a.svp_h;
+  const uint16_t* k_base = a.k + a.seq.base(b, a.sk_b, a.sk_n) + (int64_t)g * a.sk_h;
+  const uint16_t* v_base = a.v + a.seq.base(b, a.sv_b, a.sv_n) + (int64_t)g * a.sv_h;
   const float* w_row = a.wts ? a.wts + (int64_t)bg * a.wcap : nullptr;
   const int32_t* tsw_row = a.tsw ? a.tsw + (int64_t)bg * a.wcap : nullptr;
   constexpr bool kPureV = VARIANT == kPure;
@@ -677,7 +711,7 @@ void attn_pp_kernel(AttnArgs a) {
     const int t = min(t_raw, T - 1);
     const bool ph1 = t < n1;
     const int key0 = key0_of(t);
-    const int limit = ph1 ? P : a.Nk;
+    const int limit = ph1 ? P : Nk;
     const int snb = isK ? (ph1 ? skpb : skb) : (ph1 ? svpb : svb);
     const char* src = isK ? (ph1 ? kb1 : kb2) : (ph1 ? vb1 : vb2);
     const void* base = uniform_ptr(src + (int64_t)key0 * snb);
@@ -773,7 +807,7 @@ void attn_pp_kernel(AttnArgs a) {
   u32x4 qreg[kD / 16];
   {
     // rows past Nq load row Nq - 1 (no branch between the loads) and are zeroed after
-    const uint16_t* qrow = a.q + (int64_t)b * a.sq_b + (int64_t)h * a.sq_h + (int64_t)min(row, a.Nq - 1) * a.sq_n;
+    const uint16_t* qrow = a.q + a.seq.base(b, a.sq_b, a.sq_n) + (int64_t)h * a.sq_h + (int64_t)min(row, Nq - 1) * a.sq_n;
     // dims at or beyond the head dimension load dims 0..7 and are zeroed after
     u32x4 w[kD / 16];
 #pragma unroll
@@ -787,7 +821,7 @@ void attn_pp_kernel(AttnArgs a) {
 #pragma unroll
     for (int t = 0; t < kD / 16; ++t) {
       asm volatile("" : "+v"(w[t]));
-      qreg[t] = (row < a.Nq && 16 * t + 8 * hl < a.D) ? w[t] : u32x4{0, 0, 0, 0};
+      qreg[t] = (row < Nq && 16 * t + 8 * hl < a.D) ? w[t] : u32x4{0, 0, 0, 0};
     }
   }
   if (T > 0) {
@@ -889,8 +923,8 @@ void attn_pp_kernel(AttnArgs a) {
         if (kPureV) {
           mask_pure(s, (const int*)(kst + kPPTs), row, hl);
         } else if (t >= n1) {
-          if ((a.causal && key0 + kTileN - 1 > r0w) || key0 + kTileN > a.Nk)
-            mask_dense(s, key0, row, hl, a.Nk, a.causal);
+          if ((a.causal && key0 + kTileN - 1 > r0w) || key0 + kTileN > Nk)
+            mask_dense(s, key0, row, hl, Nk, a.causal);
         }
         float mx = -INFINITY;
 #pragma unroll
@@ -947,8 +981,8 @@ void attn_pp_kernel(AttnArgs a) {
     inv = l_tot > 0.0f ? 1.0f / l_tot : 1.0f;  // deltaFlashAttention.py:353-354
   else
     inv = 1.0f / l_tot;
-  if (row < a.Nq) {
-    uint16_t* orow = a.out + (int64_t)b * a.so_b + (int64_t)h * a.so_h + (int64_t)row * a.so_n;
+  if (row < Nq) {
+    uint16_t* orow = a.out + a.seq.base(b, a.so_b, a.so_n) + (int64_t)h * a.so_h + (int64_t)row * a.so_n;
 #pragma unroll
     for (int db = 0; db < 4; ++db)
 #pragma unroll
@@ -984,7 +1018,7 @@ __global__ __launch_bounds__(256) void hybrid_schedule_kernel(const int32_t* __r
                                                               int64_t sts_b, int64_t sts_h,
                                                               int Hkv, int P_host,
                                                               const int32_t* P_dev, int Nk,
-                                                              int nblk_cap,
+                                                              SeqMap seq, int nblk_cap,
                                                               int32_t* __restrict__ sched,
                                                               SchedPrep prep) {
   __shared__ int32_t s_bmax[4096];
@@ -994,11 +1028,15 @@ __global__ __launch_bounds__(256) void hybrid_schedule_kernel(const int32_t* __r
   const int bg = blockIdx.x;
   const int b = bg / Hkv, g = bg - (bg / Hkv) * Hkv;
   int P = P_host;
-  if (P_dev) P = min(*P_dev, P_host);
+  if (P_dev) P = min(seq.cu ? P_dev[b] : *P_dev, P_host);
+  if (seq.cu) {
+    Nk = seq.len(b);
+    P = min(P, Nk);  // a sequence's packed rows lie inside its own tokens
+  }
   const int nblk = (P + kBlock - 1) / kBlock;
-  const int32_t* row = ts + (int64_t)b * sts_b + (int64_t)g * sts_h;
+  const int32_t* row = ts + seq.base(b, sts_b, 1) + (int64_t)g * sts_h;
   if (blockIdx.y > 0) {
-    const int32_t* crow = (const int32_t*)prep.cnt + (int64_t)b * prep.scnt_b + (int64_t)g * prep.scnt_h;
+    const int32_t* crow = (const int32_t*)prep.cnt + seq.base(b, prep.scnt_b, 1) + (int64_t)g * prep.scnt_h;
     float* wrow = prep.wts + (int64_t)bg * prep.wcap;
     int32_t* trow = prep.tsw ? prep.tsw + (int64_t)bg * prep.wcap : nullptr;
     const int i0 = (blockIdx.y - 1) * 1024 + tid;
@@ -1079,10 +1117,16 @@ __global__ __launch_bounds__(256) void hybrid_schedule_kernel(const int32_t* __r
 }
 
 template <int V, int DT>
+static const void* attn_kernel_fn() {
+  if constexpr (V == kPure) return reinterpret_cast<const void*>(&attn_kernel_pure<DT>);
+  else return reinterpret_cast<const void*>(&attn_kernel<V, DT>);
+}
+
+template <int V, int DT>
 static int allow_lds(size_t bytes) {
   static int done = 0;
   if (!done) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_kernel<V, DT>),
+    hipError_t e = hipFuncSetAttribute(attn_kernel_fn<V, DT>(),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
     if (e != hipSuccess) return set_error(DA_ERR_HIP, "hipFuncSetAttribute: %s", hipGetErrorString(e));
     done = 1;
@@ -1116,7 +1160,10 @@ static int launch_attn_t(AttnArgs& a, hipStream_t st) {
   const size_t lds = 2 * kStageBytes;
   const unsigned grid = (unsigned)((int64_t)a.n_row_groups * a.units);
   if (int rc = allow_lds<V, DT>(lds)) return rc;
-  hipLaunchKernelGGL((attn_kernel<V, DT>), dim3(grid), dim3(256), lds, st, a);
+  if constexpr (V == kPure)
+    hipLaunchKernelGGL((attn_kernel_pure<DT>), dim3(grid), dim3(256), lds, st, a);
+  else
+    hipLaunchKernelGGL((attn_kernel<V, DT>), dim3(grid), dim3(256), lds, st, a);
   return check_launch("attention kernel");
 }
 
@@ -1199,48 +1246,45 @@ extern "C" int64_t da_hybrid_workspace_size(int64_t B, int64_t Hkv, int64_t num_
   return hybrid_ws(B, Hkv, num_packed).total;
 }
 
-extern "C" int da_hybrid_prefill(const void* q, const void* k, const void* v, const void* k_packed,
-                                 const void* v_packed, const int32_t* timestamps,
-                                 const void* counts, int counts_dtype, void* out, int dtype,
-                                 int64_t B, int64_t Hq, int64_t Hkv, int64_t Nq, int64_t Nk,
-                                 int64_t D, const int64_t* strides, int64_t num_packed,
-                                 const int32_t* num_packed_dev, int64_t window, float scale,
-                                 int variant, int no_count, void* workspace,
-                                 int64_t workspace_bytes, void* stream) {
-  if (dtype != DA_BF16 && dtype != DA_F16)
-    return set_error(DA_ERR_UNSUPPORTED, "da_hybrid_prefill: tensors must be bf16 or fp16");
-  AttnArgs a = {};
-  int rc = fill_common(a, q, k, v, out, B, Hq, Hkv, Nq, Nk, D, strides, scale, "da_hybrid_prefill");
-  if (rc) return rc;
+// Everything of da_hybrid_prefill / da_hybrid_prefill_varlen after the shapes are known:
+// validation of the packed tensors and workspace, the schedule pre-pass, the launch.
+// P_bound is the host upper bound of P (num_packed, or the longest sequence of a ragged
+// batch), which sizes the workspace.
+static int hybrid_impl(const char* who, AttnArgs& a, const void* k_packed, const void* v_packed,
+                       const int32_t* timestamps, const void* counts, int counts_dtype, int dtype,
+                       int64_t B, int64_t Hkv, int64_t Nk, const int64_t* strides, int64_t P_bound,
+                       const int32_t* num_packed_dev, int64_t window, int variant, int no_count,
+                       void* workspace, int64_t workspace_bytes, hipStream_t st) {
   DA_REQUIRE(variant == DA_VARIANT_HYBRID || variant == DA_VARIANT_SANITY ||
                  variant == DA_VARIANT_PURE_PHASE1,
-             "da_hybrid_prefill: unknown variant %d", variant);
-  DA_REQUIRE(k_packed && v_packed && timestamps && counts, "da_hybrid_prefill: null packed tensor");
-  DA_REQUIRE(counts_dtype == DA_I32 || counts_dtype == DA_F32, "da_hybrid_prefill: counts must be int32 or fp32");
-  DA_REQUIRE(num_packed > 0 && num_packed <= 4096 * kBlock, "da_hybrid_prefill: num_packed must be in [1, %d]", 4096 * kBlock);
-  DA_REQUIRE(window >= 0 && window < (1ll << 30), "da_hybrid_prefill: window must be >= 0");
-  DA_REQUIRE(aligned16(k_packed) && aligned16(v_packed), "da_hybrid_prefill: packed tensors must be 16-byte aligned");
+             "%s: unknown variant %d", who, variant);
+  DA_REQUIRE(k_packed && v_packed && timestamps && counts, "%s: null packed tensor", who);
+  DA_REQUIRE(counts_dtype == DA_I32 || counts_dtype == DA_F32, "%s: counts must be int32 or fp32", who);
+  DA_REQUIRE(P_bound > 0 && P_bound <= 4096 * kBlock, "%s: num_packed must be in [1, %d]", who, 4096 * kBlock);
+  DA_REQUIRE(window >= 0 && window < (1ll << 30), "%s: window must be >= 0", who);
+  DA_REQUIRE(aligned16(k_packed) && aligned16(v_packed), "%s: packed tensors must be 16-byte aligned", who);
   for (int i : {DA_STRIDE_KP + 2, DA_STRIDE_VP + 2})
-    DA_REQUIRE(strides[i] >= D && strides[i] < (1ll << 24),
-               "da_hybrid_prefill: packed sequence strides must be in [head_dim, 2^24) (stride %d = %lld)", i, (long long)strides[i]);
+    DA_REQUIRE(strides[i] >= a.D && strides[i] < (1ll << 24),
+               "%s: packed sequence strides must be in [head_dim, 2^24) (stride %d = %lld)", who, i,
+               (long long)strides[i]);
   DA_REQUIRE(strides[DA_STRIDE_TS + 2] == 1 && strides[DA_STRIDE_CNT + 2] == 1,
-             "da_hybrid_prefill: timestamps and counts must be contiguous along the packed axis");
-  if (!workspace || workspace_bytes < da_hybrid_workspace_size(B, Hkv, num_packed))
-    return set_error(DA_ERR_WORKSPACE, "da_hybrid_prefill: workspace of %lld bytes required",
-                     (long long)da_hybrid_workspace_size(B, Hkv, num_packed));
+             "%s: timestamps and counts must be contiguous along the packed axis", who);
+  const int64_t need = da_hybrid_workspace_size(B, Hkv, P_bound);
+  if (!workspace || workspace_bytes < need)
+    return set_error(DA_ERR_WORKSPACE, "%s: workspace of %lld bytes required", who, (long long)need);
   a.kp = (const uint16_t*)k_packed; a.vp = (const uint16_t*)v_packed;
   a.ts = timestamps; a.cnt = counts;
   a.skp_b = strides[DA_STRIDE_KP]; a.skp_h = strides[DA_STRIDE_KP + 1]; a.skp_n = strides[DA_STRIDE_KP + 2];
   a.svp_b = strides[DA_STRIDE_VP]; a.svp_h = strides[DA_STRIDE_VP + 1]; a.svp_n = strides[DA_STRIDE_VP + 2];
   a.sts_b = strides[DA_STRIDE_TS]; a.sts_h = strides[DA_STRIDE_TS + 1];
   a.scnt_b = strides[DA_STRIDE_CNT]; a.scnt_h = strides[DA_STRIDE_CNT + 1];
-  a.P_host = (int)num_packed;
+  a.P_host = (int)P_bound;
   a.P_dev = num_packed_dev;
   a.window = (int)window;
   a.no_count = no_count ? 1 : 0;
   a.cnt_is_float = counts_dtype == DA_F32;
   a.causal = 1;
-  const HybridWs wl = hybrid_ws(B, Hkv, num_packed);
+  const HybridWs wl = hybrid_ws(B, Hkv, P_bound);
   char* ws = (char*)workspace;
   a.nblk_cap = wl.nblk;
   a.sched = (const int32_t*)ws;
@@ -1248,7 +1292,6 @@ extern "C" int da_hybrid_prefill(const void* q, const void* k, const void* v, co
   a.wts = (const float*)(ws + wl.w_off);
   a.tsw = (const int32_t*)(ws + wl.ts_off);
   a.zeros = (const float*)(ws + wl.zeros_off);
-  hipStream_t st = (hipStream_t)stream;
   SchedPrep prep = {};
   if (variant != DA_VARIANT_SANITY) {
     prep.cnt = counts;
@@ -1264,13 +1307,30 @@ extern "C" int da_hybrid_prefill(const void* q, const void* k, const void* v, co
   }
   const unsigned prep_chunks = prep.wts ? (unsigned)((wl.wcap + 1023) / 1024) : 0u;
   hipLaunchKernelGGL(hybrid_schedule_kernel, dim3((unsigned)(B * Hkv), 1 + prep_chunks), dim3(256), 0, st,
-                     timestamps,
-                     a.sts_b, a.sts_h, (int)Hkv, (int)num_packed, num_packed_dev, (int)Nk, a.nblk_cap,
-                     (int32_t*)ws, prep);
-  rc = check_launch("da_hybrid_prefill(schedule)");
-  if (rc) return rc;
+                     timestamps, a.sts_b, a.sts_h, (int)Hkv, (int)P_bound, num_packed_dev, (int)Nk, a.seq,
+                     a.nblk_cap, (int32_t*)ws, prep);
+  if (int rc = check_launch("hybrid prefill (schedule)")) return rc;
   const int kv = variant == DA_VARIANT_HYBRID ? kHybrid : (variant == DA_VARIANT_SANITY ? kSanity : kPure);
   return launch_attn(kv, dtype, a, st);
+}
+
+extern "C" int da_hybrid_prefill(const void* q, const void* k, const void* v, const void* k_packed,
+                                 const void* v_packed, const int32_t* timestamps,
+                                 const void* counts, int counts_dtype, void* out, int dtype,
+                                 int64_t B, int64_t Hq, int64_t Hkv, int64_t Nq, int64_t Nk,
+                                 int64_t D, const int64_t* strides, int64_t num_packed,
+                                 const int32_t* num_packed_dev, int64_t window, float scale,
+                                 int variant, int no_count, void* workspace,
+                                 int64_t workspace_bytes, void* stream) {
+  const char* who = "da_hybrid_prefill";
+  if (dtype != DA_BF16 && dtype != DA_F16)
+    return set_error(DA_ERR_UNSUPPORTED, "%s: tensors must be bf16 or fp16", who);
+  AttnArgs a = {};
+  if (int rc = fill_common(a, q, k, v, out, B, Hq, Hkv, Nq, Nk, D, strides, scale, who)) return rc;
+  a.seq = SeqMap{nullptr, 0, (int)Nq};
+  return hybrid_impl(who, a, k_packed, v_packed, timestamps, counts, counts_dtype, dtype, B, Hkv, Nk, strides,
+                     num_packed, num_packed_dev, window, variant, no_count, workspace, workspace_bytes,
+                     (hipStream_t)stream);
 }
 
 extern "C" int da_dense_prefill(const void* q, const void* k, const void* v, void* out, int dtype,
@@ -1282,6 +1342,57 @@ extern "C" int da_dense_prefill(const void* q, const void* k, const void* v, voi
   AttnArgs a = {};
   int rc = fill_common(a, q, k, v, out, B, Hq, Hkv, Nq, Nk, D, strides, scale, "da_dense_prefill");
   if (rc) return rc;
+  a.seq = SeqMap{nullptr, 0, (int)Nq};
+  a.kp = a.k; a.vp = a.v;
+  a.causal = causal ? 1 : 0;
+  a.P_host = 0;
+  return launch_attn(kDense, dtype, a, (hipStream_t)stream);
+}
+
+// ---- ragged (varlen) batches: sequence b is tokens cu_seqlens[b] .. cu_seqlens[b+1]-1 of
+// [T, H, D] tensors; every sequence is exactly a B = 1 prefill of its own length ----
+static int varlen_common(const char* who, AttnArgs& a, const void* q, const void* k, const void* v, void* out,
+                         int dtype, int64_t B, int64_t Hq, int64_t Hkv, int64_t T, int64_t D,
+                         const int64_t* strides, const int32_t* cu_seqlens, int64_t max_seqlen, float scale) {
+  if (dtype != DA_BF16 && dtype != DA_F16)
+    return set_error(DA_ERR_UNSUPPORTED, "%s: tensors must be bf16 or fp16", who);
+  DA_REQUIRE(cu_seqlens, "%s: null cu_seqlens", who);
+  DA_REQUIRE(T > 0 && max_seqlen > 0 && max_seqlen <= T, "%s: need 0 < max_seqlen <= total tokens", who);
+  DA_REQUIRE(T < (1ll << 31), "%s: too many tokens", who);
+  if (int rc = fill_common(a, q, k, v, out, B, Hq, Hkv, max_seqlen, max_seqlen, D, strides, scale, who)) return rc;
+  a.seq = SeqMap{cu_seqlens, (int)T, (int)max_seqlen};
+  return DA_OK;
+}
+
+extern "C" int64_t da_hybrid_varlen_workspace_size(int64_t B, int64_t Hkv, int64_t max_seqlen) {
+  return da_hybrid_workspace_size(B, Hkv, max_seqlen);
+}
+
+extern "C" int da_hybrid_prefill_varlen(const void* q, const void* k, const void* v, const void* k_packed,
+                                        const void* v_packed, const int32_t* timestamps, const void* counts,
+                                        int counts_dtype, void* out, int dtype, int64_t B, int64_t Hq,
+                                        int64_t Hkv, int64_t T, int64_t D, const int64_t* strides,
+                                        const int32_t* cu_seqlens, int64_t max_seqlen,
+                                        const int32_t* num_packed, int64_t window, float scale, int variant,
+                                        int no_count, void* workspace, int64_t workspace_bytes, void* stream) {
+  const char* who = "da_hybrid_prefill_varlen";
+  AttnArgs a = {};
+  if (int rc = varlen_common(who, a, q, k, v, out, dtype, B, Hq, Hkv, T, D, strides, cu_seqlens, max_seqlen, scale))
+    return rc;
+  DA_REQUIRE(num_packed, "%s: null num_packed", who);
+  return hybrid_impl(who, a, k_packed, v_packed, timestamps, counts, counts_dtype, dtype, B, Hkv, max_seqlen,
+                     strides, max_seqlen, num_packed, window, variant, no_count, workspace, workspace_bytes,
+                     (hipStream_t)stream);
+}
+
+extern "C" int da_dense_prefill_varlen(const void* q, const void* k, const void* v, void* out, int dtype,
+                                       int64_t B, int64_t Hq, int64_t Hkv, int64_t T, int64_t D,
+                                       const int64_t* strides, const int32_t* cu_seqlens, int64_t max_seqlen,
+                                       int causal, float scale, void* stream) {
+  AttnArgs a = {};
+  if (int rc = varlen_common("da_dense_prefill_varlen", a, q, k, v, out, dtype, B, Hq, Hkv, T, D, strides,
+                             cu_seqlens, max_seqlen, scale))
+    return rc;
   a.kp = a.k; a.vp = a.v;
   a.causal = causal ? 1 : 0;
   a.P_host = 0;

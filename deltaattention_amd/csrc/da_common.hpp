@@ -83,6 +83,35 @@ struct E16<DA_F16> {
 };
 
 // ------------------------------------------------------------------------------------
+// batch layouts (device): a fixed-length batch puts sequence b at b * stride_b; a packed
+// ragged batch (cu_seqlens, the varlen entry points) puts it at tokens cu[b] ..
+// cu[b + 1] - 1, i.e. at cu[b] * stride_n.  Offsets and lengths read from cu are
+// clamped into [0, total] and to max_len, so malformed cu_seqlens cannot address memory
+// outside the tensors.
+// ------------------------------------------------------------------------------------
+struct SeqMap {
+  const int32_t* cu;  // null: fixed-length batch
+  int total;          // tokens in the packed batch (varlen) / unused
+  int max_len;        // the longest sequence (varlen) / the fixed length
+  __device__ __forceinline__ int start(int b) const {
+    if (!cu) return 0;
+    const int s = cu[b];
+    return s < 0 ? 0 : (s > total ? total : s);
+  }
+  __device__ __forceinline__ int len(int b) const {
+    if (!cu) return max_len;
+    const int s = start(b);
+    int e = cu[b + 1];
+    e = e < s ? s : (e > total ? total : e);
+    return e - s > max_len ? max_len : e - s;
+  }
+  // element offset of row 0 of sequence b in a tensor with strides (s_b, s_n)
+  __device__ __forceinline__ int64_t base(int b, int64_t s_b, int64_t s_n) const {
+    return cu ? (int64_t)start(b) * s_n : (int64_t)b * s_b;
+  }
+};
+
+// ------------------------------------------------------------------------------------
 // wave-level data movement (device)
 // ------------------------------------------------------------------------------------
 template <int CTRL>

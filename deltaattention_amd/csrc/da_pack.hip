@@ -19,6 +19,11 @@
 // workgroup zero-fills its share of the padding rows [c, P) of its head, so the
 // packed tensors equal the reference's zero-initialised ones.  P = max_g c_g is
 // computed on the device and written to num_packed.
+//
+// Both kernels also take a ragged batch (SeqMap with cu_seqlens): sequence b is then
+// packed exactly as a B = 1 batch of its own length -- its own anchors, counts and
+// P_b = max over its heads, written to num_packed[b] -- into rows [0, P_b) of its
+// slice of the token-major outputs.
 #include "da_common.hpp"
 
 namespace da {
@@ -53,8 +58,11 @@ constexpr int kScanThreads = 1024;
 constexpr int kScanWaves = kScanThreads / 64;
 constexpr int kScanUnroll = 32;  // groups per wave per pass: that many loads in flight
 
+// keep: [B, H, N] (fixed batch) or [H, T] with row h * keep_sh (ragged batch); the
+// workspace rows hold ngroups_cap groups per (batch, head).
 __global__ __launch_bounds__(kScanThreads) void pack_scan_kernel(const int32_t* __restrict__ keep,
-                                                                 int64_t N, int ngroups,
+                                                                 int64_t N_fixed, int ngroups_cap,
+                                                                 int H, SeqMap seq, int64_t keep_sh,
                                                                  int32_t* __restrict__ ws_off,
                                                                  int32_t* __restrict__ ws_next,
                                                                  int32_t* __restrict__ anchor_counts) {
@@ -63,7 +71,10 @@ __global__ __launch_bounds__(kScanThreads) void pack_scan_kernel(const int32_t* 
   __shared__ int32_t s_suffix[kScanThreads];
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int64_t bh = blockIdx.x;
-  const int32_t* krow = keep + bh * N;
+  const int b = (int)(bh / H), h = (int)(bh - (bh / H) * H);
+  const int64_t N = seq.cu ? seq.len(b) : N_fixed;
+  const int ngroups = (int)((N + 63) / 64);
+  const int32_t* krow = seq.cu ? keep + (int64_t)h * keep_sh + seq.start(b) : keep + bh * N_fixed;
 
   // wave w takes groups 32w .. 32w + 31 of every 32 * kScanWaves.  Rows past the end
   // are clamped to row N - 1 and masked afterwards, so the 32 loads issue without
@@ -124,8 +135,8 @@ __global__ __launch_bounds__(kScanThreads) void pack_scan_kernel(const int32_t* 
   __syncthreads();
   int nxt = (tid < kScanThreads - 1) ? s_suffix[tid + 1] : (int)N;
 
-  int32_t* off_row = ws_off + bh * ngroups;
-  int32_t* next_row = ws_next + bh * ngroups;
+  int32_t* off_row = ws_off + bh * ngroups_cap;
+  int32_t* next_row = ws_next + bh * ngroups_cap;
   for (int g = g0; g < g1; ++g) {
     off_row[g] = run;
     run += s_info[g] & 0xff;
@@ -138,47 +149,74 @@ __global__ __launch_bounds__(kScanThreads) void pack_scan_kernel(const int32_t* 
   if (tid == 0) anchor_counts[bh] = total;
 }
 
+// Packed outputs: K-hat / V-hat row j of (b, h) at kp + base(b) + h * sp_h + j * sp_n, its
+// timestamp and count at ts / cnt + base_c(b) + h * sc_h + j.  A fixed batch uses
+// contiguous [B, H, capacity, D] / [B, H, capacity] tensors; a ragged batch token-major
+// [T, H, D] / head-major [H, T] ones, with capacity N_b for sequence b.
+struct PackOut {
+  uint16_t* kp;
+  uint16_t* vp;
+  int32_t* ts;
+  int32_t* cnt;
+  int64_t sp_b, sp_h, sp_n;
+  int64_t sc_b, sc_h;
+  int64_t capacity;  // fixed batch
+};
+
 __global__ __launch_bounds__(256) void pack_scatter_kernel(
     const int32_t* __restrict__ keep, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, int64_t sk_b, int64_t sk_h, int64_t sk_n, int64_t sv_b,
-    int64_t sv_h, int64_t sv_n, int Hkv, int64_t N, int D, int ngroups, int BH,
-    int64_t capacity, const int32_t* __restrict__ ws_off, const int32_t* __restrict__ ws_next,
-    const int32_t* __restrict__ anchor_counts, uint16_t* __restrict__ kp,
-    uint16_t* __restrict__ vp, int32_t* __restrict__ ts, int32_t* __restrict__ cnt,
+    int64_t sv_h, int64_t sv_n, int Hkv, int64_t N_fixed, int D, int ngroups_cap, int BH,
+    SeqMap seq, int64_t keep_sh, PackOut po, const int32_t* __restrict__ ws_off,
+    const int32_t* __restrict__ ws_next, const int32_t* __restrict__ anchor_counts,
     int32_t* __restrict__ num_packed) {
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int64_t bh = blockIdx.y;
   const int64_t b = bh / Hkv, h = bh - (bh / Hkv) * Hkv;
   const int g = blockIdx.x * 4 + wid;
+  const int64_t N = seq.cu ? seq.len((int)b) : N_fixed;
+  const int ngroups = (int)((N + 63) / 64);
+  const int64_t capacity = seq.cu ? N : po.capacity;
 
+  // P: over every (batch, head) of a fixed batch (modeling_llama.py:656), over the heads
+  // of this sequence for a ragged one
   int P = 0;
-  for (int i = lane; i < BH; i += 64) P = max(P, anchor_counts[i]);
+  if (seq.cu) {
+    for (int i = lane; i < Hkv; i += 64) P = max(P, anchor_counts[b * Hkv + i]);
+  } else {
+    for (int i = lane; i < BH; i += 64) P = max(P, anchor_counts[i]);
+  }
   P = wave_reduce_max(P);
   const int c = anchor_counts[bh];
-  if (blockIdx.x == 0 && blockIdx.y == 0 && tid == 0) *num_packed = P;
+  if (blockIdx.x == 0 && tid == 0) {
+    if (seq.cu && h == 0) num_packed[b] = P;
+    else if (!seq.cu && bh == 0) *num_packed = P;
+  }
 
-  const int64_t prow = bh * capacity;  // first packed row of this head
+  const int64_t kp_row0 = seq.base((int)b, po.sp_b, po.sp_n) + h * po.sp_h;  // packed row 0 of this head
+  const int64_t c_row0 = seq.base((int)b, po.sc_b, 1) + h * po.sc_h;
+  const int32_t* krow = seq.cu ? keep + h * keep_sh + seq.start((int)b) : keep + bh * N_fixed;
   const int nw = D >> 1;               // 4-byte words per row
   if (g < ngroups) {
     const int64_t r = (int64_t)g * 64 + lane;
-    const bool is_anchor = r < N && keep[bh * N + r] != 0;
+    const bool is_anchor = r < N && krow[r] != 0;
     const uint64_t bits = __ballot(is_anchor);
-    const int off = ws_off[bh * ngroups + g];
+    const int off = ws_off[bh * ngroups_cap + g];
     if (is_anchor) {
       const int rank = __popcll(bits & ((1ull << lane) - 1ull));
       const uint64_t higher = (lane == 63) ? 0ull : (bits >> (lane + 1)) << (lane + 1);
-      const int next = higher ? g * 64 + __builtin_ctzll(higher) : ws_next[bh * ngroups + g];
+      const int next = higher ? g * 64 + __builtin_ctzll(higher) : ws_next[bh * ngroups_cap + g];
       const int64_t dst = off + rank;
       if (dst < capacity) {
-        ts[prow + dst] = (int32_t)r;                // tritonModules.py:131-132
-        cnt[prow + dst] = (int32_t)(next - r);      // modeling_llama.py:683-685
+        po.ts[c_row0 + dst] = (int32_t)r;                // tritonModules.py:131-132
+        po.cnt[c_row0 + dst] = (int32_t)(next - r);      // modeling_llama.py:683-685
       }
     }
     // Copy the anchor rows, sixteen rows per step so that their loads are in flight
     // together (a 64-row group holds about 64 / r anchors).
     constexpr int kRows = 16;
-    const uint16_t* kbase = k + b * sk_b + h * sk_h + 2 * lane;
-    const uint16_t* vbase = v + b * sv_b + h * sv_h + 2 * lane;
+    const uint16_t* kbase = k + seq.base((int)b, sk_b, sk_n) + h * sk_h + 2 * lane;
+    const uint16_t* vbase = v + seq.base((int)b, sv_b, sv_n) + h * sv_h + 2 * lane;
     const bool act = lane < nw;
     uint64_t rem = bits;
     int64_t dst = off;
@@ -204,8 +242,8 @@ __global__ __launch_bounds__(256) void pack_scatter_kernel(
       for (int j = 0; j < kRows; ++j) {
         const int64_t d = dst + j;
         if (act && j < nr && d < capacity) {
-          *(uint32_t*)(kp + (prow + d) * D + 2 * lane) = kw[j];
-          *(uint32_t*)(vp + (prow + d) * D + 2 * lane) = vw[j];
+          *(uint32_t*)(po.kp + kp_row0 + d * po.sp_n + 2 * lane) = kw[j];
+          *(uint32_t*)(po.vp + kp_row0 + d * po.sp_n + 2 * lane) = vw[j];
         }
       }
       dst += nr;
@@ -219,11 +257,11 @@ __global__ __launch_bounds__(256) void pack_scatter_kernel(
     const int64_t row = r0 + i / nw;
     const int wd = i % nw;
     if (row < pad_end) {
-      *(uint32_t*)(kp + (prow + row) * D + 2 * wd) = 0u;
-      *(uint32_t*)(vp + (prow + row) * D + 2 * wd) = 0u;
+      *(uint32_t*)(po.kp + kp_row0 + row * po.sp_n + 2 * wd) = 0u;
+      *(uint32_t*)(po.vp + kp_row0 + row * po.sp_n + 2 * wd) = 0u;
       if (wd == 0) {
-        ts[prow + row] = 0;
-        cnt[prow + row] = 0;
+        po.ts[c_row0 + row] = 0;
+        po.cnt[c_row0 + row] = 0;
       }
     }
   }
@@ -236,6 +274,23 @@ using namespace da;
 extern "C" int64_t da_pack_workspace_size(int64_t B, int64_t Hkv, int64_t N) {
   const int64_t ngroups = (N + 63) / 64;
   return 2 * B * Hkv * ngroups * (int64_t)sizeof(int32_t);
+}
+
+// Launch of the two kernels for a fixed batch (seq.cu null) or a ragged one.
+static int launch_pack(const char* who, const int32_t* keep, const void* k, const void* v, int64_t B, int64_t Hkv,
+                       int64_t N_fixed, int64_t D, int64_t sk_b, int64_t sk_h, int64_t sk_n, int64_t sv_b,
+                       int64_t sv_h, int64_t sv_n, int64_t ngroups, SeqMap seq, int64_t keep_sh, PackOut po,
+                       int32_t* anchor_counts, int32_t* num_packed, void* workspace, hipStream_t st) {
+  int32_t* ws_off = (int32_t*)workspace;
+  int32_t* ws_next = ws_off + B * Hkv * ngroups;
+  hipLaunchKernelGGL(pack_scan_kernel, dim3((unsigned)(B * Hkv)), dim3(kScanThreads), 0, st, keep, N_fixed,
+                     (int)ngroups, (int)Hkv, seq, keep_sh, ws_off, ws_next, anchor_counts);
+  if (int rc = check_launch(who)) return rc;
+  hipLaunchKernelGGL(pack_scatter_kernel, dim3((unsigned)((ngroups + 3) / 4), (unsigned)(B * Hkv)),
+                     dim3(256), 0, st, keep, (const uint16_t*)k, (const uint16_t*)v, sk_b, sk_h,
+                     sk_n, sv_b, sv_h, sv_n, (int)Hkv, N_fixed, (int)D, (int)ngroups, (int)(B * Hkv),
+                     seq, keep_sh, po, ws_off, ws_next, anchor_counts, num_packed);
+  return check_launch(who);
 }
 
 extern "C" int da_pack(const int32_t* keep, const void* k, const void* v, int dtype, int64_t B,
@@ -261,17 +316,42 @@ extern "C" int da_pack(const int32_t* keep, const void* k, const void* v, int dt
   if (!workspace || workspace_bytes < da_pack_workspace_size(B, Hkv, N))
     return set_error(DA_ERR_WORKSPACE, "da_pack: workspace of %lld bytes required",
                      (long long)da_pack_workspace_size(B, Hkv, N));
-  hipStream_t st = (hipStream_t)stream;
-  int32_t* ws_off = (int32_t*)workspace;
-  int32_t* ws_next = ws_off + B * Hkv * ngroups;
-  hipLaunchKernelGGL(pack_scan_kernel, dim3((unsigned)(B * Hkv)), dim3(kScanThreads), 0, st, keep, N,
-                     (int)ngroups, ws_off, ws_next, anchor_counts);
-  int rc = check_launch("da_pack(scan)");
-  if (rc) return rc;
-  hipLaunchKernelGGL(pack_scatter_kernel, dim3((unsigned)((ngroups + 3) / 4), (unsigned)(B * Hkv)),
-                     dim3(256), 0, st, keep, (const uint16_t*)k, (const uint16_t*)v, sk_b, sk_h,
-                     sk_n, sv_b, sv_h, sv_n, (int)Hkv, N, (int)D, (int)ngroups, (int)(B * Hkv),
-                     capacity, ws_off, ws_next, anchor_counts, (uint16_t*)k_packed,
-                     (uint16_t*)v_packed, timestamps, counts, num_packed);
-  return check_launch("da_pack(scatter)");
+  PackOut po = {(uint16_t*)k_packed, (uint16_t*)v_packed, timestamps, counts,
+                Hkv * capacity * D, capacity * D, D, Hkv * capacity, capacity, capacity};
+  return launch_pack("da_pack", keep, k, v, B, Hkv, N, D, sk_b, sk_h, sk_n, sv_b, sv_h, sv_n, ngroups,
+                     SeqMap{nullptr, 0, (int)N}, N, po, anchor_counts, num_packed, workspace, (hipStream_t)stream);
+}
+
+extern "C" int64_t da_pack_varlen_workspace_size(int64_t B, int64_t Hkv, int64_t max_seqlen) {
+  return da_pack_workspace_size(B, Hkv, max_seqlen);
+}
+
+extern "C" int da_pack_varlen(const int32_t* keep, const void* k, const void* v, int dtype, int64_t B,
+                              int64_t Hkv, int64_t T, int64_t D, int64_t sk_t, int64_t sk_h, int64_t sv_t,
+                              int64_t sv_h, const int32_t* cu_seqlens, int64_t max_seqlen, void* k_packed,
+                              void* v_packed, int32_t* timestamps, int32_t* counts, int32_t* anchor_counts,
+                              int32_t* num_packed, void* workspace, int64_t workspace_bytes, void* stream) {
+  const char* who = "da_pack_varlen";
+  DA_REQUIRE(keep && k && v && k_packed && v_packed && timestamps && counts && anchor_counts && num_packed &&
+                 cu_seqlens,
+             "%s: null pointer", who);
+  if (dtype != DA_BF16 && dtype != DA_F16)
+    return set_error(DA_ERR_UNSUPPORTED, "%s: K and V must be bf16 or fp16", who);
+  DA_REQUIRE(B > 0 && Hkv > 0 && T > 0 && D > 0, "%s: empty shape", who);
+  if (D > 128 || (D & 1)) return set_error(DA_ERR_UNSUPPORTED, "%s: head_dim must be even and <= 128", who);
+  DA_REQUIRE(T < (1ll << 31) && max_seqlen > 0 && max_seqlen <= T, "%s: need 0 < max_seqlen <= total tokens < 2^31", who);
+  const int64_t ngroups = (max_seqlen + 63) / 64;
+  if (ngroups > kMaxGroups) return set_error(DA_ERR_UNSUPPORTED, "%s: sequence longer than %d", who, kMaxGroups * 64);
+  DA_REQUIRE(B * Hkv < 65536, "%s: too many heads", who);
+  DA_REQUIRE(((sk_t | sk_h | sv_t | sv_h) & 1) == 0 && ((uintptr_t)k & 3) == 0 && ((uintptr_t)v & 3) == 0 &&
+                 ((uintptr_t)k_packed & 3) == 0 && ((uintptr_t)v_packed & 3) == 0,
+             "%s: rows must be 4-byte aligned", who);
+  if (!workspace || workspace_bytes < da_pack_varlen_workspace_size(B, Hkv, max_seqlen))
+    return set_error(DA_ERR_WORKSPACE, "%s: workspace of %lld bytes required", who,
+                     (long long)da_pack_varlen_workspace_size(B, Hkv, max_seqlen));
+  // outputs: K-hat / V-hat token-major [T, Hkv, D], timestamps / counts head-major [Hkv, T]
+  PackOut po = {(uint16_t*)k_packed, (uint16_t*)v_packed, timestamps, counts, 0, D, Hkv * D, 0, T, 0};
+  return launch_pack(who, keep, k, v, B, Hkv, max_seqlen, D, 0, sk_h, sk_t, 0, sv_h, sv_t, ngroups,
+                     SeqMap{cu_seqlens, (int)T, (int)max_seqlen}, T, po, anchor_counts, num_packed, workspace,
+                     (hipStream_t)stream);
 }

@@ -24,6 +24,8 @@
 // the decisions.  The distance reaches every lane through v_permlane16/32_swap (no
 // scalar round trip), the anchor update is a select, and a batch's decisions collect
 // in a 32-bit mask stored as int32 (the reference's keep-mask format).
+#include <algorithm>
+
 #include "da_common.hpp"
 
 namespace da {
@@ -80,11 +82,16 @@ __device__ __forceinline__ bool select_step(uint32_t xb, float& a0, float& a1, f
   return kp;
 }
 
+// Keys: a fixed-length batch [B, H, N, D] with the caller's chunk size cs, or (seq.cu set)
+// a ragged batch of [T, H, D] tensors where sequence b is chunked by the reference's rule
+// on its own length: min(cs, N_b) rows per chunk, or ceil(N_b / divide_to) when
+// divide_to > 0 (modeling_llama.py:602-610).  keep is [B, H, N] for a fixed batch and
+// [H, T] (row h * keep_sh + token) for a ragged one; chunk_counts is [B, H, nc].
 template <bool COS, bool A16, int DT>
 __global__ __launch_bounds__(256) void select_kernel(
     const uint16_t* __restrict__ k, int64_t sk_b, int64_t sk_h, int64_t sk_n, int H, int64_t N,
     int D, int64_t cs, int64_t nc, int64_t total_chunks, float thr, int32_t* __restrict__ keep,
-    int32_t* __restrict__ chunk_counts) {
+    int32_t* __restrict__ chunk_counts, SeqMap seq, int64_t keep_sh, int divide_to) {
 #pragma clang fp contract(off)
   const int lane = threadIdx.x & 63;
   const int64_t w = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
@@ -92,16 +99,19 @@ __global__ __launch_bounds__(256) void select_kernel(
   const int64_t bh = w / nc;
   const int64_t c = w - bh * nc;
   const int64_t b = bh / H, h = bh - (bh / H) * H;
-  if (c * cs >= N) {  // tritonModules.py:34-35 (count stays 0, modeling_llama.py:637)
+  const int64_t Nb = seq.cu ? seq.len((int)b) : N;
+  int64_t csb = cs;
+  if (seq.cu) csb = divide_to > 0 ? (Nb + divide_to - 1) / divide_to : (cs < Nb ? cs : Nb);
+  if (Nb <= 0 || c * csb >= Nb) {  // tritonModules.py:34-35 (count stays 0, modeling_llama.py:637)
     if (lane == 0) chunk_counts[w] = 0;
     return;
   }
   // rows are 32-bit from here on (N < 2^31)
-  const int s = (int)(c * cs);
-  const int e = (int)((c * cs + cs < N) ? c * cs + cs : N);
-  const uint16_t* base = k + b * sk_b + h * sk_h + 2 * lane;
+  const int s = (int)(c * csb);
+  const int e = (int)((c * csb + csb < Nb) ? c * csb + csb : Nb);
+  const uint16_t* base = k + seq.base((int)b, sk_b, sk_n) + h * sk_h + 2 * lane;
   const bool active = 2 * lane < D;
-  int32_t* keep_row = keep + bh * N;
+  int32_t* keep_row = keep + (seq.cu ? h * keep_sh + seq.start((int)b) : bh * N);
   auto row_bits = [&](int r) -> uint32_t {
     return (active && r < e) ? *(const uint32_t*)(base + (int64_t)r * sk_n) : 0u;
   };
@@ -139,6 +149,32 @@ __global__ __launch_bounds__(256) void select_kernel(
   if (lane == 0) chunk_counts[w] = count;  // tritonModules.py:68-69
 }
 
+static int launch_select(const void* k, int dtype, int64_t B, int64_t Hkv, int64_t N, int64_t D, int64_t sk_b,
+                         int64_t sk_h, int64_t sk_n, float threshold, bool use_cosine, bool a16, int64_t chunk_size,
+                         int64_t num_chunks, int32_t* keep, int32_t* chunk_counts, SeqMap seq, int64_t keep_sh,
+                         int divide_to, hipStream_t st, const char* who) {
+  DA_REQUIRE(((sk_b | sk_h | sk_n) & 1) == 0 && ((uintptr_t)k & 3) == 0,
+             "%s: key rows must be 4-byte aligned (even strides)", who);
+  const int64_t total = B * Hkv * num_chunks;
+  const int64_t blocks = (total + 3) / 4;
+  DA_REQUIRE(blocks < (1ll << 31), "%s: too many chunks", who);
+#define DA_SELECT_LAUNCH(COS, A16, DT)                                                                       \
+  hipLaunchKernelGGL((select_kernel<COS, A16, DT>), dim3((unsigned)blocks), dim3(256), 0, st, (const uint16_t*)k, \
+                     sk_b, sk_h, sk_n, (int)Hkv, N, (int)D, chunk_size, num_chunks, total, threshold, keep,  \
+                     chunk_counts, seq, keep_sh, divide_to)
+  if (dtype == DA_F16) {
+    if (use_cosine) DA_SELECT_LAUNCH(true, false, DA_F16);
+    else if (a16) DA_SELECT_LAUNCH(false, true, DA_F16);
+    else DA_SELECT_LAUNCH(false, false, DA_F16);
+  } else {
+    if (use_cosine) DA_SELECT_LAUNCH(true, false, DA_BF16);
+    else if (a16) DA_SELECT_LAUNCH(false, true, DA_BF16);
+    else DA_SELECT_LAUNCH(false, false, DA_BF16);
+  }
+#undef DA_SELECT_LAUNCH
+  return check_launch(who);
+}
+
 }  // namespace da
 
 using namespace da;
@@ -159,23 +195,32 @@ extern "C" int da_select(const void* k, int dtype, int64_t B, int64_t Hkv, int64
   DA_REQUIRE(N < (1ll << 31), "da_select: sequence too long");
   DA_REQUIRE(((sk_b | sk_h | sk_n) & 1) == 0 && ((uintptr_t)k & 3) == 0,
              "da_select: key rows must be 4-byte aligned (even strides)");
-  const int64_t total = B * Hkv * num_chunks;
-  const int64_t blocks = (total + 3) / 4;
-  DA_REQUIRE(blocks < (1ll << 31), "da_select: too many chunks");
-  hipStream_t st = (hipStream_t)stream;
-#define DA_SELECT_LAUNCH(COS, A16, DT)                                                                       \
-  hipLaunchKernelGGL((select_kernel<COS, A16, DT>), dim3((unsigned)blocks), dim3(256), 0, st, (const uint16_t*)k, \
-                     sk_b, sk_h, sk_n, (int)Hkv, N, (int)D, chunk_size, num_chunks, total, threshold, keep,  \
-                     chunk_counts)
-  if (dtype == DA_F16) {
-    if (use_cosine) DA_SELECT_LAUNCH(true, false, DA_F16);
-    else if (a16) DA_SELECT_LAUNCH(false, true, DA_F16);
-    else DA_SELECT_LAUNCH(false, false, DA_F16);
-  } else {
-    if (use_cosine) DA_SELECT_LAUNCH(true, false, DA_BF16);
-    else if (a16) DA_SELECT_LAUNCH(false, true, DA_BF16);
-    else DA_SELECT_LAUNCH(false, false, DA_BF16);
-  }
-#undef DA_SELECT_LAUNCH
-  return check_launch("da_select");
+  return launch_select(k, dtype, B, Hkv, N, D, sk_b, sk_h, sk_n, threshold, use_cosine, a16, chunk_size,
+                       num_chunks, keep, chunk_counts, SeqMap{nullptr, 0, (int)N}, N, 0, (hipStream_t)stream,
+                       "da_select");
+}
+
+extern "C" int da_select_varlen(const void* k, int dtype, int64_t B, int64_t Hkv, int64_t T, int64_t D,
+                                int64_t sk_t, int64_t sk_h, const int32_t* cu_seqlens, int64_t max_seqlen,
+                                float threshold, int flags, int64_t chunk_size, int64_t divide_to,
+                                int32_t* keep, int32_t* chunk_counts, int64_t max_chunks, void* stream) {
+  const char* who = "da_select_varlen";
+  DA_REQUIRE(k && keep && chunk_counts && cu_seqlens, "%s: null pointer", who);
+  DA_REQUIRE((flags & ~(DA_SELECT_COSINE | DA_SELECT_ARITH16)) == 0, "%s: unknown flags 0x%x", who, flags);
+  const bool use_cosine = flags & DA_SELECT_COSINE;
+  const bool a16 = !use_cosine && (flags & DA_SELECT_ARITH16);
+  if (dtype != DA_BF16 && dtype != DA_F16)
+    return set_error(DA_ERR_UNSUPPORTED, "%s: keys must be bf16 or fp16", who);
+  DA_REQUIRE(B > 0 && Hkv > 0 && T > 0 && D > 0, "%s: empty shape", who);
+  if (D > 128 || (D & 1)) return set_error(DA_ERR_UNSUPPORTED, "%s: head_dim must be even and <= 128 (got %lld)", who, (long long)D);
+  DA_REQUIRE(T < (1ll << 31) && max_seqlen > 0 && max_seqlen <= T, "%s: need 0 < max_seqlen <= total tokens < 2^31", who);
+  DA_REQUIRE(divide_to >= 0, "%s: divide_to must be >= 0", who);
+  // the chunking rule of modeling_llama.py:602-610, per sequence
+  const int64_t cs = chunk_size > 0 ? chunk_size : 0;
+  const int div = chunk_size > 0 ? 0 : (divide_to > 0 ? (int)divide_to : 1);
+  const int64_t need = chunk_size > 0 ? std::max<int64_t>(1, (max_seqlen + chunk_size - 1) / chunk_size) : div;
+  DA_REQUIRE(max_chunks >= need, "%s: max_chunks must be at least %lld", who, (long long)need);
+  return launch_select(k, dtype, B, Hkv, max_seqlen, D, 0, sk_h, sk_t, threshold, use_cosine, a16, cs, max_chunks,
+                       keep, chunk_counts, SeqMap{cu_seqlens, (int)T, (int)max_seqlen}, T, div,
+                       (hipStream_t)stream, who);
 }

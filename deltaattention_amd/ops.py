@@ -20,7 +20,8 @@ from . import _native
 from ._native import DA_F32, DA_I32, DA_VARIANT, check, dtype_code, lib, strides_array
 
 __all__ = ["PackedKV", "chunking", "select", "pack", "hybrid_prefill", "dense_prefill",
-           "delta_prefill"]
+           "delta_prefill", "VarlenBatch", "varlen_batch", "PackedVarlen", "select_varlen",
+           "pack_varlen", "hybrid_prefill_varlen", "delta_prefill_varlen", "dense_prefill_varlen"]
 
 
 def _stream() -> ctypes.c_void_p:
@@ -275,44 +276,199 @@ def _seq_bounds(cu_seqlens, total: int):
     return list(zip(cu[:-1], cu[1:]))
 
 
-def _bhnd(x: torch.Tensor, s: int, e: int) -> torch.Tensor:
-    """[1, H, n, D] view of tokens s..e-1 of a [T, H, D] tensor (no copy)."""
-    return x[s:e].permute(1, 0, 2).unsqueeze(0)
+@dataclass
+class VarlenBatch:
+    """A ragged batch: cu_seqlens on the device (int32 [B + 1]), B and the longest length."""
+    cu: torch.Tensor
+    batch: int
+    max_seqlen: int
+
+
+def varlen_batch(cu_seqlens, total: int, device, max_seqlen: Optional[int] = None) -> VarlenBatch:
+    """cu_seqlens (host list / tensor, or a device int32 tensor) -> VarlenBatch.  Host values
+    are validated (rising from 0 to ``total``); for a device tensor without ``max_seqlen``
+    the lengths are read back once (one synchronisation)."""
+    if isinstance(cu_seqlens, VarlenBatch):
+        return cu_seqlens
+    if isinstance(cu_seqlens, torch.Tensor) and cu_seqlens.device.type == "cuda":
+        cu = cu_seqlens if cu_seqlens.dtype == torch.int32 else cu_seqlens.to(torch.int32)
+        cu = cu.contiguous()
+        if max_seqlen is None:
+            bounds = _seq_bounds(cu, total)
+            max_seqlen = max(e - s for s, e in bounds)
+        return VarlenBatch(cu, cu.numel() - 1, int(max_seqlen))
+    bounds = _seq_bounds(cu_seqlens, total)
+    host = [0] + [e for _, e in bounds]
+    return VarlenBatch(torch.tensor(host, dtype=torch.int32, device=device), len(bounds),
+                       max(1, max(e - s for s, e in bounds)))
+
+
+def _check_varlen(q, k, v):
+    if q.dim() != 3 or k.dim() != 3 or v.dim() != 3:
+        raise ValueError("varlen tensors are [tokens, heads, head_dim]")
+    if q.shape[0] != k.shape[0] or k.shape != v.shape:
+        raise ValueError("q, k and v must hold the same tokens; k and v the same heads")
+
+
+def select_varlen(k: torch.Tensor, cu_seqlens, threshold: float, chunk_size: int = 512,
+                  divide_to: int = 0, metric: str = "euclidean", arith: str = "fp32",
+                  max_seqlen: Optional[int] = None) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Delta-mode selection of every sequence of a ragged batch in one launch: k [T, Hkv, D]
+    -> keep [Hkv, T] int32, chunk counts [B, Hkv, max_chunks] int32.  Each sequence is
+    chunked by the reference's rule on its own length (modeling_llama.py:602-610)."""
+    _require_device(k)
+    dt = _require_half(k)
+    k = _last_dim_contig(k)
+    T, H, D = k.shape
+    vb = varlen_batch(cu_seqlens, T, k.device, max_seqlen)
+    nc = max(1, -(-vb.max_seqlen // chunk_size)) if chunk_size > 0 else max(1, divide_to)
+    use_cos = metric == "cosine"
+    thr = float(threshold) if use_cos else float(threshold) ** 2
+    keep = torch.zeros((H, T), dtype=torch.int32, device=k.device)
+    counts = torch.empty((vb.batch, H, nc), dtype=torch.int32, device=k.device)
+    rc = lib().da_select_varlen(k.data_ptr(), dt, vb.batch, H, T, D, k.stride(0), k.stride(1),
+                                vb.cu.data_ptr(), vb.max_seqlen, ctypes.c_float(thr),
+                                _select_flags(metric, arith), chunk_size, divide_to,
+                                keep.data_ptr(), counts.data_ptr(), nc, _stream())
+    check(rc, "da_select_varlen")
+    return keep, counts
+
+
+@dataclass
+class PackedVarlen:
+    """Packed anchors of a ragged batch: k_packed / v_packed [T, Hkv, D] (row j of sequence b
+    at token cu[b] + j), timestamps / counts [Hkv, T] likewise, anchor_counts [B, Hkv] and
+    num_packed [B] (P_b) on the device; rows [c_bg, P_b) are zero, rows beyond undefined."""
+    k_packed: torch.Tensor
+    v_packed: torch.Tensor
+    timestamps: torch.Tensor
+    counts: torch.Tensor
+    anchor_counts: torch.Tensor
+    num_packed: torch.Tensor
+
+
+def pack_varlen(keep: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqlens,
+                max_seqlen: Optional[int] = None) -> PackedVarlen:
+    """Index + pack + counts of every sequence of a ragged batch in one pass
+    (modeling_llama.py:655-685 per sequence)."""
+    _require_device(keep, k, v)
+    dt = _require_half(k, v)
+    k, v = _last_dim_contig(k), _last_dim_contig(v)
+    T, H, D = k.shape
+    vb = varlen_batch(cu_seqlens, T, k.device, max_seqlen)
+    keep = keep.contiguous()
+    if keep.shape != (H, T) or keep.dtype != torch.int32:
+        raise ValueError("keep must be an int32 [Hkv, T] tensor (as select_varlen returns it)")
+    dev = k.device
+    out = PackedVarlen(torch.empty((T, H, D), dtype=k.dtype, device=dev),
+                       torch.empty((T, H, D), dtype=v.dtype, device=dev),
+                       torch.empty((H, T), dtype=torch.int32, device=dev),
+                       torch.empty((H, T), dtype=torch.int32, device=dev),
+                       torch.empty((vb.batch, H), dtype=torch.int32, device=dev),
+                       torch.empty((vb.batch,), dtype=torch.int32, device=dev))
+    ws_bytes = lib().da_pack_varlen_workspace_size(vb.batch, H, vb.max_seqlen)
+    ws = torch.empty((max(1, ws_bytes),), dtype=torch.uint8, device=dev)
+    rc = lib().da_pack_varlen(keep.data_ptr(), k.data_ptr(), v.data_ptr(), dt, vb.batch, H, T, D,
+                              k.stride(0), k.stride(1), v.stride(0), v.stride(1), vb.cu.data_ptr(),
+                              vb.max_seqlen, out.k_packed.data_ptr(), out.v_packed.data_ptr(),
+                              out.timestamps.data_ptr(), out.counts.data_ptr(),
+                              out.anchor_counts.data_ptr(), out.num_packed.data_ptr(), ws.data_ptr(),
+                              ws_bytes, _stream())
+    check(rc, "da_pack_varlen")
+    return out
+
+
+def _varlen_strides(q, k, v, out, kp=None, vp=None, ts=None, cnt=None):
+    """The 24-entry stride array with (0, head, token) per token-major tensor and
+    (0, head, 1) for the head-major timestamps / counts."""
+    vals = [0] * 24
+    for base, t in ((0, q), (3, k), (6, v), (9, kp), (12, vp), (15, out)):
+        if t is not None:
+            vals[base:base + 3] = [0, t.stride(1), t.stride(0)]
+    for base, t in ((18, ts), (21, cnt)):
+        if t is not None:
+            vals[base:base + 3] = [0, t.stride(0), t.stride(1)]
+    return strides_array(vals)
+
+
+def hybrid_prefill_varlen(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, packed: PackedVarlen,
+                          cu_seqlens, window: int = 128, scale: Optional[float] = None,
+                          variant: str = "hybrid", no_count: bool = False,
+                          max_seqlen: Optional[int] = None,
+                          out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Two-phase compressed prefill of a ragged batch in one launch: every sequence gets
+    the schedule and result of a B = 1 hybrid prefill of its own length."""
+    if variant not in DA_VARIANT:
+        raise ValueError(f"variant must be one of {sorted(DA_VARIANT)}")
+    _check_varlen(q, k, v)
+    _require_device(q, k, v, packed.k_packed)
+    dt = _require_half(q, k, v, packed.k_packed, packed.v_packed)
+    q, k, v = _last_dim_contig(q), _last_dim_contig(k), _last_dim_contig(v)
+    T, Hq, D = q.shape
+    Hkv = k.shape[1]
+    vb = varlen_batch(cu_seqlens, T, q.device, max_seqlen)
+    if scale is None:
+        scale = D ** -0.5
+    if out is None:
+        out = torch.empty_like(q)
+    dtype_code(q, out)
+    ws_bytes = lib().da_hybrid_varlen_workspace_size(vb.batch, Hkv, vb.max_seqlen)
+    ws = torch.empty((max(1, ws_bytes),), dtype=torch.uint8, device=q.device)
+    st = _varlen_strides(q, k, v, out, packed.k_packed, packed.v_packed, packed.timestamps,
+                         packed.counts)
+    rc = lib().da_hybrid_prefill_varlen(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), packed.k_packed.data_ptr(),
+        packed.v_packed.data_ptr(), packed.timestamps.data_ptr(), packed.counts.data_ptr(),
+        DA_F32 if packed.counts.dtype == torch.float32 else DA_I32, out.data_ptr(), dt,
+        vb.batch, Hq, Hkv, T, D, st, vb.cu.data_ptr(), vb.max_seqlen,
+        packed.num_packed.data_ptr(), int(window), ctypes.c_float(scale), DA_VARIANT[variant],
+        1 if no_count else 0, ws.data_ptr(), ws_bytes, _stream())
+    check(rc, "da_hybrid_prefill_varlen")
+    return out
 
 
 def delta_prefill_varlen(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqlens,
                          threshold: float, chunk_size: int = 512, divide_to: int = 0,
                          metric: str = "euclidean", window: int = 128,
                          scale: Optional[float] = None, variant: str = "hybrid",
-                         no_count: bool = False) -> torch.Tensor:
+                         no_count: bool = False, arith: str = "fp32",
+                         max_seqlen: Optional[int] = None, return_packed: bool = False):
     """Delta prefill of a packed ragged batch: q [T, Hq, D], k, v [T, Hkv, D] with the
-    sequences at cu_seqlens (host values, length B + 1) -> out [T, Hq, D].
+    sequences at cu_seqlens -> out [T, Hq, D].
 
-    The reference has no varlen API; each sequence is exactly a B = 1 delta prefill
-    with its own chunking, anchors, P and schedule.  The sequences go through the same
-    kernels on the stream one after another, reading and writing the packed tensors in
-    place through strided views.
-    """
-    if q.dim() != 3 or k.dim() != 3 or v.dim() != 3:
-        raise ValueError("varlen tensors are [tokens, heads, head_dim]")
-    out = torch.empty_like(q)
-    for s, e in _seq_bounds(cu_seqlens, q.shape[0]):
-        if e == s:
-            continue
-        delta_prefill(_bhnd(q, s, e), _bhnd(k, s, e), _bhnd(v, s, e), threshold, chunk_size,
-                      divide_to, metric, window, scale, variant, no_count, out=_bhnd(out, s, e))
-    return out
+    The reference has no varlen API; each sequence is exactly a B = 1 delta prefill with
+    its own chunking, anchors, P and schedule.  Three launches cover the whole batch
+    (select, pack, hybrid prefill; plus the schedule pre-pass), with every per-sequence
+    quantity on the device."""
+    _check_varlen(q, k, v)
+    vb = varlen_batch(cu_seqlens, q.shape[0], q.device, max_seqlen)
+    keep, _ = select_varlen(k, vb, threshold, chunk_size, divide_to, metric, arith)
+    packed = pack_varlen(keep, k, v, vb)
+    out = hybrid_prefill_varlen(q, k, v, packed, vb, window, scale, variant, no_count)
+    return (out, packed) if return_packed else out
 
 
 def dense_prefill_varlen(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqlens,
-                         causal: bool = True, scale: Optional[float] = None) -> torch.Tensor:
-    """Dense flash prefill of a packed ragged batch (the control of delta_prefill_varlen)."""
-    if q.dim() != 3 or k.dim() != 3 or v.dim() != 3:
-        raise ValueError("varlen tensors are [tokens, heads, head_dim]")
-    out = torch.empty_like(q)
-    for s, e in _seq_bounds(cu_seqlens, q.shape[0]):
-        if e == s:
-            continue
-        dense_prefill(_bhnd(q, s, e), _bhnd(k, s, e), _bhnd(v, s, e), causal, scale,
-                      out=_bhnd(out, s, e))
+                         causal: bool = True, scale: Optional[float] = None,
+                         max_seqlen: Optional[int] = None,
+                         out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Dense flash prefill of a packed ragged batch in one launch (the control of
+    delta_prefill_varlen)."""
+    _check_varlen(q, k, v)
+    _require_device(q, k, v)
+    dt = _require_half(q, k, v)
+    q, k, v = _last_dim_contig(q), _last_dim_contig(k), _last_dim_contig(v)
+    T, Hq, D = q.shape
+    Hkv = k.shape[1]
+    vb = varlen_batch(cu_seqlens, T, q.device, max_seqlen)
+    if scale is None:
+        scale = D ** -0.5
+    if out is None:
+        out = torch.empty_like(q)
+    dtype_code(q, out)
+    st = _varlen_strides(q, k, v, out)
+    rc = lib().da_dense_prefill_varlen(q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), dt,
+                                       vb.batch, Hq, Hkv, T, D, st, vb.cu.data_ptr(), vb.max_seqlen,
+                                       1 if causal else 0, ctypes.c_float(scale), _stream())
+    check(rc, "da_dense_prefill_varlen")
     return out

@@ -141,6 +141,64 @@ int da_dense_prefill(const void* q, const void* k, const void* v, void* out, int
                      const int64_t* strides, int causal, float scale, void* stream);
 
 /*
+ * Ragged (varlen) batches.  The reference has no varlen API; its semantics for a batch of
+ * sequences of different lengths is "each sequence is a B = 1 prefill" (modeling_llama.py:
+ * 602-685 per sequence: own chunking, anchors, P and schedule), which these entry points
+ * compute in one launch per stage over the whole batch.  Sequence b is tokens
+ * cu_seqlens[b] .. cu_seqlens[b + 1] - 1 (cu_seqlens: device int32 [B + 1], non-decreasing
+ * from 0 to T; lengths at most max_seqlen).  Offsets and lengths read from cu_seqlens are
+ * clamped into [0, T] and to max_seqlen on the device.  Token-major tensors are [T, H, D]
+ * with strides (token, head) and a contiguous head dimension.
+ *
+ * da_select_varlen: keys k [T, Hkv, D]; keep [Hkv, T] int32 contiguous (position
+ * cu_seqlens[b] + i of row g for token i of sequence b); chunk_counts [B, Hkv, max_chunks]
+ * int32 contiguous, 0 for chunks past a sequence's end.  Chunking per sequence: chunk_size
+ * > 0 gives min(chunk_size, N_b) rows per chunk, else ceil(N_b / divide_to) (divide_to 0
+ * meaning 1); max_chunks must be at least ceil(max_seqlen / chunk_size) (chunk_size > 0)
+ * or max(1, divide_to).  threshold and flags as for da_select.
+ */
+int da_select_varlen(const void* k, int dtype, int64_t B, int64_t Hkv, int64_t T, int64_t D,
+                     int64_t sk_t, int64_t sk_h, const int32_t* cu_seqlens, int64_t max_seqlen,
+                     float threshold, int flags, int64_t chunk_size, int64_t divide_to,
+                     int32_t* keep, int32_t* chunk_counts, int64_t max_chunks, void* stream);
+
+/*
+ * da_pack_varlen: keep [Hkv, T] (as da_select_varlen writes it, keep of token 0 of every
+ * sequence must be 1); k, v [T, Hkv, D].  Outputs: k_packed, v_packed [T, Hkv, D]
+ * contiguous, packed row j of (b, g) at token cu_seqlens[b] + j; timestamps, counts
+ * [Hkv, T] int32 contiguous, likewise (timestamps are positions inside the sequence);
+ * rows [c_bg, P_b) zero-filled.  anchor_counts [B, Hkv]; num_packed [B] int32 receives
+ * P_b = max over the sequence's heads.  workspace: da_pack_varlen_workspace_size bytes.
+ */
+int64_t da_pack_varlen_workspace_size(int64_t B, int64_t Hkv, int64_t max_seqlen);
+int da_pack_varlen(const int32_t* keep, const void* k, const void* v, int dtype, int64_t B,
+                   int64_t Hkv, int64_t T, int64_t D, int64_t sk_t, int64_t sk_h, int64_t sv_t,
+                   int64_t sv_h, const int32_t* cu_seqlens, int64_t max_seqlen, void* k_packed,
+                   void* v_packed, int32_t* timestamps, int32_t* counts, int32_t* anchor_counts,
+                   int32_t* num_packed, void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * da_hybrid_prefill_varlen / da_dense_prefill_varlen: q, out [T, Hq, D]; k, v [T, Hkv, D];
+ * k_packed, v_packed, timestamps, counts as da_pack_varlen writes them (any token and head
+ * strides); num_packed: device [B] (P_b).  strides: the 24-entry array of
+ * da_hybrid_prefill with the batch entries ignored and the sequence entries holding the
+ * token strides.  Each sequence gets exactly the schedule and result of a B = 1
+ * da_hybrid_prefill / da_dense_prefill of its own length.
+ */
+int64_t da_hybrid_varlen_workspace_size(int64_t B, int64_t Hkv, int64_t max_seqlen);
+int da_hybrid_prefill_varlen(const void* q, const void* k, const void* v, const void* k_packed,
+                             const void* v_packed, const int32_t* timestamps, const void* counts,
+                             int counts_dtype, void* out, int dtype, int64_t B, int64_t Hq,
+                             int64_t Hkv, int64_t T, int64_t D, const int64_t* strides,
+                             const int32_t* cu_seqlens, int64_t max_seqlen,
+                             const int32_t* num_packed, int64_t window, float scale, int variant,
+                             int no_count, void* workspace, int64_t workspace_bytes, void* stream);
+int da_dense_prefill_varlen(const void* q, const void* k, const void* v, void* out, int dtype,
+                            int64_t B, int64_t Hq, int64_t Hkv, int64_t T, int64_t D,
+                            const int64_t* strides, const int32_t* cu_seqlens, int64_t max_seqlen,
+                            int causal, float scale, void* stream);
+
+/*
  * Decode step of the compressed cache.  Replaces fused_hybrid_decode_update_kernel
  * (deltaDecoding.py:9-104) as launched by HybridCompressedCache.update (:181-211).
  *

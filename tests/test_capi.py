@@ -23,7 +23,9 @@ def test_header_declares_the_expected_entry_points():
         "da_last_error", "da_version", "da_select", "da_pack_workspace_size", "da_pack",
         "da_hybrid_workspace_size", "da_hybrid_prefill", "da_dense_prefill",
         "da_decode_update", "da_decode_workspace_size", "da_decode_attention",
-        "da_decode_attention_noalloc"])
+        "da_decode_attention_noalloc", "da_select_varlen", "da_pack_varlen_workspace_size",
+        "da_pack_varlen", "da_hybrid_varlen_workspace_size", "da_hybrid_prefill_varlen",
+        "da_dense_prefill_varlen"])
 
 
 def test_library_exports_every_declared_symbol():
@@ -110,6 +112,32 @@ def test_decode_rejects_misaligned_values():
             rc = fn(a, 1, 1, 32, 8, D, 32 * D, D, a, vp, *st_p, a, 8 * cap, cap, a, cap, a, vx,
                     *st_x, W, 0, f, a, 32 * D, D, *tail)
             assert rc == -1 and "value rows" in _err()
+
+
+def test_varlen_entry_points_reject_bad_arguments():
+    lib = _native.lib()
+    fake = ctypes.c_void_p(1 << 20)
+    f = ctypes.c_float(1.0)
+    # null cu_seqlens, max_seqlen beyond the token count, max_chunks too small
+    assert lib.da_select_varlen(fake, 1, 2, 8, 1000, 128, 1024, 128, None, 600, f, 0, 512, 0,
+                                fake, fake, 2, None) == -1
+    assert lib.da_select_varlen(fake, 1, 2, 8, 1000, 128, 1024, 128, fake, 1001, f, 0, 512, 0,
+                                fake, fake, 2, None) == -1
+    assert lib.da_select_varlen(fake, 1, 2, 8, 1000, 128, 1024, 128, fake, 600, f, 0, 512, 0,
+                                fake, fake, 1, None) == -1
+    assert "max_chunks" in _err()
+    need = lib.da_pack_varlen_workspace_size(2, 8, 600)
+    assert need == 2 * 2 * 8 * 10 * 4
+    assert lib.da_pack_varlen(fake, fake, fake, 1, 2, 8, 1000, 128, 1024, 128, 1024, 128, fake, 600,
+                              fake, fake, fake, fake, fake, fake, fake, need - 4, None) == -4
+    st = _native.strides_array([0, 128, 4096] + [0, 128, 1024] * 2 + [0, 128, 1024] * 2 +
+                               [0, 128, 4096] + [0, 1000, 1] * 2)
+    assert lib.da_hybrid_varlen_workspace_size(2, 8, 600) == lib.da_hybrid_workspace_size(2, 8, 600)
+    assert lib.da_hybrid_prefill_varlen(fake, fake, fake, fake, fake, fake, fake, 3, fake, 1, 2, 32, 8,
+                                        1000, 128, st, None, 600, fake, 128, f, 0, 0, fake, 1 << 30,
+                                        None) == -1
+    assert lib.da_dense_prefill_varlen(fake, fake, fake, fake, 1, 2, 32, 8, 1000, 128, st, fake, 0, 1,
+                                       f, None) == -1
 
 
 def test_workspace_sizes():

@@ -17,6 +17,10 @@ def _batch(lens, hq=8, hkv=2, d=128, seed=3):
     from deltaattention_amd import synth
     qs, ks, vs = [], [], []
     for i, n in enumerate(lens):
+        if n == 0:
+            for lst, h in ((qs, hq), (ks, hkv), (vs, hkv)):
+                lst.append(torch.zeros((0, h, d), dtype=torch.bfloat16, device="cuda"))
+            continue
         rho = np.random.default_rng(seed + i).uniform(0.6, 0.95, size=hkv)  # per head
         q, k, v = synth.make_layer_inputs(1, hq, hkv, n, d, rho=rho, seed=seed + i,
                                           device="cuda")
@@ -84,3 +88,70 @@ def test_varlen_rejects_bad_cu_seqlens(gpu):
         ops.delta_prefill_varlen(q, k, v, [0, 100, 64], 9.0)
     with pytest.raises(ValueError, match="cu_seqlens"):
         ops.dense_prefill_varlen(q, k, v, [0, 64])
+
+
+LENS2 = [1000, 0, 700, 1, 2100, 129]   # an empty sequence and a one-token one
+
+
+def _per_seq(x, s, e):
+    return x[s:e].permute(1, 0, 2).unsqueeze(0).contiguous()
+
+
+@pytest.mark.parametrize("chunk,divide_to", [(512, 0), (0, 3)])
+def test_varlen_select_pack_bitexact(gpu, chunk, divide_to):
+    """select_varlen and pack_varlen against the oracle run on each sequence alone:
+    keep rows, chunk counts, anchor counts, P_b, timestamps, counts and packed rows
+    bit-exact, zero padding up to P_b included."""
+    from deltaattention_amd import ops
+    from oracle import select_oracle_c as OC
+    q, k, v, cu = _batch(LENS2, hq=8, hkv=2)
+    tau = 9.0
+    announce(f"varlen select+pack lens {LENS2} chunk={chunk} divide_to={divide_to}")
+    keep, cc = ops.select_varlen(k, cu, tau, chunk, divide_to)
+    packed = ops.pack_varlen(keep, k, v, cu)
+    torch.cuda.synchronize()
+    keep_h, cc_h = keep.cpu().numpy(), cc.cpu().numpy()
+    P_h = packed.num_packed.cpu().numpy()
+    for b, (s, e) in enumerate(zip(cu[:-1], cu[1:])):
+        n = e - s
+        if n == 0:
+            assert P_h[b] == 0 and (cc_h[b] == 0).all()
+            continue
+        kf = _per_seq(k, s, e).float().cpu().numpy()
+        vf = _per_seq(v, s, e).float().cpu().numpy()
+        okeep, occ = OC.select_delta(kf, tau, chunk, divide_to)
+        assert np.array_equal(keep_h[:, s:e], okeep[0]), f"keep of sequence {b}"
+        assert np.array_equal(cc_h[b, :, :occ.shape[-1]], occ[0]) and (cc_h[b, :, occ.shape[-1]:] == 0).all()
+        ref = O.pack(kf, vf, okeep)
+        P = ref["P"]
+        assert P_h[b] == P
+        assert np.array_equal(packed.anchor_counts[b].cpu().numpy(), ref["anchor_counts"][0])
+        assert np.array_equal(packed.timestamps[:, s:s + P].cpu().numpy(), ref["timestamps"][0])
+        assert np.array_equal(packed.counts[:, s:s + P].cpu().numpy(), ref["counts"][0])
+        assert np.array_equal(packed.k_packed[s:s + P].permute(1, 0, 2).float().cpu().numpy(), ref["k_packed"][0])
+        assert np.array_equal(packed.v_packed[s:s + P].permute(1, 0, 2).float().cpu().numpy(), ref["v_packed"][0])
+
+
+@pytest.mark.parametrize("hq,hkv", [(8, 2), (6, 3)], ids=["gqa4-grouped", "gqa2-per-head"])
+@pytest.mark.parametrize("variant", ["hybrid", "sanity", "pure_phase1"])
+def test_varlen_variants_equal_per_sequence_runs(gpu, hq, hkv, variant):
+    """One varlen launch equals B = 1 launches sequence by sequence, bit for bit, for every
+    variant and for both attention kernels (GQA group a multiple of 4 or not); the empty
+    sequence leaves its (zero) rows untouched.  cu_seqlens is passed as a device tensor
+    with max_seqlen."""
+    from deltaattention_amd import ops
+    q, k, v, cu = _batch(LENS2, hq=hq, hkv=hkv)
+    tau = 9.0
+    announce(f"varlen {variant} Hq={hq} Hkv={hkv} lens {LENS2}")
+    cu_dev = torch.tensor(cu, dtype=torch.int32, device=gpu)
+    out = ops.delta_prefill_varlen(q, k, v, cu_dev, tau, 512, window=128, variant=variant,
+                                   max_seqlen=max(LENS2))
+    dense = ops.dense_prefill_varlen(q, k, v, cu_dev, max_seqlen=max(LENS2))
+    for s, e in zip(cu[:-1], cu[1:]):
+        if e == s:
+            continue
+        ref = ops.delta_prefill(_per_seq(q, s, e), _per_seq(k, s, e), _per_seq(v, s, e), tau, 512,
+                                window=128, variant=variant)
+        assert torch.equal(_per_seq(out, s, e), ref), f"{variant} sequence [{s}, {e})"
+        ref = ops.dense_prefill(_per_seq(q, s, e), _per_seq(k, s, e), _per_seq(v, s, e))
+        assert torch.equal(_per_seq(dense, s, e), ref), f"dense sequence [{s}, {e})"
