@@ -610,7 +610,7 @@ def measure_layer(args, N, ratio, headline):
         "roofline": {"bound": "mfma", "achieved": round(hyb_tflops, 2), "peak": BF16_PEAK_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(hyb_tflops / BF16_PEAK_TFLOPS, 4),
                      "traffic": traffic_bytes(args, N, r_real, ratio),
-                     "kernel": "attn_pp_kernel<hybrid> (da_hybrid_prefill)",
+                     "kernel": "attn_w64_kernel<hybrid> (da_hybrid_prefill)",
                      "algorithmic_flops": fl["algorithmic"]},
     }
     rec.update({k2: v2 for k2, v2 in res.items() if k2 not in ("seq_len",)})

@@ -89,7 +89,7 @@ struct AttnArgs {
   int causal;
   const int32_t* sched;  // [B*Hkv][2][nblk_cap]: block maxima, prefix maxima
   int nblk_cap;
-  // prepared by the schedule kernel for attn_pp_kernel, [B*Hkv][wcap] each:
+  // prepared by the schedule kernel for the ping-pong kernel, [B*Hkv][wcap] each:
   const float* wts;    // key bias log2(w_i) / scale_log2 of packed row i (-inf where w_i = 0)
   const int32_t* tsw;  // timestamp of packed row i, INT_MAX where the weight is 0
   const float* zeros;  // 64 zero biases (the exact tiles)
@@ -482,52 +482,6 @@ void attn_kernel_pure(AttnArgs a) {
   attn_body<kPure, DT>(a);
 }
 
-// ====================================================================================
-// Ping-pong kernel for GQA groups that are a multiple of 4 (the Llama-3 hot path).
-//
-// A workgroup is 8 waves, two per SIMD.  Waves 0-3 (group A) own query rows
-// R0..R0+31 and waves 4-7 (group B) rows R0+32..R0+63, each wave one query head of a
-// GQA group of 4, so all 8 waves read the same K/V tiles.  In every section one group
-// runs its matrix work (P.V of the previous tile and Q.K of the current one: 32 MFMAs,
-// at raised issue priority) while the other runs its softmax (VALU), and the roles
-// swap each section: group B runs one section behind group A, so the two waves that
-// share a SIMD always have complementary work and the MFMA pipe and the VALU
-// co-execute.  Two sections form a window; the workgroup synchronises once per window.
-//
-// K and V tiles go straight from memory to LDS (buffer_load ... lds), three stages
-// each, issued two windows ahead of their use; V is kept row-major and read as V^T
-// with ds_read_b64_tr_b16.  No tile passes through registers.
-//
-// The running maximum is updated lazily: only when a tile's maximum exceeds it by
-// more than 2^8 in probability (8 in log2 units) are O and l rescaled, so p stays
-// below 256 and the rescale (64 multiplies) is rare.  The result is unchanged; only
-// the rounding reference point of bf16(p) moves.
-// ====================================================================================
-// Masks of tile scores.  Dense keys: causal (key <= row) and key < Nk.  Pure Phase 1:
-// key valid iff it is a live anchor with timestamp <= row (tl holds INT_MAX otherwise).
-__device__ __forceinline__ void mask_dense(f32x16* s, int key0, int row, int hl, int Nk, bool causal) {
-#pragma unroll
-  for (int kb2 = 0; kb2 < 2; ++kb2)
-#pragma unroll
-    for (int r = 0; r < 16; ++r) {
-      const int key = key0 + kb2 * 32 + 8 * (r >> 2) + 4 * hl + (r & 3);
-      const bool ok = key < Nk && (!causal || key <= row);
-      if (!ok) s[kb2][r] = -INFINITY;
-    }
-}
-__device__ __forceinline__ void mask_pure(f32x16* s, const int* tl, int row, int hl) {
-#pragma unroll
-  for (int kb2 = 0; kb2 < 2; ++kb2)
-#pragma unroll
-    for (int r4 = 0; r4 < 4; ++r4) {
-      const int4 t4 = *(const int4*)(tl + kb2 * 32 + 8 * r4 + 4 * hl);
-      if (!(t4.x <= row)) s[kb2][4 * r4 + 0] = -INFINITY;
-      if (!(t4.y <= row)) s[kb2][4 * r4 + 1] = -INFINITY;
-      if (!(t4.z <= row)) s[kb2][4 * r4 + 2] = -INFINITY;
-      if (!(t4.w <= row)) s[kb2][4 * r4 + 3] = -INFINITY;
-    }
-}
-
 // Third dword of a raw buffer resource on gfx9 (32-bit data format, no swizzle).
 constexpr int kBufferDword3 = 0x00020000;
 
@@ -568,6 +522,23 @@ template <int N>
 __device__ __forceinline__ void lgkm_wait(i16x4& a, i16x4& b) {
   asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(a), "+v"(b) : "i"(N));
 }
+// ds_read_b128 issued as asm (waited for with lgkm_wait), so that the reads stay ahead
+// of the MFMAs that use them.
+__device__ __forceinline__ u32x4 ds_read_b128_asm(uint32_t addr) {
+  u32x4 v;
+  asm volatile("ds_read_b128 %0, %1" : "=v"(v) : "v"(addr));
+  return v;
+}
+template <int N>
+__device__ __forceinline__ void lgkm_wait(u32x4& a, u32x4& b) {
+  asm volatile("s_waitcnt lgkmcnt(%2)" : "+v"(a), "+v"(b) : "i"(N));
+}
+// An unspecified value that costs no instruction: for a register array on a path where
+// it is dead, so that it is not live around the loop.
+template <typename T>
+__device__ __forceinline__ void undefined(T& x) {
+  asm volatile("" : "=v"(x));
+}
 template <typename F, int... I>
 __device__ __forceinline__ void static_for_impl(F&& f, std::integer_sequence<int, I...>) {
   (f(std::integral_constant<int, I>{}), ...);
@@ -589,50 +560,90 @@ __device__ __forceinline__ float halves_sum(float x) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-// MFMAs of a P.V block whose V^T operand reads run this many MFMAs ahead.
-constexpr int kTrAhead = 6;
-
-// Scheduling pattern for a block of 16 LDS operand reads feeding 16 MFMAs: eight reads
-// are issued ahead, then reads and MFMAs alternate, so an MFMA rarely waits for LDS.
-__device__ __forceinline__ void pipe_mfma_reads_deep() {
-  __builtin_amdgcn_sched_group_barrier(0x100, 8, 0);  // DS read x8
-#pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // MFMA
-    __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);  // DS read
-  }
-  __builtin_amdgcn_sched_group_barrier(0x008, 8, 0);  // MFMA x8
-}
-
 // s_waitcnt immediate (gfx9 encoding) that waits for vmcnt <= n only.
 constexpr int vmcnt_only(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 
-constexpr int kPPMetaSlot = kTileN * 8;  // float weights[64], int timestamps[64]
-constexpr int kPPLds = 3 * kKBytes + 3 * kVBytes + 4 * kPPMetaSlot;
-// offsets of the weights and timestamps relative to (slot - kPPCnt), as in a K stage
-constexpr int kPPCnt = kKBytes;
-constexpr int kPPTs = kKBytes + kTileN * 4;
+// The running maximum is updated lazily: only when a tile's maximum exceeds it by more
+// than 2^8 in probability (8 in log2 units) are O and l rescaled.
 constexpr float kLazyLog2 = 8.0f;
+
+// ====================================================================================
+// Ping-pong kernel for GQA groups that are a multiple of 4 (the Llama-3 hot path).
+//
+// A workgroup is 8 waves, two per SIMD, and covers one logical 128-row query block of
+// the reference's schedule for 4 query heads of one GQA group, so all 8 waves read the
+// same K/V tiles.  Waves 0-3 (group A) own rows R0..R0+63 and waves 4-7 (group B) rows
+// R0+64..R0+127, each wave one query head, as two 32-row column blocks.  Tiles are 32
+// keys; every tile boundary falls on the reference's logical 128-key grid.
+//
+// In every section one group runs its matrix work (P.V of the previous tile, then Q.K
+// of the current one: 32 MFMAs at raised issue priority) while the other group runs its
+// softmax (VALU); group B runs one section behind group A, so the two waves sharing a
+// SIMD have complementary work and the MFMA pipe and the VALU co-execute.  Two sections
+// form a window; the workgroup synchronises once per window.  Every K fragment and every
+// V^T fragment read from LDS feeds two MFMAs, one per column block.
+//
+// K and V tiles go straight from memory to LDS (buffer_load ... lds), three stages each,
+// issued two windows (K) and one window (V) ahead of their use; V is kept row-major and
+// read as V^T with ds_read_b64_tr_b16.  No tile passes through registers.  Q of column
+// block 0 stays in registers; Q of column block 1 sits in LDS, lane-private (each lane
+// reads back only what it wrote), which keeps the wave within 256 registers.
+// ====================================================================================
+constexpr int kWTK = 32;                         // keys per tile
+constexpr int kWKBytes = kWTK * kD * 2;          // 8 KiB
+constexpr int kWVBytes = kWTK * kD * 2;          // 8 KiB
+constexpr int kWMetaSlot = 64 * 8;               // weights[64] fp32, timestamps[64] int32
+constexpr int kWCnt = 0, kWTs = 64 * 4;          // offsets inside a meta slot
+constexpr int kWQBytes = 32 * kD * 2;          // Q of one 32-row column block, per wave
+constexpr int kWLds = 3 * kWKBytes + 3 * kWVBytes + 4 * kWMetaSlot + 8 * kWQBytes;
+// K stages and Q blocks start at multiples of 256 bytes (the kernel has no static LDS, so
+// its dynamic LDS starts at address 0): the K / Q fragment addresses are formed by XOR.
+static_assert(kWKBytes % 256 == 0 && (3 * kWKBytes + 3 * kWVBytes + 4 * kWMetaSlot) % 256 == 0 &&
+              kWQBytes % 256 == 0, "K stages and Q blocks must be 256-byte aligned");
+
+// Masks of one 32-key x 32-row score block (S^T register r holds key 8 (r / 4) + 4 hl +
+// r % 4 of the tile for the lane's row).
+__device__ __forceinline__ void mask_dense32(f32x16& s, int key0, int row, int hl, int Nk, bool causal) {
+#pragma unroll
+  for (int r = 0; r < 16; ++r) {
+    const int key = key0 + 8 * (r >> 2) + 4 * hl + (r & 3);
+    const bool ok = key < Nk && (!causal || key <= row);
+    if (!ok) s[r] = -INFINITY;
+  }
+}
+__device__ __forceinline__ void mask_pure32(f32x16& s, const int* tl, int row, int hl) {
+#pragma unroll
+  for (int r4 = 0; r4 < 4; ++r4) {
+    const int4 t4 = *(const int4*)(tl + 8 * r4 + 4 * hl);
+    if (!(t4.x <= row)) s[4 * r4 + 0] = -INFINITY;
+    if (!(t4.y <= row)) s[4 * r4 + 1] = -INFINITY;
+    if (!(t4.z <= row)) s[4 * r4 + 2] = -INFINITY;
+    if (!(t4.w <= row)) s[4 * r4 + 3] = -INFINITY;
+  }
+}
 
 template <int VARIANT, int DT>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
-void attn_pp_kernel(AttnArgs a) {
+void attn_w64_kernel(AttnArgs a) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
   char* const kst0 = smem;
-  char* const vst0 = smem + 3 * kKBytes;
-  char* const meta0 = smem + 3 * kKBytes + 3 * kVBytes;
+  char* const vst0 = smem + 3 * kWKBytes;
+  char* const meta0 = smem + 3 * kWKBytes + 3 * kWVBytes;
   const int tid = threadIdx.x, lane = tid & 63;
-  const int wid = tid >> 6;  // uniform per wave; kept as a VGPR value (lower register pressure)
+  const int wid = tid >> 6;  // uniform per wave
+  // Q of column block 1, lane-private: each lane reads back only the 16-byte chunks it
+  // wrote (the K fragment layout), so the 32 registers it would take stay free
+  char* const qs = meta0 + 4 * kWMetaSlot + wid * kWQBytes;
   const int grp = wid >> 2, hw = wid & 3;
   const int hl = lane >> 5, ql = lane & 31;
 
-  // ---- workgroup -> (unit, row group): XCD-aware, longest rows first ----
+  // ---- workgroup -> (unit, row group).  A unit is 4 query heads of one (batch, KV
+  // head), g-major.  When the units split evenly over the 8 XCDs (workgroup i runs on
+  // XCD i mod 8), each XCD takes a contiguous range of units and walks their row groups
+  // longest first, so a unit's K/V stay in one XCD's L2 ----
   const int wg = blockIdx.x;
   int unit, rg;
   if ((a.units & 7) == 0) {
-    // workgroup i runs on XCD i mod 8; each XCD takes whole units (a KV head of one
-    // sequence) and runs them one after another, every unit's row groups longest first,
-    // so the 32 CUs of an XCD share one unit's K/V in their L2
     const int xcd = wg & 7, idx = wg >> 3, upx = a.units >> 3;
     unit = xcd * upx + idx / a.n_row_groups;
     rg = a.n_row_groups - 1 - idx % a.n_row_groups;
@@ -640,26 +651,24 @@ void attn_pp_kernel(AttnArgs a) {
     unit = wg % a.units;
     rg = a.n_row_groups - 1 - wg / a.units;
   }
-  // KV-head-major units (see attn_kernel)
   const int hunits = a.G >> 2;
   const int gb = unit / hunits;  // g * B + b
   const int hu = unit - gb * hunits;
   const int g = gb / a.B, b = gb - (gb / a.B) * a.B;
   const int bg = b * a.Hkv + g;
   const int h = g * a.G + hu * 4 + hw;
-  const int R0 = rg * 64;
+  const int R0 = rg * 128;
   const int Nq = a.seq.cu ? a.seq.len(b) : a.Nq;
   const int Nk = a.seq.cu ? a.seq.len(b) : a.Nk;
   if (R0 >= Nq) return;  // a row group past the end of a shorter sequence (whole workgroup)
-  const int r0w = R0 + grp * 32;
-  const int wg_end = R0 + 64;
-  const int start_m = (R0 / kBlock) * kBlock;
-  const int row = r0w + ql;
+  const int r0w = R0 + grp * 64;  // first row of this wave; column block cb holds r0w + 32 cb + ql
+  const int wg_end = R0 + 128;
+  const int start_m = R0;
 
-  // ---- schedule (identical to attn_kernel) ----
+  // ---- schedule of the logical 128-row block R0 ----
   int P = a.P_host;
   if (a.P_dev) P = min(a.seq.cu ? a.P_dev[b] : *a.P_dev, a.P_host);
-  if (a.seq.cu) P = min(P, Nk);  // a sequence's packed rows lie inside its own tokens
+  if (a.seq.cu) P = min(P, Nk);
   int n1 = 0, ds = 0;
   int kend = a.causal ? min(Nk, wg_end) : Nk;
   if (VARIANT == kHybrid || VARIANT == kSanity) {
@@ -669,13 +678,13 @@ void attn_pp_kernel(AttnArgs a) {
     int n_safe, last;
     safe_prefix(bmax, pmax, nblk, start_m - a.window, n_safe, last);
     ds = max(0, ((last + 1) / kBlock) * kBlock);
-    if (VARIANT == kHybrid) n1 = n_safe * (kBlock / kTileN);
+    if (VARIANT == kHybrid) n1 = n_safe * (kBlock / kWTK);
     kend = min(Nk, wg_end);
   } else if (VARIANT == kPure) {
-    n1 = (P + kTileN - 1) / kTileN;
+    n1 = (P + kWTK - 1) / kWTK;
     kend = 0;
   }
-  const int n2 = kend > ds ? (kend - ds + kTileN - 1) / kTileN : 0;
+  const int n2 = kend > ds ? (kend - ds + kWTK - 1) / kWTK : 0;
   const int T = n1 + n2;
 
   const uint16_t* kp_base = a.kp + a.seq.base(b, a.skp_b, a.skp_n) + (int64_t)g * a.skp_h;
@@ -687,16 +696,16 @@ void attn_pp_kernel(AttnArgs a) {
   constexpr bool kPureV = VARIANT == kPure;
   constexpr bool kWeights = VARIANT == kHybrid || VARIANT == kPure;
 
-  auto key0_of = [&](int t) { return t < n1 ? t * kTileN : ds + (t - n1) * kTileN; };
-  auto skipped = [&](int t) { return t >= n1 && a.causal && key0_of(t) > r0w + 31; };
+  auto key0_of = [&](int t) { return t < n1 ? t * kWTK : ds + (t - n1) * kWTK; };
+  auto skipped = [&](int t) { return t >= n1 && a.causal && key0_of(t) > r0w + 63; };
 
-  // ---- staging: loads straight into LDS (buffer_load ... lds), three stages each
-  // for K and V and a ring of four slots for the tiles' weights.  Wave w loads the
-  // 4-row chunks 2w and 2w + 1 of both tiles: lane l writes 16 bytes at chunk base +
-  // 16 l, i.e. row 4c + l / 16 at position l % 16, so it fetches the source chunk that
-  // the swizzled layout keeps there.  The buffer resource covers exactly the tile's
-  // valid keys: rows past the end arrive as zeros.  Each wave issues the same loads in
-  // every window, so the s_waitcnt vmcnt(n) at the end of a window, n = the loads of
+  // ---- staging: loads straight into LDS, three stages each for K and V and a ring of
+  // four slots for the tiles' weights.  Wave w loads rows 4w .. 4w + 3 of both tiles:
+  // lane l writes 16 bytes at 1 KiB w + 16 l, i.e. row 4w + l / 16 at position l % 16,
+  // so it fetches the source chunk that the swizzled layout keeps there.  The buffer
+  // resource covers exactly the tile's valid keys: rows past the end, and 8-dim chunks
+  // at or beyond the head dimension, arrive as zeros.  Each wave issues the same loads
+  // in every window, so the s_waitcnt vmcnt(n) at the end of a window, n = the loads of
   // this window, waits exactly for those of the window before. ----
   const int wid_s = __builtin_amdgcn_readfirstlane(wid);
   const char* kb1 = (const char*)uniform_ptr(kp_base);
@@ -715,45 +724,39 @@ void attn_pp_kernel(AttnArgs a) {
     const int snb = isK ? (ph1 ? skpb : skb) : (ph1 ? svpb : svb);
     const char* src = isK ? (ph1 ? kb1 : kb2) : (ph1 ? vb1 : vb2);
     const void* base = uniform_ptr(src + (int64_t)key0 * snb);
-    const int nrows = max(0, min(limit - key0, kTileN));
+    const int nrows = max(0, min(limit - key0, kWTK));
     const int range = __builtin_amdgcn_readfirstlane(nrows * snb);
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<void*>(base), (short)0, range, kBufferDword3);
-    char* dst = isK ? kst0 + (t_raw % 3) * kKBytes : vst0 + (t_raw % 3) * kVBytes;
-#pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int rc = 2 * wid_s + j;
-      const int rowt = rc * 4 + (lane >> 4);
-      const int pos = lane & 15;
-      const int chunk = pos ^ (isK ? (rowt & 15) : 4 * (rowt & 3));
-      // 8-dim chunks at or beyond the head dimension read at the end of the range:
-      // out of range, so they arrive as zeros (BLOCK_D padding of the reference)
-      const int off = chunk * 8 < a.D ? rowt * snb + chunk * 16 : range;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)(dst + rc * 1024), 16,
-                                               off, 0, 0, 0);
-    }
+    char* dst = isK ? kst0 + (t_raw % 3) * kWKBytes : vst0 + (t_raw % 3) * kWVBytes;
+    const int rowt = wid_s * 4 + (lane >> 4);
+    const int pos = lane & 15;
+    const int chunk = pos ^ (isK ? (rowt & 15) : 4 * (rowt & 3));
+    const int off = chunk * 8 < a.D ? rowt * snb + chunk * 16 : range;
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)(dst + wid_s * 1024), 16,
+                                             off, 0, 0, 0);
   };
-  // key biases (and timestamps) of the tile's 64 keys, into slot t % 4 of their ring: a
-  // packed tile reads the prepared biases (-inf for rows without weight, rows at and
-  // beyond P included), an exact tile 64 zeros; S^T starts at them
-  auto meta_of = [&](int t) { return meta0 + (t & 3) * kPPMetaSlot; };
+  // key biases (and timestamps) of the tile's 32 keys, into slot t % 4 of their ring
+  // (lanes 32-63 read past the range: zeros); a packed tile reads the prepared biases,
+  // an exact tile zeros; S^T starts at them
+  auto meta_of = [&](int t) { return meta0 + (t & 3) * kWMetaSlot; };
   auto dma_meta = [&](int t_raw) {
     if (!kWeights) return;
     const int t = min(t_raw, T - 1);
     const bool ph1 = t < n1;
-    const int key0 = ph1 ? t * kTileN : 0;
-    const int nrows = ph1 ? max(0, min(a.wcap - key0, kTileN)) : kTileN;
-    char* dst = meta_of(t_raw) - kPPCnt;
+    const int key0 = ph1 ? t * kWTK : 0;
+    const int nrows = ph1 ? max(0, min(a.wcap - key0, kWTK)) : kWTK;
+    char* dst = meta_of(t_raw);
     const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<void*>(uniform_ptr(ph1 ? w_row + key0 : a.zeros)), (short)0,
         __builtin_amdgcn_readfirstlane(nrows * 4), kBufferDword3);
-    __builtin_amdgcn_raw_ptr_buffer_load_lds(rc, (__attribute__((address_space(3))) void*)(dst + kPPCnt), 4,
+    __builtin_amdgcn_raw_ptr_buffer_load_lds(rc, (__attribute__((address_space(3))) void*)(dst + kWCnt), 4,
                                              lane * 4, 0, 0, 0);
     if (kPureV) {
       const __amdgpu_buffer_rsrc_t rt = __builtin_amdgcn_make_buffer_rsrc(
           const_cast<void*>(uniform_ptr(tsw_row + key0)), (short)0, __builtin_amdgcn_readfirstlane(nrows * 4),
           kBufferDword3);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rt, (__attribute__((address_space(3))) void*)(dst + kPPTs), 4,
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rt, (__attribute__((address_space(3))) void*)(dst + kWTs), 4,
                                                lane * 4, 0, 0, 0);
     }
   };
@@ -763,65 +766,55 @@ void attn_pp_kernel(AttnArgs a) {
     if (wid_s == 0) dma_meta(tk);
   };
 
-  // ---- per-lane LDS offsets (stage-relative) ----
-  int k_off[kD / 16];
-#pragma unroll
-  for (int tt = 0; tt < kD / 16; ++tt) k_off[tt] = k_lds_off(ql, 2 * tt + hl);  // + 8192 * kb2
-  // V stays row-major (16-byte chunk c of key row r at position c ^ 4 (r & 3)); the
-  // A operand V^T of a P.V MFMA comes from two ds_read_b64_tr_b16: in each group of 16
-  // lanes, lane 4e + q points at keys row + e, head dims 4q .. 4q + 3, and lane i
-  // receives head dim i of the 4 rows.  v_off[db] covers keys 16u + 4 (lane / 32) + 0..3
-  // (+ 4096 u; + 2048 for keys 8 further) and head dims 32 db + 16 ((lane / 16) & 1) + ..
-  int v_off[4];
-  {
-    const int gq = lane >> 4, sq = lane & 15, q = sq >> 2;
-    const int base = (4 * (gq >> 1) + q) * 256 + ((2 * (gq & 1) + ((sq & 3) >> 1)) << 4) + 8 * (sq & 1);
-#pragma unroll
-    for (int db = 0; db < 4; ++db) v_off[db] = base + 64 * (db ^ q);
-  }
+  // ---- per-lane LDS offsets (stage-relative).  K: rows of 256 bytes, 16-byte chunk c
+  // of row r at position c ^ (r & 15); the lane reads chunk 2 j + hl of row ql.  V^T:
+  // fragments of 16 keys x 32 head dims (db) read with ds_read_b64_tr_b16 from rows
+  // whose chunks sit at c ^ 4 (r & 3).  Both are recomputed in each matrix section
+  // (made opaque there) rather than held in registers ----
+  int k_row = ql * 256, k_swz = ql & 15;
+  int v_q = (lane & 15) >> 2;
+  int v_lane = (4 * ((lane >> 4) >> 1) + v_q) * 256 + ((2 * ((lane >> 4) & 1) + ((lane & 3) >> 1)) << 4) +
+                     8 * (lane & 1);
 
-
-  f32x16 o[4];
+  f32x16 o[2][4];
 #pragma unroll
-  for (int i = 0; i < 4; ++i) o[i] = f32x16{};
+  for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) o[cb][i] = f32x16{};
   f32x16 s[2];
-  u32x4 pw[4];
-  float m_used = -INFINITY, l_i = 0.0f;
+  u32x4 pw[2][2];
+  float m_used[2] = {-INFINITY, -INFINITY}, l_i[2] = {0.0f, 0.0f};
   const float c = a.scale_log2;
   const float lazy_thr = kLazyLog2 / c;
 
-  // Sections 2k and 2k + 1 form window k; the workgroup synchronises only at the end
-  // of a window (within one, each group works on its own registers and on stages that
-  // no load touches).  Window k issues the loads of K(k+2) (with its weights) and of
-  // V(k+1) at its start and waits at its end for those of window k - 1.  K(t) is read
-  // in window t, V(t) in window t + 1 and the weights of tile t in windows t and t + 1;
-  // the loads that overwrite stage t % 3 (ring slot t % 4) come in window t + 1 (t + 2,
-  // t + 2), after the barrier.  Wave 0 loads the weights; the barrier after its wait
-  // publishes them.
   if (T > 0) {
     dma_rows(true, 0);
     if (wid_s == 0) dma_meta(0);
     dma_issue(1, 0);
   }
-  // ---- Q^T in registers, loaded while the first tiles are in flight ----
+  // ---- Q^T of both column blocks in registers, loaded while the first tiles are in
+  // flight; rows past Nq load row Nq - 1 and dims past D dims 0..7, zeroed after ----
   u32x4 qreg[kD / 16];
-  {
-    // rows past Nq load row Nq - 1 (no branch between the loads) and are zeroed after
+#pragma unroll
+  for (int cb = 0; cb < 2; ++cb) {
+    const int row = r0w + 32 * cb + ql;
     const uint16_t* qrow = a.q + a.seq.base(b, a.sq_b, a.sq_n) + (int64_t)h * a.sq_h + (int64_t)min(row, Nq - 1) * a.sq_n;
-    // dims at or beyond the head dimension load dims 0..7 and are zeroed after
     u32x4 w[kD / 16];
 #pragma unroll
     for (int t = 0; t < kD / 16; ++t) {
       const int d0 = 16 * t + 8 * hl;
       w[t] = *(const u32x4*)(qrow + (d0 < a.D ? d0 : 0));
     }
-    // Redefine Q^T here so the loop does not see it as an outstanding load: otherwise
-    // every S = K Q^T block waits for all memory loads, including the staging loads
-    // meant to land two sections later.
+    // redefined so that the loop does not see Q as an outstanding load (the S = K Q^T
+    // blocks would otherwise wait for every memory load, the staging loads included)
 #pragma unroll
     for (int t = 0; t < kD / 16; ++t) {
       asm volatile("" : "+v"(w[t]));
-      qreg[t] = (row < Nq && 16 * t + 8 * hl < a.D) ? w[t] : u32x4{0, 0, 0, 0};
+      const u32x4 qv = (row < Nq && 16 * t + 8 * hl < a.D) ? w[t] : u32x4{0, 0, 0, 0};
+      if (cb == 0)
+        qreg[t] = qv;
+      else
+        *(u32x4*)(qs + k_row + (((2 * t + hl) ^ k_swz) << 4)) = qv;
     }
   }
   if (T > 0) {
@@ -829,15 +822,20 @@ void attn_pp_kernel(AttnArgs a) {
     lds_barrier();
   }
 
-  const int nsec = T > 0 ? 2 * T + 2 : 0;
-  for (int sec = 0; sec < nsec; ++sec) {
+  constexpr int kWAhead = 3;    // V^T fragments read ahead of their MFMAs
+  constexpr int kWQKAhead = 2;  // (K, Q) fragment pairs read ahead of their MFMAs
+  const int nwin = T > 0 ? T + 1 : 0;
+  // One window = two sections.  Group 0 runs matrix(w), softmax(w); group 1 runs
+  // softmax(w - 1), matrix(w).  Each group has a loop of its own with the section kinds
+  // fixed at compile time, so that only P (group 0) or only S (group 1) is live across
+  // the loop's back edge.
+  auto section = [&](const int sec, auto GRP, auto ODD) {
+    constexpr int grp_c = decltype(GRP)::value;
+    constexpr bool odd = decltype(ODD)::value;
     const int tl = sec >> 1;
-    const int sw = sec - grp;
-    // window tl loads K(tl + 2) and V(tl + 1), group A in its matrix section (between
-    // its P.V and Q.K blocks).  Group B issues them in its softmax section in the
-    // variants with packed tiles and in its matrix section in the dense one (the faster
-    // placement of each, measured).
-    bool issued = (sec & 1) != (VARIANT == kDense ? grp : 0);
+    const int sw = sec - grp_c;
+    // each wave issues its window's tile loads in its matrix section (after the P.V block)
+    bool issued = odd != (grp_c != 0);
     auto issue_once = [&]() {
       if (!issued) {
         dma_issue(tl + 2, tl + 1);
@@ -846,152 +844,248 @@ void attn_pp_kernel(AttnArgs a) {
     };
     if (sw >= 0) {
       const int t = sw >> 1;
-      if ((sw & 1) == 0) {
-        // ---- matrix section: O^T += V^T P^T for tile t-1, then S^T = K Q^T for tile t ----
-        // Raised issue priority: the matrix pipe is the bottleneck, the softmax wave on
-        // the same SIMD takes the remaining issue slots.
+      if constexpr (((odd ? 1 : 0) + grp_c) % 2 == 0) {
+        // ---- matrix section: O^T += V^T P^T for tile t-1, then S^T = K Q^T for tile t,
+        // each LDS fragment feeding both column blocks ----
         __builtin_amdgcn_s_setprio(1);
+        const bool do_pv = t >= 1 && !skipped(t - 1);
         const bool do_qk = t < T && !skipped(t);
-        if (kWeights && do_qk) {
-          // S^T starts at the keys' bias log2(weight) / c (packed tiles; 0 for exact
-          // tiles, -inf for rows that carry no weight), so that exp2(c (s - m)) in the
-          // softmax is already the weighted probability.  Loaded before the P.V block
-          // (S is free by now), outside the Q.K block's read pipeline.
-          const float* lw = (const float*)meta_of(t) + 4 * hl;
+        // One stream of LDS operand reads for the section: the V^T fragments of the P.V
+        // block, then (hybrid, pure) the keys' biases, then the (K, Q) fragment pairs of
+        // the S^T block, each read a few MFMA pairs ahead of its use, across the border
+        // between the blocks.  The stream's order is fixed at compile time, so every wait
+        // is an exact lgkmcnt.
+        auto block = [&](auto PVC, auto QKC) {
+          constexpr bool PV = decltype(PVC)::value, QK = decltype(QKC)::value;
+          constexpr bool BIAS = QK && kWeights;
+          constexpr int NPV = PV ? 8 : 0, NQK = QK ? kD / 16 : 0;
+          constexpr int EBIAS = NPV;                   // stream index of the bias reads
+          constexpr int EQK = NPV + (BIAS ? 1 : 0);    // stream index of (K, Q) pair 0
+          constexpr int E = EQK + NQK;                 // stream length
+          constexpr int NM = NPV + NQK;                // MFMA pairs
+          // stream element of MFMA pair i; elements issued before pair i's wait
+          constexpr auto el = [](int i) { return i < NPV ? i : EQK + (i - NPV); };
+          constexpr auto size = [](int e) { return (BIAS && e == EBIAS) ? 4 : 2; };
+          constexpr auto issued = [el](int i) {
+            int n = 0;
+            for (int k = 0; k <= i; ++k) {
+              const int a = el(k) + 1 + (k < NPV ? kWAhead - 1 : kWQKAhead - 1);
+              n = a > n ? a : n;
+            }
+            return n < E ? n : E;
+          };
+          constexpr auto pending = [el, size, issued](int i) {
+            int c = 0;
+            for (int e = el(i) + 1; e < issued(i); ++e) c += size(e);
+            return c;
+          };
+          uint32_t va[4] = {0, 0, 0, 0};
+          if constexpr (PV) {
+            const uint32_t vb = lds_addr(vst0) + ((t - 1) % 3) * kWVBytes;
+            // opaque: otherwise the offsets are hoisted out of the loop into registers
+            asm volatile("" : "+v"(v_lane), "+v"(v_q));
 #pragma unroll
-          for (int kb2 = 0; kb2 < 2; ++kb2) {
-            const f32x4 b0 = *(const f32x4*)(lw + kb2 * 32);
-            const f32x4 b1 = *(const f32x4*)(lw + kb2 * 32 + 8);
-            const f32x4 b2 = *(const f32x4*)(lw + kb2 * 32 + 16);
-            const f32x4 b3 = *(const f32x4*)(lw + kb2 * 32 + 24);
-            s[kb2] = __builtin_shufflevector(__builtin_shufflevector(b0, b1, 0, 1, 2, 3, 4, 5, 6, 7),
-                                             __builtin_shufflevector(b2, b3, 0, 1, 2, 3, 4, 5, 6, 7),
-                                             0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15);
+            for (int db = 0; db < 4; ++db) va[db] = vb + v_lane + 64 * (db ^ v_q);
           }
-        }
-        if (t >= 1 && !skipped(t - 1)) {
-          // The V^T operands come from transpose reads issued by hand (the compiler
-          // would make each wait for every load to LDS in flight), four MFMAs ahead,
-          // with the matching lgkmcnt waits: LDS reads complete in order.
-          const uint32_t vb = lds_addr(vst0) + ((t - 1) % 3) * kVBytes;
-          uint32_t va[4];
+          uint32_t kla = 0, qla = 0, bla = 0;
+          int kx = 0;
+          if constexpr (QK) {
+            asm volatile("" : "+v"(k_row), "+v"(k_swz));
+            // chunk 2 j + hl of the lane's row sits at ((2 j + hl) ^ k_swz) * 16 =
+            // ((32 j) ^ kx) + klo with kx = (k_swz & 14) * 16, klo = (hl ^ k_swz & 1) * 16.
+            // The stage and Q bases are multiples of 256, so the address of chunk 2 j + hl
+            // is (base + klo + kx) ^ (32 j): one XOR per read.
+            kx = (k_swz & 14) << 4;
+            const int klo = k_row + (((hl ^ k_swz) & 1) << 4) + kx;
+            kla = lds_addr(kst0 + (t % 3) * kWKBytes) + klo;
+            qla = lds_addr(qs) + klo;
+            bla = lds_addr(meta_of(t) + kWCnt) + 16 * hl;
+          }
+          i16x4 vlo[8], vhi[8];
+          u32x4 kw[kD / 16], qw[kD / 16], bw[4];
+          auto read = [&](auto EC) {
+            constexpr int e = decltype(EC)::value;
+            if constexpr (e < NPV) {
+              vlo[e] = ds_read_tr16<(e >> 2) * 4096>(va[e & 3]);
+              vhi[e] = ds_read_tr16<(e >> 2) * 4096 + 2048>(va[e & 3]);
+            } else if constexpr (BIAS && e == EBIAS) {
 #pragma unroll
-          for (int db = 0; db < 4; ++db) va[db] = vb + v_off[db];
-          i16x4 vlo[16], vhi[16];
-          static_for<kTrAhead>([&](auto I) {
-            constexpr int j = decltype(I)::value;
-            vlo[j] = ds_read_tr16<(j >> 2) * 4096>(va[j & 3]);
-            vhi[j] = ds_read_tr16<(j >> 2) * 4096 + 2048>(va[j & 3]);
-          });
-          static_for<16>([&](auto I) {
+              for (int r = 0; r < 4; ++r) bw[r] = ds_read_b128_asm(bla + 32 * r);
+            } else {
+              constexpr int j = e - EQK;
+              kw[j] = ds_read_b128_asm(kla ^ (32u * j));
+              qw[j] = ds_read_b128_asm(qla ^ (32u * j));
+            }
+          };
+          static_for<issued(0)>(read);
+          issue_once();  // the tile loads go out while the first reads are in flight
+          static_for<NM>([&](auto I) {
             constexpr int i = decltype(I)::value;
-            // reads issued after those of MFMA i
-            constexpr int after = 2 * ((i + kTrAhead - 1 < 15 ? i + kTrAhead - 1 : 15) - i);
-            lgkm_wait<after>(vlo[i], vhi[i]);
-            const i16x8 vw = __builtin_shufflevector(vlo[i], vhi[i], 0, 1, 2, 3, 4, 5, 6, 7);
-            o[i & 3] = E16<DT>::mfma(__builtin_bit_cast(u32x4, vw), pw[i >> 2], o[i & 3]);
-            if constexpr (i + kTrAhead < 16) {
-              constexpr int j = i + kTrAhead;
-              vlo[j] = ds_read_tr16<(j >> 2) * 4096>(va[j & 3]);
-              vhi[j] = ds_read_tr16<(j >> 2) * 4096 + 2048>(va[j & 3]);
+            if constexpr (i < NPV) {
+              lgkm_wait<pending(i)>(vlo[i], vhi[i]);
+              const u32x4 vw = __builtin_bit_cast(u32x4, __builtin_shufflevector(vlo[i], vhi[i], 0, 1, 2, 3, 4, 5, 6, 7));
+              o[0][i & 3] = E16<DT>::mfma(vw, pw[0][i >> 2], o[0][i & 3]);
+              o[1][i & 3] = E16<DT>::mfma(vw, pw[1][i >> 2], o[1][i & 3]);
+            } else {
+              constexpr int j = i - NPV;
+              lgkm_wait<pending(i)>(kw[j], qw[j]);
+              if constexpr (j == 0) {
+                // S^T starts at the keys' biases (read before pair 0, so complete now),
+                // or at zero (the MFMA's inline constant)
+                if constexpr (BIAS) {
+                  asm volatile("" : "+v"(bw[0]), "+v"(bw[1]), "+v"(bw[2]), "+v"(bw[3]));
+                  const f32x4 b0 = __builtin_bit_cast(f32x4, bw[0]), b1 = __builtin_bit_cast(f32x4, bw[1]);
+                  const f32x4 b2 = __builtin_bit_cast(f32x4, bw[2]), b3 = __builtin_bit_cast(f32x4, bw[3]);
+                  const f32x16 c0 = __builtin_shufflevector(__builtin_shufflevector(b0, b1, 0, 1, 2, 3, 4, 5, 6, 7),
+                                                            __builtin_shufflevector(b2, b3, 0, 1, 2, 3, 4, 5, 6, 7),
+                                                            0, 1, 2, 3, 4, 5, 6, 7, 8, 9, 10, 11, 12, 13, 14, 15);
+                  s[0] = E16<DT>::mfma(kw[0], qreg[0], c0);
+                  s[1] = E16<DT>::mfma(kw[0], qw[0], c0);
+                } else {
+                  s[0] = E16<DT>::mfma(kw[0], qreg[0], f32x16{});
+                  s[1] = E16<DT>::mfma(kw[0], qw[0], f32x16{});
+                }
+              } else {
+                s[0] = E16<DT>::mfma(kw[j], qreg[j], s[0]);
+                s[1] = E16<DT>::mfma(kw[j], qw[j], s[1]);
+              }
             }
+            static_for<issued(i + 1 < NM ? i + 1 : i) - issued(i)>([&](auto K) {
+              read(std::integral_constant<int, issued(i) + decltype(K)::value>{});
+            });
           });
-        }
+        };
+        using BT = std::integral_constant<bool, true>;
+        using BF = std::integral_constant<bool, false>;
+        // The S^T block always runs: where tile t is past the end or skipped, it reads a
+        // stage and a bias slot that hold other data (in bounds) and the softmax ignores
+        // the result.  A third instantiation without it costs more registers than the
+        // few blocks it saves.
+        if (do_pv)
+          block(BT{}, BT{});
+        else
+          block(BF{}, BT{});
         issue_once();
-        if (do_qk) {
-          const char* kst = kst0 + (t % 3) * kKBytes;
-          if (!kWeights) {
-            s[0] = f32x16{};
-            s[1] = f32x16{};
-          }
-          // the two key blocks alternate so that consecutive MFMAs do not depend on each other
-#pragma unroll
-          for (int tt = 0; tt < kD / 16; ++tt) {
-#pragma unroll
-            for (int kb2 = 0; kb2 < 2; ++kb2) {
-              const u32x4 w = *(const u32x4*)(kst + k_off[tt] + kb2 * 8192);
-              s[kb2] = E16<DT>::mfma(w, qreg[tt], s[kb2]);
-            }
-          }
-          pipe_mfma_reads_deep();
+        if (!do_qk) {
+          // not read before the next QK block defines it
+          undefined(s[0]);
+          undefined(s[1]);
         }
         __builtin_amdgcn_s_setprio(0);
-      } else if (t < T && !skipped(t)) {
-        // ---- softmax section for tile t ----
-        const char* kst = meta_of(t) - kPPCnt;  // timestamps at kPPTs
+      } else if (!(t < T && !skipped(t))) {
+        // not read before the next softmax defines it
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb)
+#pragma unroll
+          for (int j = 0; j < 2; ++j) undefined(pw[cb][j]);
+      } else {
+        // ---- softmax section for tile t: the two column blocks side by side (independent
+        // chains that fill each other's latencies), one ballot for both ----
+        const char* ms = meta_of(t);
         const int key0 = key0_of(t);
-        if (kPureV) {
-          mask_pure(s, (const int*)(kst + kPPTs), row, hl);
-        } else if (t >= n1) {
-          if ((a.causal && key0 + kTileN - 1 > r0w) || key0 + kTileN > Nk)
-            mask_dense(s, key0, row, hl, Nk, a.causal);
+        float mx[2];
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb) {
+          const int row = r0w + 32 * cb + ql;
+          if (kPureV) {
+            mask_pure32(s[cb], (const int*)(ms + kWTs), row, hl);
+          } else if (t >= n1) {
+            if ((a.causal && key0 + kWTK - 1 > r0w + 32 * cb) || key0 + kWTK > Nk)
+              mask_dense32(s[cb], key0, row, hl, Nk, a.causal);
+          }
         }
-        float mx = -INFINITY;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) mx = __builtin_fmaxf(mx, __builtin_fmaxf(s[0][r], s[1][r]));
-        mx = halves_max(mx);
-        const bool upd = mx > m_used + lazy_thr;  // no NaN when m_used = -inf
-        if (VARIANT != kDense) issue_once();
-        if (__ballot(upd)) {
-          const float m_new = upd ? mx : m_used;
-          const float alpha = exp2_fast((m_used - m_new) * c);
+        for (int cb = 0; cb < 2; ++cb) {
+          float m = -INFINITY;
 #pragma unroll
-          for (int db = 0; db < 4; ++db)
-#pragma unroll
-            for (int r = 0; r < 16; ++r) o[db][r] *= alpha;
-          l_i *= alpha;
-          m_used = m_new;
+          for (int r = 0; r < 16; r += 2) m = __builtin_fmaxf(m, __builtin_fmaxf(s[cb][r], s[cb][r + 1]));
+          mx[cb] = halves_max(m);
         }
-        const float neg = (m_used == -INFINITY) ? 0.0f : -m_used * c;
-        // P in the 16-bit type for the P.V MFMAs; the row sum adds the fp32 p, as
-        // deltaFlashAttention.py:86-98
-        float psa = 0.0f, psb = 0.0f;
+        // no NaN when m_used = -inf
+        const bool upd0 = mx[0] > m_used[0] + lazy_thr, upd1 = mx[1] > m_used[1] + lazy_thr;
+        if (__ballot(upd0 || upd1)) {
+          // alpha = 1 exactly where a lane keeps its maximum (also where that maximum
+          // is still -inf)
 #pragma unroll
-        for (int kb2 = 0; kb2 < 2; ++kb2) {
+          for (int cb = 0; cb < 2; ++cb) {
+            const bool upd = cb == 0 ? upd0 : upd1;
+            const float m_new = upd ? mx[cb] : m_used[cb];
+            const float alpha = upd ? exp2_fast((m_used[cb] - m_new) * c) : 1.0f;
+#pragma unroll
+            for (int db = 0; db < 4; ++db)
+#pragma unroll
+              for (int r = 0; r < 16; ++r) o[cb][db][r] *= alpha;
+            l_i[cb] *= alpha;
+            m_used[cb] = m_new;
+          }
+        }
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb) {
+          const float neg = (m_used[cb] == -INFINITY) ? 0.0f : -m_used[cb] * c;
+          // P in the 16-bit type for the P.V MFMAs; the row sum adds the fp32 p, as
+          // deltaFlashAttention.py:86-98
+          float psa = 0.0f, psb = 0.0f;
 #pragma unroll
           for (int r4 = 0; r4 < 4; ++r4) {
             float p[4];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) p[e] = exp2_fast(__builtin_fmaf(s[kb2][4 * r4 + e], c, neg));
-            pw[2 * kb2 + (r4 >> 1)][(r4 & 1) * 2 + 0] = E16<DT>::pack(p[0], p[1]);
-            pw[2 * kb2 + (r4 >> 1)][(r4 & 1) * 2 + 1] = E16<DT>::pack(p[2], p[3]);
+            for (int e = 0; e < 4; ++e) p[e] = exp2_fast(__builtin_fmaf(s[cb][4 * r4 + e], c, neg));
+            pw[cb][r4 >> 1][(r4 & 1) * 2 + 0] = E16<DT>::pack(p[0], p[1]);
+            pw[cb][r4 >> 1][(r4 & 1) * 2 + 1] = E16<DT>::pack(p[2], p[3]);
             psa += p[0] + p[1];
             psb += p[2] + p[3];
           }
+          l_i[cb] += psa + psb;
         }
-        l_i += psa + psb;
       }
     }
     issue_once();
-    if (sec & 1) {
+    if (odd) {
       // the loads of window tl - 1 are done when at most this window's are pending
       if (wid_s == 0)
-        __builtin_amdgcn_s_waitcnt(vmcnt_only(4 + (kWeights ? 1 : 0) + (kPureV ? 1 : 0)));
+        __builtin_amdgcn_s_waitcnt(vmcnt_only(2 + (kWeights ? 1 : 0) + (kPureV ? 1 : 0)));
       else
-        __builtin_amdgcn_s_waitcnt(vmcnt_only(4));
+        __builtin_amdgcn_s_waitcnt(vmcnt_only(2));
       barrier_keep_loads();
+    }
+  };
+  using False = std::integral_constant<bool, false>;
+  using True = std::integral_constant<bool, true>;
+  if (grp == 0) {
+    for (int w = 0; w < nwin; ++w) {
+      section(2 * w, std::integral_constant<int, 0>{}, False{});
+      section(2 * w + 1, std::integral_constant<int, 0>{}, True{});
+    }
+  } else {
+    for (int w = 0; w < nwin; ++w) {
+      section(2 * w, std::integral_constant<int, 1>{}, False{});
+      section(2 * w + 1, std::integral_constant<int, 1>{}, True{});
     }
   }
   __builtin_amdgcn_s_waitcnt(vmcnt_only(0));  // no load may land in LDS after the exit
 
   // ---- finalize ----
-  const float l_tot = halves_sum(l_i);
-  float inv;
-  if (VARIANT == kPure)
-    inv = l_tot > 0.0f ? 1.0f / l_tot : 1.0f;  // deltaFlashAttention.py:353-354
-  else
-    inv = 1.0f / l_tot;
-  if (row < Nq) {
-    uint16_t* orow = a.out + a.seq.base(b, a.so_b, a.so_n) + (int64_t)h * a.so_h + (int64_t)row * a.so_n;
 #pragma unroll
-    for (int db = 0; db < 4; ++db)
+  for (int cb = 0; cb < 2; ++cb) {
+    const float l_tot = halves_sum(l_i[cb]);
+    float inv;
+    if (VARIANT == kPure)
+      inv = l_tot > 0.0f ? 1.0f / l_tot : 1.0f;  // deltaFlashAttention.py:353-354
+    else
+      inv = 1.0f / l_tot;
+    const int row = r0w + 32 * cb + ql;
+    if (row < Nq) {
+      uint16_t* orow = a.out + a.seq.base(b, a.so_b, a.so_n) + (int64_t)h * a.so_h + (int64_t)row * a.so_n;
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        u32x2 w;
-        w[0] = E16<DT>::pack(o[db][4 * j + 0] * inv, o[db][4 * j + 1] * inv);
-        w[1] = E16<DT>::pack(o[db][4 * j + 2] * inv, o[db][4 * j + 3] * inv);
-        if (db * 32 + 8 * j + 4 * hl < a.D) *(u32x2*)(orow + db * 32 + 8 * j + 4 * hl) = w;
-      }
+      for (int db = 0; db < 4; ++db)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          u32x2 w;
+          w[0] = E16<DT>::pack(o[cb][db][4 * j + 0] * inv, o[cb][db][4 * j + 1] * inv);
+          w[1] = E16<DT>::pack(o[cb][db][4 * j + 2] * inv, o[cb][db][4 * j + 3] * inv);
+          if (db * 32 + 8 * j + 4 * hl < a.D) *(u32x2*)(orow + db * 32 + 8 * j + 4 * hl) = w;
+        }
+    }
   }
 }
 
@@ -1135,10 +1229,10 @@ static int allow_lds(size_t bytes) {
 }
 
 template <int V, int DT>
-static int allow_lds_pp(size_t bytes) {
+static int allow_lds_w64(size_t bytes) {
   static int done = 0;
   if (!done) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_pp_kernel<V, DT>),
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_w64_kernel<V, DT>),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes);
     if (e != hipSuccess) return set_error(DA_ERR_HIP, "hipFuncSetAttribute: %s", hipGetErrorString(e));
     done = 1;
@@ -1149,12 +1243,12 @@ static int allow_lds_pp(size_t bytes) {
 template <int V, int DT>
 static int launch_attn_t(AttnArgs& a, hipStream_t st) {
   if (a.hpw == 4) {
-    a.rows_per_wg = 64;
-    a.n_row_groups = (a.Nq + 63) / 64;
-    const size_t lds = kPPLds;
+    a.rows_per_wg = 128;
+    a.n_row_groups = (a.Nq + 127) / 128;
+    const size_t lds = kWLds;
     const unsigned grid = (unsigned)((int64_t)a.n_row_groups * a.units);
-    if (int rc = allow_lds_pp<V, DT>(lds)) return rc;
-    hipLaunchKernelGGL((attn_pp_kernel<V, DT>), dim3(grid), dim3(512), lds, st, a);
+    if (int rc = allow_lds_w64<V, DT>(lds)) return rc;
+    hipLaunchKernelGGL((attn_w64_kernel<V, DT>), dim3(grid), dim3(512), lds, st, a);
     return check_launch("attention kernel (ping-pong)");
   }
   const size_t lds = 2 * kStageBytes;

@@ -13,7 +13,7 @@ Every configuration runs the HIP path at its real shape and sizes:
 * config 4: a ragged batch of 8 sequences of 4096..32768 tokens with rho ~ U[0.6, 0.95]
   per (sequence, KV head), each sequence compared as a B = 1 prefill.
 
-With Hkv = 8 and a GQA group of 4, configs 1-4 run attn_pp_kernel's XCD-aware grid
+With Hkv = 8 and a GQA group of 4, configs 1-4 run the ping-pong kernel's XCD-aware grid
 mapping (8 (batch, KV head) units), the launch behind every benchmarked number.
 
 Bars: selection, keep masks, counts, timestamps and the packed rows are bit-exact;
