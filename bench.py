@@ -49,9 +49,10 @@ def parse_args():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--dtype", choices=("bf16", "fp16"), default="bf16",
                     help="16-bit type of Q, K, V (configs 1 and 2); bf16 is the headline")
-    ap.add_argument("--only", choices=("delta", "hybrid", "dense", "compress", "copy"), default=None,
-                    help="run one part for K steps (copy: a 1 GiB device copy, the reference for "
-                         "calibrating the FETCH_SIZE / WRITE_SIZE counters)")
+    ap.add_argument("--only", choices=("delta", "hybrid", "dense", "compress", "copy", "convert"), default=None,
+                    help="run one part for K steps (copy: a 1 GiB device copy; convert: 1 GiB of fp32 "
+                         "read and written as bf16 by a vectorized elementwise kernel -- the "
+                         "references for calibrating the WRITE_SIZE / FETCH_SIZE counters)")
     ap.add_argument("--decode", action="store_true",
                     help="per-token decode latency over the compressed cache left by a "
                          "config-1 prefill (update + attention), against the same decode "
@@ -642,9 +643,13 @@ def run_only(args):
         "compress": lambda: ops.pack(ops.select(k, tau, 512)[0], k, v, out=packed),
     }
     if args.only == "copy":
-        src = torch.ones(1 << 29, dtype=torch.int16, device=q.device)  # 1 GiB
+        src = torch.randint(0, 1000, (1 << 29,), dtype=torch.int16, device=q.device)  # 1 GiB
         dst = torch.empty_like(src)
         fns["copy"] = lambda: dst.copy_(src)
+    if args.only == "convert":
+        src = torch.randn(1 << 28, dtype=torch.float32, device=q.device)  # 1 GiB read
+        dst = torch.empty(1 << 28, dtype=torch.bfloat16, device=q.device)  # 512 MiB written
+        fns["convert"] = lambda: dst.copy_(src)
     fn = fns[args.only]
     for _ in range(args.warmup):
         fn()

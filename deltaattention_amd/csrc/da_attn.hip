@@ -482,6 +482,14 @@ void attn_kernel_pure(AttnArgs a) {
   attn_body<kPure, DT>(a);
 }
 
+// min(max(x, 0), hi) for a wave-uniform x, kept in scalar registers (the compiler would
+// otherwise form a clamp that only exists as a vector instruction, v_med3).
+__device__ __forceinline__ int clamp0_uniform(int x, int hi) {
+  x = __builtin_amdgcn_readfirstlane(x < hi ? x : hi);
+  asm volatile("" : "+s"(x));
+  return x > 0 ? x : 0;
+}
+
 // Third dword of a raw buffer resource on gfx9 (32-bit data format, no swizzle).
 constexpr int kBufferDword3 = 0x00020000;
 
@@ -697,7 +705,14 @@ void attn_w64_kernel(AttnArgs a) {
   constexpr bool kWeights = VARIANT == kHybrid || VARIANT == kPure;
 
   auto key0_of = [&](int t) { return t < n1 ? t * kWTK : ds + (t - n1) * kWTK; };
-  auto skipped = [&](int t) { return t >= n1 && a.causal && key0_of(t) > r0w + 63; };
+  // causal: a Phase-2 tile whose first key is past the wave's last row (r0w + 63) is
+  // skipped; tiles n1 + (r0w + 63 - ds) / 32 + 1 onwards are
+  int t_skip = INT_MAX;
+  if (a.causal) {
+    const int d = r0w + 63 - ds;
+    t_skip = __builtin_amdgcn_readfirstlane(d < 0 ? n1 : n1 + d / kWTK + 1);
+  }
+  auto skipped = [&](int t) { return t >= t_skip; };
 
   // ---- staging: loads straight into LDS, three stages each for K and V and a ring of
   // four slots for the tiles' weights.  Wave w loads rows 4w .. 4w + 3 of both tiles:
@@ -724,15 +739,16 @@ void attn_w64_kernel(AttnArgs a) {
     const int snb = isK ? (ph1 ? skpb : skb) : (ph1 ? svpb : svb);
     const char* src = isK ? (ph1 ? kb1 : kb2) : (ph1 ? vb1 : vb2);
     const void* base = uniform_ptr(src + (int64_t)key0 * snb);
-    const int nrows = max(0, min(limit - key0, kWTK));
-    const int range = __builtin_amdgcn_readfirstlane(nrows * snb);
+    const int range = clamp0_uniform(limit - key0, kWTK) * snb;
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<void*>(base), (short)0, range, kBufferDword3);
-    char* dst = isK ? kst0 + (t_raw % 3) * kWKBytes : vst0 + (t_raw % 3) * kWVBytes;
+    char* dst = isK ? kst0 + ((unsigned)t_raw % 3u) * kWKBytes : vst0 + ((unsigned)t_raw % 3u) * kWVBytes;
     const int rowt = wid_s * 4 + (lane >> 4);
     const int pos = lane & 15;
     const int chunk = pos ^ (isK ? (rowt & 15) : 4 * (rowt & 3));
-    const int off = chunk * 8 < a.D ? rowt * snb + chunk * 16 : range;
+    // rowt < 32 and snb < 2^24 (the host limits sequence strides to 2^23 elements); a
+    // chunk at or past the head dimension reads past the range (zeros), without a branch
+    const int off = __mul24(rowt, snb) + chunk * 16 + (chunk * 8 < a.D ? 0 : range);
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)(dst + wid_s * 1024), 16,
                                              off, 0, 0, 0);
   };
@@ -745,17 +761,16 @@ void attn_w64_kernel(AttnArgs a) {
     const int t = min(t_raw, T - 1);
     const bool ph1 = t < n1;
     const int key0 = ph1 ? t * kWTK : 0;
-    const int nrows = ph1 ? max(0, min(a.wcap - key0, kWTK)) : kWTK;
+    const int nrows = ph1 ? clamp0_uniform(a.wcap - key0, kWTK) : kWTK;
     char* dst = meta_of(t_raw);
     const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<void*>(uniform_ptr(ph1 ? w_row + key0 : a.zeros)), (short)0,
-        __builtin_amdgcn_readfirstlane(nrows * 4), kBufferDword3);
+        nrows * 4, kBufferDword3);
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rc, (__attribute__((address_space(3))) void*)(dst + kWCnt), 4,
                                              lane * 4, 0, 0, 0);
     if (kPureV) {
       const __amdgpu_buffer_rsrc_t rt = __builtin_amdgcn_make_buffer_rsrc(
-          const_cast<void*>(uniform_ptr(tsw_row + key0)), (short)0, __builtin_amdgcn_readfirstlane(nrows * 4),
-          kBufferDword3);
+          const_cast<void*>(uniform_ptr(tsw_row + key0)), (short)0, nrows * 4, kBufferDword3);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rt, (__attribute__((address_space(3))) void*)(dst + kWTs), 4,
                                                lane * 4, 0, 0, 0);
     }
@@ -881,7 +896,7 @@ void attn_w64_kernel(AttnArgs a) {
           };
           uint32_t va[4] = {0, 0, 0, 0};
           if constexpr (PV) {
-            const uint32_t vb = lds_addr(vst0) + ((t - 1) % 3) * kWVBytes;
+            const uint32_t vb = lds_addr(vst0) + ((unsigned)(t - 1) % 3u) * kWVBytes;
             // opaque: otherwise the offsets are hoisted out of the loop into registers
             asm volatile("" : "+v"(v_lane), "+v"(v_q));
 #pragma unroll
@@ -897,7 +912,7 @@ void attn_w64_kernel(AttnArgs a) {
             // is (base + klo + kx) ^ (32 j): one XOR per read.
             kx = (k_swz & 14) << 4;
             const int klo = k_row + (((hl ^ k_swz) & 1) << 4) + kx;
-            kla = lds_addr(kst0 + (t % 3) * kWKBytes) + klo;
+            kla = lds_addr(kst0 + ((unsigned)t % 3u) * kWKBytes) + klo;
             qla = lds_addr(qs) + klo;
             bla = lds_addr(meta_of(t) + kWCnt) + 16 * hl;
           }
@@ -1292,8 +1307,8 @@ static int fill_common(AttnArgs& a, const void* q, const void* k, const void* v,
     DA_REQUIRE((st[i] & 7) == 0, "%s: strides must be multiples of 8 elements (stride %d = %lld)", who, i, (long long)st[i]);
   DA_REQUIRE(aligned16(q) && aligned16(k) && aligned16(v) && aligned16(out), "%s: tensors must be 16-byte aligned", who);
   for (int i : {DA_STRIDE_K + 2, DA_STRIDE_V + 2})
-    DA_REQUIRE(st[i] >= D && st[i] < (1ll << 24),
-               "%s: key/value sequence strides must be in [head_dim, 2^24) (stride %d = %lld)", who, i, (long long)st[i]);
+    DA_REQUIRE(st[i] >= D && st[i] < (1ll << 23),
+               "%s: key/value sequence strides must be in [head_dim, 2^23) (stride %d = %lld)", who, i, (long long)st[i]);
   a.q = (const uint16_t*)q; a.k = (const uint16_t*)k; a.v = (const uint16_t*)v; a.out = (uint16_t*)out;
   a.sq_b = st[DA_STRIDE_Q]; a.sq_h = st[DA_STRIDE_Q + 1]; a.sq_n = st[DA_STRIDE_Q + 2];
   a.sk_b = st[DA_STRIDE_K]; a.sk_h = st[DA_STRIDE_K + 1]; a.sk_n = st[DA_STRIDE_K + 2];
@@ -1358,8 +1373,8 @@ static int hybrid_impl(const char* who, AttnArgs& a, const void* k_packed, const
   DA_REQUIRE(window >= 0 && window < (1ll << 30), "%s: window must be >= 0", who);
   DA_REQUIRE(aligned16(k_packed) && aligned16(v_packed), "%s: packed tensors must be 16-byte aligned", who);
   for (int i : {DA_STRIDE_KP + 2, DA_STRIDE_VP + 2})
-    DA_REQUIRE(strides[i] >= a.D && strides[i] < (1ll << 24),
-               "%s: packed sequence strides must be in [head_dim, 2^24) (stride %d = %lld)", who, i,
+    DA_REQUIRE(strides[i] >= a.D && strides[i] < (1ll << 23),
+               "%s: packed sequence strides must be in [head_dim, 2^23) (stride %d = %lld)", who, i,
                (long long)strides[i]);
   DA_REQUIRE(strides[DA_STRIDE_TS + 2] == 1 && strides[DA_STRIDE_CNT + 2] == 1,
              "%s: timestamps and counts must be contiguous along the packed axis", who);

@@ -267,7 +267,7 @@ int da_decode_attention_noalloc(const void* q, int dtype, int64_t B, int64_t Hq,
  * strides for da_hybrid_prefill / da_dense_prefill: int64[3 * 8] element strides
  * (batch, head, sequence) of, in order: q, k, v, k_packed, v_packed, out,
  * timestamps (sequence stride must be 1), counts (sequence stride must be 1).
- * The sequence strides of k, v, k_packed and v_packed must lie in [D, 2^24): key and
+ * The sequence strides of k, v, k_packed and v_packed must lie in [D, 2^23): key and
  * value rows may not overlap.  da_dense_prefill reads the q, k, v and out triples only.
  */
 #define DA_STRIDE_Q 0
