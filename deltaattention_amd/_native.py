@@ -51,7 +51,25 @@ SIGNATURES = {
     "da_decode_attention_noalloc": (_I, [_P, _I, _L, _L, _L, _L, _L, _L, _P, _P, _L, _L, _L, _P, _L,
                                          _L, _P, _L, _P, _P, _L, _L, _L, _L, _L, _F, _P, _L, _L,
                                          _P]),
+    "da_decode_step": (_I, [_P, _P]),
 }
+
+
+class DecodeStep(ctypes.Structure):
+    """struct DaDecodeStep of include/deltaattn.h (field for field)."""
+    _fields_ = [
+        ("new_k", _P), ("new_v", _P), ("sn_b", _L), ("sn_h", _L),
+        ("q", _P), ("sq_b", _L), ("sq_h", _L),
+        ("out", _P), ("so_b", _L), ("so_h", _L),
+        ("k_exact", _P), ("v_exact", _P), ("sx_b", _L), ("sx_h", _L), ("sx_s", _L),
+        ("k_packed", _P), ("v_packed", _P), ("sp_b", _L), ("sp_h", _L), ("sp_s", _L),
+        ("counts", _P), ("timestamps", _P), ("sc_b", _L), ("sc_h", _L),
+        ("lengths", _P), ("capacity", _L),
+        ("exact_seq_len", _L), ("total_seq_len", _L), ("window", _L),
+        ("threshold", _F), ("use_cosine", ctypes.c_int32), ("scale", _F), ("dtype", ctypes.c_int32),
+        ("B", _L), ("Hq", _L), ("Hkv", _L), ("D", _L),
+        ("workspace", _P), ("workspace_bytes", _L),
+    ]
 
 DA_DECODE_SCRATCH_BYTES = 32 << 20
 

@@ -363,23 +363,23 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeAttnArgs a) {
 
 using namespace da;
 
-extern "C" int da_decode_update(const void* new_k, const void* new_v, int dtype, int64_t B,
-                                int64_t Hkv, int64_t D, int64_t sn_b, int64_t sn_h, void* k_exact,
-                                void* v_exact, int64_t sx_b, int64_t sx_h, int64_t sx_s,
-                                void* k_packed, void* v_packed, int64_t sp_b, int64_t sp_h,
-                                int64_t sp_s, int32_t* counts, int32_t* timestamps, int64_t sc_b,
-                                int64_t sc_h, int32_t* lengths, int64_t capacity,
-                                int64_t exact_seq_len, int64_t total_seq_len, int64_t window,
-                                float threshold, int use_cosine, void* stream) {
+// Checks and launch of the cache update, shared by da_decode_update and da_decode_step.
+static int decode_update_impl(const void* new_k, const void* new_v, int dtype, int64_t B, int64_t Hkv, int64_t D,
+                              int64_t sn_b, int64_t sn_h, void* k_exact, void* v_exact, int64_t sx_b,
+                              int64_t sx_h, int64_t sx_s, void* k_packed, void* v_packed, int64_t sp_b,
+                              int64_t sp_h, int64_t sp_s, int32_t* counts, int32_t* timestamps, int64_t sc_b,
+                              int64_t sc_h, int32_t* lengths, int64_t capacity, int64_t exact_seq_len,
+                              int64_t total_seq_len, int64_t window, float threshold, int use_cosine,
+                              void* stream, const char* who) {
   DA_REQUIRE(new_k && new_v && k_exact && v_exact && k_packed && v_packed && counts && timestamps && lengths,
-             "da_decode_update: null pointer");
+             "%s: null pointer", who);
   if (dtype != DA_BF16 && dtype != DA_F16)
-    return set_error(DA_ERR_UNSUPPORTED, "da_decode_update: the cache must be bf16 or fp16");
-  DA_REQUIRE(B > 0 && Hkv > 0 && window > 0 && capacity > 0, "da_decode_update: empty shape");
-  if (D > 128 || (D & 1)) return set_error(DA_ERR_UNSUPPORTED, "da_decode_update: head_dim must be even and <= 128");
-  DA_REQUIRE(exact_seq_len >= 0 && total_seq_len >= 0, "da_decode_update: negative lengths");
+    return set_error(DA_ERR_UNSUPPORTED, "%s: the cache must be bf16 or fp16", who);
+  DA_REQUIRE(B > 0 && Hkv > 0 && window > 0 && capacity > 0, "%s: empty shape", who);
+  if (D > 128 || (D & 1)) return set_error(DA_ERR_UNSUPPORTED, "%s: head_dim must be even and <= 128", who);
+  DA_REQUIRE(exact_seq_len >= 0 && total_seq_len >= 0, "%s: negative lengths", who);
   DA_REQUIRE(((sn_b | sn_h | sx_b | sx_h | sx_s | sp_b | sp_h | sp_s) & 1) == 0,
-             "da_decode_update: rows must be 4-byte aligned");
+             "%s: rows must be 4-byte aligned", who);
   DecodeUpdateArgs a = {};
   a.new_k = (const uint16_t*)new_k; a.new_v = (const uint16_t*)new_v; a.sn_b = sn_b; a.sn_h = sn_h;
   a.kx = (uint16_t*)k_exact; a.vx = (uint16_t*)v_exact; a.sx_b = sx_b; a.sx_h = sx_h; a.sx_s = sx_s;
@@ -396,7 +396,21 @@ extern "C" int da_decode_update(const void* new_k, const void* new_v, int dtype,
     if (use_cosine) hipLaunchKernelGGL((decode_update_kernel<true, DA_BF16>), dim3(blocks), dim3(256), 0, st, a);
     else hipLaunchKernelGGL((decode_update_kernel<false, DA_BF16>), dim3(blocks), dim3(256), 0, st, a);
   }
-  return check_launch("da_decode_update");
+  return check_launch(who);
+}
+
+extern "C" int da_decode_update(const void* new_k, const void* new_v, int dtype, int64_t B,
+                                int64_t Hkv, int64_t D, int64_t sn_b, int64_t sn_h, void* k_exact,
+                                void* v_exact, int64_t sx_b, int64_t sx_h, int64_t sx_s,
+                                void* k_packed, void* v_packed, int64_t sp_b, int64_t sp_h,
+                                int64_t sp_s, int32_t* counts, int32_t* timestamps, int64_t sc_b,
+                                int64_t sc_h, int32_t* lengths, int64_t capacity,
+                                int64_t exact_seq_len, int64_t total_seq_len, int64_t window,
+                                float threshold, int use_cosine, void* stream) {
+  return decode_update_impl(new_k, new_v, dtype, B, Hkv, D, sn_b, sn_h, k_exact, v_exact, sx_b, sx_h, sx_s,
+                            k_packed, v_packed, sp_b, sp_h, sp_s, counts, timestamps, sc_b, sc_h, lengths,
+                            capacity, exact_seq_len, total_seq_len, window, threshold, use_cosine, stream,
+                            "da_decode_update");
 }
 
 template <int DT>
@@ -487,6 +501,31 @@ extern "C" int da_decode_attention(const void* q, int dtype, int64_t B, int64_t 
   return decode_attention_impl(q, dtype, B, Hq, Hkv, sq_b, sq_h, k_packed, v_packed, sp_b, sp_h, sp_s, counts,
                                sc_b, sc_h, lengths, capacity, k_exact, v_exact, sx_b, sx_h, sx_s, window,
                                exact_len, scale, out, so_b, so_h, (float*)workspace, (hipStream_t)stream);
+}
+
+// One decode token in one call: the cache update, then the attention over the updated
+// cache (its ring holds min(exact_seq_len + 1, window) tokens).
+extern "C" int da_decode_step(const DaDecodeStep* s, void* stream) {
+  const char* who = "da_decode_step";
+  DA_REQUIRE(s, "%s: null argument block", who);
+  const int64_t exact_len = s->exact_seq_len + 1 < s->window ? s->exact_seq_len + 1 : s->window;
+  if (int rc = decode_attention_check(s->q, s->dtype, s->B, s->Hq, s->Hkv, s->D, s->k_packed, s->v_packed, s->sp_b,
+                                      s->sp_h, s->sp_s, s->counts, s->lengths, s->capacity, s->k_exact,
+                                      s->v_exact, s->sx_b, s->sx_h, s->sx_s, s->window, exact_len, s->out, who))
+    return rc;
+  const int64_t need = da_decode_workspace_size(s->B, s->Hq, s->capacity, s->window);
+  if (!s->workspace || s->workspace_bytes < need)
+    return set_error(DA_ERR_WORKSPACE, "%s: workspace of %lld bytes required", who, (long long)need);
+  if (int rc = decode_update_impl(s->new_k, s->new_v, s->dtype, s->B, s->Hkv, s->D, s->sn_b, s->sn_h, s->k_exact,
+                                  s->v_exact, s->sx_b, s->sx_h, s->sx_s, s->k_packed, s->v_packed, s->sp_b,
+                                  s->sp_h, s->sp_s, s->counts, s->timestamps, s->sc_b, s->sc_h, s->lengths,
+                                  s->capacity, s->exact_seq_len, s->total_seq_len, s->window, s->threshold,
+                                  s->use_cosine, stream, who))
+    return rc;
+  return decode_attention_impl(s->q, s->dtype, s->B, s->Hq, s->Hkv, s->sq_b, s->sq_h, s->k_packed, s->v_packed,
+                               s->sp_b, s->sp_h, s->sp_s, s->counts, s->sc_b, s->sc_h, s->lengths, s->capacity,
+                               s->k_exact, s->v_exact, s->sx_b, s->sx_h, s->sx_s, s->window, exact_len, s->scale,
+                               s->out, s->so_b, s->so_h, (float*)s->workspace, (hipStream_t)stream);
 }
 
 // ------------------------------------------------------------------------------------

@@ -16,7 +16,7 @@ import torch
 
 from . import globVR
 from ._launch import HALF, KernelLauncher, tensor, unit_stride
-from ._native import check, dtype_code, lib
+from ._native import DecodeStep, check, dtype_code, lib
 
 try:  # transformers' Cache base (the reference subclasses it, deltaDecoding.py:2, 111)
     from transformers import Cache as _CacheBase
@@ -29,6 +29,14 @@ __all__ = ["HybridCompressedCache", "fused_hybrid_decode_update_kernel",
 
 def _stream():
     return ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+
+def _raw_stream(device: torch.device) -> int:
+    """The current stream's handle without building a torch Stream object."""
+    get = getattr(torch._C, "_cuda_getCurrentRawStream", None)
+    if get is None:  # pragma: no cover - older torch
+        return torch.cuda.current_stream(device).cuda_stream
+    return get(device.index if device.index is not None else torch.cuda.current_device())
 
 
 def _metric_threshold():
@@ -175,6 +183,7 @@ class HybridCompressedCache(_CacheBase):
         self.exact_seq_lens = [0 for _ in range(L)]
         self.max_packed_len = [0 for _ in range(L)]
         self.total_seq_lens = [0 for _ in range(L)]
+        self._plans = {}  # layer -> (DaDecodeStep block, workspace) for decode_step
 
     def _expand_capacity(self, target_capacity):
         """Grow to max(2 * capacity, target) keeping contents (deltaDecoding.py:138-157)."""
@@ -193,6 +202,7 @@ class HybridCompressedCache(_CacheBase):
         self.k_packed, self.v_packed = new_k, new_v
         self.packed_counts, self.packed_timestamps = new_c, new_t
         self.capacity = new_capacity
+        self._plans = {}
 
     def initialize_from_prefill(self, layer_idx, k_packed, v_packed, counts, timestamps, k_exact,
                                 v_exact, original_q_len):
@@ -245,6 +255,78 @@ class HybridCompressedCache(_CacheBase):
         self.exact_seq_lens[layer_idx] += 1
         self.total_seq_lens[layer_idx] += 1
         return key_states, value_states
+
+    def _plan(self, layer_idx, Hq):
+        """The layer's DaDecodeStep block with the cache fields filled in, and its
+        workspace; rebuilt when the capacity grows (the tensors move)."""
+        plan = self._plans.get((layer_idx, Hq))
+        if plan is not None:
+            return plan
+        st = DecodeStep()
+        kp, vp = self.k_packed[layer_idx], self.v_packed[layer_idx]
+        kx, vx = self.k_exact[layer_idx], self.v_exact[layer_idx]
+        cnt, ts = self.packed_counts[layer_idx], self.packed_timestamps[layer_idx]
+        st.k_exact, st.v_exact = kx.data_ptr(), vx.data_ptr()
+        st.sx_b, st.sx_h, st.sx_s = kx.stride(0), kx.stride(1), kx.stride(2)
+        st.k_packed, st.v_packed = kp.data_ptr(), vp.data_ptr()
+        st.sp_b, st.sp_h, st.sp_s = kp.stride(0), kp.stride(1), kp.stride(2)
+        st.counts, st.timestamps = cnt.data_ptr(), ts.data_ptr()
+        st.sc_b, st.sc_h = cnt.stride(0), cnt.stride(1)
+        st.lengths = self.packed_lengths[layer_idx].data_ptr()
+        st.capacity = self.capacity
+        st.window = self.exact_window_size
+        st.dtype = dtype_code(kp, vp, kx, vx)
+        st.B, st.Hq, st.Hkv, st.D = self.bsz, Hq, self.n_kv_heads, self.head_dim
+        ws_bytes = lib().da_decode_workspace_size(self.bsz, Hq, self.capacity, self.exact_window_size)
+        ws = torch.empty((max(1, ws_bytes),), dtype=torch.uint8, device=self.device)
+        st.workspace, st.workspace_bytes = ws.data_ptr(), ws_bytes
+        plan = (st, ws, ctypes.byref(st))
+        self._plans[(layer_idx, Hq)] = plan
+        return plan
+
+    def decode_step(self, query_states, key_states, value_states, layer_idx, scaling=None):
+        """One decode token of one layer in one library call: ``update`` and
+        ``decode_attention`` (modeling_llama.py:565-567 then :453-518) fused into
+        ``da_decode_step``, with the layer's argument block built once.  q [B, Hq, 1, D],
+        key/value [B, Hkv, 1, D] -> [B, Hq, 1, D]; results and cache state are those of
+        the two calls in sequence."""
+        if self.max_packed_len[layer_idx] + 1 >= self.capacity:
+            self._expand_capacity(self.capacity + 1024)
+        B, Hq, _, D = query_states.shape
+        want = (self.bsz, self.n_kv_heads, 1, self.head_dim)
+        if (B, D) != (self.bsz, self.head_dim) or query_states.shape[2] != 1 \
+                or tuple(key_states.shape) != want or tuple(value_states.shape) != want:
+            raise ValueError(f"decode_step: expected q [{self.bsz}, Hq, 1, {self.head_dim}] and "
+                             f"key/value {list(want)}, got {list(query_states.shape)}, "
+                             f"{list(key_states.shape)}, {list(value_states.shape)}")
+        st, ws, ref = self._plan(layer_idx, Hq)
+        q = query_states.squeeze(2)
+        if q.stride(-1) != 1:
+            q = q.contiguous()
+        k = key_states if key_states.stride(-1) == 1 else key_states.contiguous()
+        v = value_states if value_states.stride(-1) == 1 else value_states.contiguous()
+        if k.stride()[:2] != v.stride()[:2]:
+            k, v = k.contiguous(), v.contiguous()
+        if dtype_code(q, k, v) != st.dtype:
+            raise TypeError("decode_step: query, key and value must have the cache's dtype")
+        out = torch.empty((B, Hq, D), dtype=q.dtype, device=q.device)
+        threshold, use_cos = _metric_threshold()
+        st.new_k, st.new_v, st.sn_b, st.sn_h = k.data_ptr(), v.data_ptr(), k.stride(0), k.stride(1)
+        st.q, st.sq_b, st.sq_h = q.data_ptr(), q.stride(0), q.stride(1)
+        st.out, st.so_b, st.so_h = out.data_ptr(), out.stride(0), out.stride(1)
+        st.exact_seq_len = self.exact_seq_lens[layer_idx]
+        st.total_seq_len = self.total_seq_lens[layer_idx]
+        st.threshold = float(threshold)
+        st.use_cosine = 1 if use_cos else 0
+        st.scale = D ** -0.5 if scaling is None else float(scaling)
+        check(lib().da_decode_step(ref, _raw_stream(q.device)), "HybridCompressedCache.decode_step")
+        if self.exact_seq_lens[layer_idx] >= self.exact_window_size:
+            self.max_packed_len[layer_idx] += 1
+            if self.total_seq_lens[layer_idx] % 256 == 0:  # reconcile with the device (:219-221)
+                self.max_packed_len[layer_idx] = int(self.packed_lengths[layer_idx].max().item())
+        self.exact_seq_lens[layer_idx] += 1
+        self.total_seq_lens[layer_idx] += 1
+        return out.unsqueeze(2)
 
     def get_seq_length(self, layer_idx: int = 0) -> int:
         return self.total_seq_lens[layer_idx]

@@ -180,16 +180,23 @@ def delta_llama_attention_forward(self, hidden_states: torch.Tensor,
         if cache.get_seq_length(self.layer_idx) == 0:
             raise RuntimeError("compressed decode needs a prefill hand-off first: this layer's "
                                "HybridCompressedCache is empty")
-        ev = timing.start_event()
-        cache.update(key_states, value_states, self.layer_idx)       # :565-567
-        timing.stop_event("time_delta_decode_cache_update", ev)
-        if self.layer_idx == 0:
-            _kv_size_sample(cache)
-        ev_dec = timing.start_event()
-        out = deltaDecoding.decode_attention(query_states, cache, self.layer_idx,
-                                             scaling=self.scaling)  # [B, Hq, 1, D]
-        timing.stop_event("time_delta_decode_attn_calc", ev_dec)
-        timing.stop_event("time_delta_decode_inner_total", ev_dec)
+        if not timing.enabled():
+            # update (:565-567) and the decode attention (:453-518) in one library call
+            out = cache.decode_step(query_states, key_states, value_states, self.layer_idx,
+                                    scaling=self.scaling)            # [B, Hq, 1, D]
+            if self.layer_idx == 0:
+                _kv_size_sample(cache)
+        else:
+            ev = timing.start_event()
+            cache.update(key_states, value_states, self.layer_idx)   # :565-567
+            timing.stop_event("time_delta_decode_cache_update", ev)
+            if self.layer_idx == 0:
+                _kv_size_sample(cache)
+            ev_dec = timing.start_event()
+            out = deltaDecoding.decode_attention(query_states, cache, self.layer_idx,
+                                                 scaling=self.scaling)  # [B, Hq, 1, D]
+            timing.stop_event("time_delta_decode_attn_calc", ev_dec)
+            timing.stop_event("time_delta_decode_inner_total", ev_dec)
         attn_output = out.transpose(1, 2)
 
     attn_output = attn_output.reshape(*input_shape, -1).contiguous()

@@ -242,6 +242,49 @@ int da_decode_attention(const void* q, int dtype, int64_t B, int64_t Hq, int64_t
                         void* stream);
 
 /*
+ * One decode token in one call: da_decode_update, then da_decode_attention over the
+ * updated cache (exact_len = min(exact_seq_len + 1, window)).  No counterpart in the
+ * reference, which runs the two kernels from its cache object and attention wrapper
+ * (deltaDecoding.py:181-233, modeling_llama.py:453-518): it is for callers whose host
+ * path per token matters (token-by-token decode, one call per layer instead of two,
+ * with every argument in one block the caller fills once per layer and updates per
+ * token).  Fields mean what the same-named arguments of the two entries above mean;
+ * the checks are theirs (D = 128 for the attention).  Results are bit-identical to the
+ * two calls in sequence.
+ */
+typedef struct DaDecodeStep {
+  /* this token */
+  const void* new_k;   /* [B, Hkv, 1, D] */
+  const void* new_v;
+  int64_t sn_b, sn_h;
+  const void* q;       /* [B, Hq, D] */
+  int64_t sq_b, sq_h;
+  void* out;           /* [B, Hq, D] */
+  int64_t so_b, so_h;
+  /* one layer of the cache */
+  void* k_exact;       /* [B, Hkv, W, D] */
+  void* v_exact;
+  int64_t sx_b, sx_h, sx_s;
+  void* k_packed;      /* [B, Hkv, capacity, D] */
+  void* v_packed;
+  int64_t sp_b, sp_h, sp_s;
+  int32_t* counts;     /* [B, Hkv, capacity] */
+  int32_t* timestamps;
+  int64_t sc_b, sc_h;
+  int32_t* lengths;    /* [B * Hkv] */
+  int64_t capacity;
+  int64_t exact_seq_len, total_seq_len, window;  /* host trackers before this token */
+  float threshold;
+  int32_t use_cosine;
+  float scale;
+  int32_t dtype;
+  int64_t B, Hq, Hkv, D;
+  void* workspace;     /* da_decode_workspace_size(B, Hq, capacity, window) bytes */
+  int64_t workspace_bytes;
+} DaDecodeStep;
+int da_decode_step(const DaDecodeStep* step, void* stream);
+
+/*
  * da_decode_attention without a workspace and without any allocation.  No counterpart
  * in the reference: it is for callers that cannot allocate device memory (code under
  * HIP graph capture, serving loops, harnesses that forbid hipMalloc).  Arguments and

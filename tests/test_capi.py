@@ -25,7 +25,7 @@ def test_header_declares_the_expected_entry_points():
         "da_decode_update", "da_decode_workspace_size", "da_decode_attention",
         "da_decode_attention_noalloc", "da_select_varlen", "da_pack_varlen_workspace_size",
         "da_pack_varlen", "da_hybrid_varlen_workspace_size", "da_hybrid_prefill_varlen",
-        "da_dense_prefill_varlen"])
+        "da_dense_prefill_varlen", "da_decode_step"])
 
 
 def test_library_exports_every_declared_symbol():
@@ -165,3 +165,28 @@ def test_ops_refuse_cpu_tensors():
         ops.select(k, 1.0)
     with pytest.raises(ValueError, match="no CPU path"):
         ops.dense_prefill(k, k, k)
+
+
+def test_decode_step_block_matches_header_and_checks_workspace():
+    """The ctypes DecodeStep mirrors DaDecodeStep field for field, and the entry point
+    reads the block at those offsets: a valid block with no workspace is refused with
+    DA_ERR_WORKSPACE before anything is launched."""
+    text = open(HEADER).read()
+    body = re.search(r"typedef struct DaDecodeStep \{(.*?)\} DaDecodeStep;", text, re.S).group(1)
+    body = re.sub(r"/\*.*?\*/", "", body, flags=re.S)
+    names = re.findall(r"\**\s*(\w+)\s*[,;]", body)
+    assert names == [f for f, _ in _native.DecodeStep._fields_]
+    lib = _native.lib()
+    assert lib.da_decode_step(None, None) == -1 and "null" in _err()
+    a = 1 << 20
+    D, cap, W, Hq, Hkv = 128, 64, 16, 32, 8
+    st = _native.DecodeStep(
+        new_k=a, new_v=a, sn_b=Hkv * D, sn_h=D, q=a, sq_b=Hq * D, sq_h=D, out=a, so_b=Hq * D,
+        so_h=D, k_exact=a, v_exact=a, sx_b=Hkv * W * D, sx_h=W * D, sx_s=D, k_packed=a,
+        v_packed=a, sp_b=Hkv * cap * D, sp_h=cap * D, sp_s=D,
+        counts=a, timestamps=a, sc_b=Hkv * cap, sc_h=cap, lengths=a, capacity=cap, exact_seq_len=3,
+        total_seq_len=3, window=W, threshold=1.0, use_cosine=0, scale=0.088, dtype=_native.DA_BF16, B=1,
+        Hq=Hq, Hkv=Hkv, D=D, workspace=None, workspace_bytes=0)
+    assert lib.da_decode_step(ctypes.byref(st), None) == -4 and "workspace" in _err()
+    st.Hq = 30    # not a multiple of Hkv: the attention checks run first
+    assert lib.da_decode_step(ctypes.byref(st), None) == -1

@@ -220,6 +220,50 @@ def test_decode_cache_matches_oracle(gpu, metric, tau, dtype):
             setattr(globVR, name, val)
 
 
+@pytest.mark.parametrize("metric,tau", [("euclidean", 9.5), ("cosine", 0.9)])
+def test_decode_step_equals_update_then_attention(gpu, metric, tau):
+    """HybridCompressedCache.decode_step (one da_decode_step call per token) against
+    cache.update + decode_attention on a twin cache: every step's output and the final
+    cache state bit-identical, through ring fill, eviction into the packed cache and a
+    capacity growth (initial capacity 8) that rebuilds the cached argument block."""
+    from types import SimpleNamespace
+    from deltaattention_amd import globVR
+    from deltaattention_amd.deltaDecoding import HybridCompressedCache, decode_attention
+    B, Hq, Hkv, W, steps = 2, 8, 2, 16, 96
+    q, k, v = _inputs(B, Hq, Hkv, steps, 11)
+    cfg = SimpleNamespace(hidden_size=Hq * 128, num_attention_heads=Hq, num_key_value_heads=Hkv,
+                          num_hidden_layers=2, head_dim=128)
+    saved = dict(vars(globVR))
+    try:
+        globVR.row_delta_threshold, globVR.row_similarity_metric = tau, metric
+        a = HybridCompressedCache(cfg, B, dtype=torch.bfloat16, exact_window_size=W,
+                                  initial_capacity=8)
+        b = HybridCompressedCache(cfg, B, dtype=torch.bfloat16, exact_window_size=W,
+                                  initial_capacity=8)
+        qg, kg, vg = q.to(gpu), k.to(gpu), v.to(gpu)
+        announce(f"decode_step {metric}: {steps} steps on layer 1, B={B} Hq={Hq} Hkv={Hkv} W={W}")
+        for t in range(steps):
+            qt, kt, vt = qg[:, :, t:t + 1], kg[:, :, t:t + 1], vg[:, :, t:t + 1]
+            a.update(kt, vt, 1)
+            want = decode_attention(qt, a, 1, scaling=0.07)
+            got = b.decode_step(qt, kt, vt, 1, scaling=0.07)
+            assert got.shape == want.shape == (B, Hq, 1, 128)
+            assert torch.equal(got, want), t
+        assert b.capacity == a.capacity > 8
+        assert (b.exact_seq_lens, b.total_seq_lens) == (a.exact_seq_lens, a.total_seq_lens)
+        n = int(a.packed_lengths[1].max().item())
+        assert 0 < n < B * Hkv * (steps - W)
+        for name in ("packed_lengths", "packed_counts", "packed_timestamps", "k_packed",
+                     "v_packed", "k_exact", "v_exact"):
+            assert torch.equal(getattr(a, name), getattr(b, name)), name
+        with pytest.raises(ValueError):
+            b.decode_step(qg[:, :, :1], kg[:, :1, :1], vg[:, :1, :1], 1)
+        print(f"decode_step {metric}: packed length {n} after {steps} tokens", flush=True)
+    finally:
+        for name, val in saved.items():
+            setattr(globVR, name, val)
+
+
 @pytest.mark.parametrize("B,Hq,Hkv,cap,W,exact,dtype", [
     (1, 32, 8, 40000, 128, 128, torch.bfloat16),   # dense-like length: 600+ slices per head
     (1, 32, 8, 40000, 128, 128, torch.float16),

@@ -102,10 +102,20 @@ def _spy_layer0(monkeypatch):
             rec["attn"].append((q.detach().clone(), out.detach().clone()))
         return out
 
+    real_step = HybridCompressedCache.decode_step
+
+    def step(self, q, k, v, layer_idx, scaling=None):
+        out = real_step(self, q, k, v, layer_idx, scaling=scaling)
+        if layer_idx == 0:
+            rec["kv"].append((k.detach().clone(), v.detach().clone()))
+            rec["attn"].append((q.detach().clone(), out.detach().clone()))
+        return out
+
     monkeypatch.setattr(attention, "delta_prefill_attention", prefill)
     monkeypatch.setattr(attention, "delta_decode_handoff", handoff)
     monkeypatch.setattr(HybridCompressedCache, "update", update)
     monkeypatch.setattr(deltaDecoding, "decode_attention", decode)
+    monkeypatch.setattr(HybridCompressedCache, "decode_step", step)
     return rec
 
 
@@ -120,14 +130,17 @@ def _assert_cache_equals(cache, st, what):
     assert np.array_equal(cache.v_exact[0].float().cpu().numpy(), st["v_exact"]), what
 
 
-@pytest.mark.parametrize("impl", ["deltaattention", "deltaattention_dense"], ids=["path1", "path2"])
-def test_model_prefill_then_decode_compressed_cache(gpu, monkeypatch, impl):
+@pytest.mark.parametrize("impl,timed", [("deltaattention", True), ("deltaattention_dense", True),
+                                        ("deltaattention", False)],
+                         ids=["path1", "path2", "path1-fused-step"])
+def test_model_prefill_then_decode_compressed_cache(gpu, monkeypatch, impl, timed):
     """A 2-layer Llama-3-8B-shaped model (hidden 4096, 32 query / 8 KV heads, head_dim
     128; vocab cut to 1024) prefills 2048 tokens into a HybridCompressedCache through
     llama_swap.install's forward and decodes 64 tokens one at a time.  PATH 1 hands its
     packed history to the cache (modeling_llama.py:761-773); PATH 2 packs after the dense
     prefill when delta_decode is set (:805-879); every later token runs PATH 3: update,
-    then the compressed decode attention (:565-567, :453-518, :883-897).  Layer 0 is
+    then the compressed decode attention (:565-567, :453-518, :883-897), as two calls
+    under stage timing and as one HybridCompressedCache.decode_step without.  Layer 0 is
     replayed in the oracle from the keys and queries it saw: the cache after the hand-off
     and after the last step is bit-exact, and every step's decode attention is within
     tolerance."""
@@ -142,7 +155,7 @@ def test_model_prefill_then_decode_compressed_cache(gpu, monkeypatch, impl):
     model = llama_swap.random_llama(cfg, gpu, seed=3)
     for name, val in (("packing_mode", "delta"), ("chunk_size", 512), ("row_delta_threshold", tau),
                       ("row_similarity_metric", "euclidean"), ("delta_decode", True),
-                      ("dense_window_size", 128), ("time_internal", True), ("kv_log_interval", 16),
+                      ("dense_window_size", 128), ("time_internal", timed), ("kv_log_interval", 16),
                       ("sanity", False), ("pure_phase1", False), ("no_count", False)):
         monkeypatch.setattr(globVR, name, val, raising=False)
     timing.reset()
@@ -181,10 +194,12 @@ def test_model_prefill_then_decode_compressed_cache(gpu, monkeypatch, impl):
     print(f"{impl}: {steps} steps, worst max-abs {worst:.3e}, packed length "
           f"{int(st['lengths'].max())}, appended {appended} of {8 * steps} evictions", flush=True)
     assert 0 < appended < 8 * steps     # the threshold both merges and appends
-    timing.resolve_latency_events()
-    stats = globVR.latency_stats
-    for key in ("time_prefill_forward_total", "time_decode_forward_total",
-                "time_delta_decode_cache_update", "time_delta_decode_attn_calc"):
-        assert stats.get(key, {}).get("calls", 0) > 0, key
+    assert len(rec["kv"]) == len(rec["attn"]) == steps
+    if timed:
+        timing.resolve_latency_events()
+        stats = globVR.latency_stats
+        for key in ("time_prefill_forward_total", "time_decode_forward_total",
+                    "time_delta_decode_cache_update", "time_delta_decode_attn_calc"):
+            assert stats.get(key, {}).get("calls", 0) > 0, key
     assert len(globVR.kv_compression_samples) >= steps // 16
     timing.reset()

@@ -69,7 +69,12 @@ def _stub(monkeypatch):
     monkeypatch.setattr(attention, "dense_prefill_attention", dense)
     monkeypatch.setattr(attention, "delta_decode_handoff", handoff)
     monkeypatch.setattr(HybridCompressedCache, "update", update)
+    def step(self, q, k, v, layer_idx, scaling=None):   # decode_step = update + attention
+        update(self, k, v, layer_idx)
+        return decode(q, self, layer_idx, scaling)
+
     monkeypatch.setattr(deltaDecoding, "decode_attention", decode)
+    monkeypatch.setattr(HybridCompressedCache, "decode_step", step)
     return calls
 
 
