@@ -71,6 +71,32 @@ def test_select_bitexact_config1_shape(gpu):
         assert (keep.cpu().numpy() == ok).all()
 
 
+@pytest.mark.parametrize("H,N,chunk,tau,metric,arith", [
+    (1, 3000, 1, 9.0, "euclidean", "fp32"),       # one-row chunks
+    (2, 3000, 33, 9.0, "euclidean", "fp32"),      # a one-row last batch
+    (2, 3000, 512, 1e6, "euclidean", "fp32"),     # one anchor per chunk
+    (2, 3000, 512, 0.999, "cosine", "fp32"),      # nearly every row kept
+    (2, 5000, 8193, 9.0, "euclidean", "fp32"),
+    (1, 20000, 10000, 9.0, "euclidean", "fp32"),
+    (8, 32768, 256, 10.3, "euclidean", "fp32"),   # 1024 chunks
+    (8, 32768, 128, 0.9, "cosine", "fp32"),       # 2048 chunks
+    (8, 32768, 256, 10.3, "euclidean", "native"),
+])
+def test_select_chunk_shapes(gpu, H, N, chunk, tau, metric, arith):
+    """Selection against the sequential oracle over chunk lengths from 1 to 10000 rows,
+    grids of 2 to 2048 chunks and thresholds that keep one row per chunk or nearly
+    every row."""
+    from deltaattention_amd import ops, synth
+    k = synth.make_layer_inputs(1, H, H, N, 128, seed=21, rope_base=500000.0)[1]
+    announce(f"select H={H} N={N} chunk={chunk} tau={tau} {metric} {arith}")
+    keep, cc = ops.select(k.to(gpu), tau, chunk, 0, metric, arith=arith)
+    ok, occ = OC.select_delta(k.float().numpy(), tau, chunk, 0, metric,
+                              arith="bf16" if arith == "native" else "fp32")
+    assert np.array_equal(cc.cpu().numpy(), occ), "chunk counts differ"
+    keep_h = keep.cpu().numpy()
+    assert np.array_equal(keep_h, ok), f"keep differs at {np.argwhere(keep_h != ok)[:5]}"
+
+
 @pytest.mark.parametrize("dtype,oracle_arith", [(torch.bfloat16, "bf16"), (torch.float16, "fp16")])
 def test_select_native_arith_bitexact(gpu, dtype, oracle_arith):
     """arith="native": the Euclidean distance in the keys' 16-bit arithmetic, bit-exact
