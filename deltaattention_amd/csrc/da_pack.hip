@@ -163,6 +163,9 @@ struct PackOut {
   int64_t capacity;  // fixed batch
 };
 
+// VEC: K, V and the packed rows are 16-byte aligned with D a multiple of 8, and each
+// anchor row moves as 16-byte chunks, four rows per load instruction.
+template <bool VEC>
 __global__ __launch_bounds__(256) void pack_scatter_kernel(
     const int32_t* __restrict__ keep, const uint16_t* __restrict__ k,
     const uint16_t* __restrict__ v, int64_t sk_b, int64_t sk_h, int64_t sk_n, int64_t sv_b,
@@ -170,6 +173,7 @@ __global__ __launch_bounds__(256) void pack_scatter_kernel(
     SeqMap seq, int64_t keep_sh, PackOut po, const int32_t* __restrict__ ws_off,
     const int32_t* __restrict__ ws_next, const int32_t* __restrict__ anchor_counts,
     int32_t* __restrict__ num_packed) {
+  __shared__ int s_rows[VEC ? 4 : 1][64];  // a wave's anchor rows in packed order
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   const int64_t bh = blockIdx.y;
   const int64_t b = bh / Hkv, h = bh - (bh / Hkv) * Hkv;
@@ -211,6 +215,38 @@ __global__ __launch_bounds__(256) void pack_scatter_kernel(
         po.ts[c_row0 + dst] = (int32_t)r;                // tritonModules.py:131-132
         po.cnt[c_row0 + dst] = (int32_t)(next - r);      // modeling_llama.py:683-685
       }
+      if (VEC) s_rows[wid][rank] = lane;
+    }
+    if (VEC) {
+      // sixteen anchor rows per step: lane (sub, c) moves 16-byte chunk c of row sub + 4i
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+      const int na = __popcll(bits);
+      const int sub = lane >> 4, cq = lane & 15;
+      const bool actq = cq < (D >> 3);
+      const uint16_t* kbase = k + seq.base((int)b, sk_b, sk_n) + h * sk_h + 8 * cq;
+      const uint16_t* vbase = v + seq.base((int)b, sv_b, sv_n) + h * sv_h + 8 * cq;
+      for (int j0 = 0; j0 < na; j0 += 16) {
+        uint4 kw[4], vw[4];
+        int64_t dj[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int j = j0 + 4 * i + sub;
+          const bool ok = actq && j < na;
+          const int64_t src = (int64_t)g * 64 + (ok ? s_rows[wid][j] : 0);
+          dj[i] = ok ? off + j : -1;
+          kw[i] = ok ? *(const uint4*)(kbase + src * sk_n) : uint4{0u, 0u, 0u, 0u};
+          vw[i] = ok ? *(const uint4*)(vbase + src * sv_n) : uint4{0u, 0u, 0u, 0u};
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          if (dj[i] >= 0 && dj[i] < capacity) {
+            *(uint4*)(po.kp + kp_row0 + dj[i] * po.sp_n + 8 * cq) = kw[i];
+            *(uint4*)(po.vp + kp_row0 + dj[i] * po.sp_n + 8 * cq) = vw[i];
+          }
+        }
+      }
     }
     // Copy the anchor rows, sixteen rows per step so that their loads are in flight
     // together (a 64-row group holds about 64 / r anchors).
@@ -218,7 +254,7 @@ __global__ __launch_bounds__(256) void pack_scatter_kernel(
     const uint16_t* kbase = k + seq.base((int)b, sk_b, sk_n) + h * sk_h + 2 * lane;
     const uint16_t* vbase = v + seq.base((int)b, sv_b, sv_n) + h * sv_h + 2 * lane;
     const bool act = lane < nw;
-    uint64_t rem = bits;
+    uint64_t rem = VEC ? 0ull : bits;
     int64_t dst = off;
     while (rem) {
       int rows[kRows];
@@ -250,13 +286,16 @@ __global__ __launch_bounds__(256) void pack_scatter_kernel(
     }
   }
 
-  // Zero padding rows [c, min(P, capacity)) of this head, 256 rows per workgroup.
+  // Zero padding rows [c, min(P, capacity)) of this head, 256 rows per workgroup; most
+  // workgroups have none and skip the loop.
   const int64_t pad_end = (P < capacity) ? P : capacity;
   const int64_t r0 = (int64_t)c + (int64_t)blockIdx.x * 256;
-  for (int i = tid; i < 256 * nw; i += 256) {
-    const int64_t row = r0 + i / nw;
-    const int wd = i % nw;
-    if (row < pad_end) {
+  if (r0 < pad_end) {
+    const int nrows = pad_end - r0 < 256 ? (int)(pad_end - r0) : 256;
+    for (int i = tid; i < nrows * nw; i += 256) {
+      const int rr = i / nw;
+      const int wd = i - rr * nw;
+      const int64_t row = r0 + rr;
       *(uint32_t*)(po.kp + kp_row0 + row * po.sp_n + 2 * wd) = 0u;
       *(uint32_t*)(po.vp + kp_row0 + row * po.sp_n + 2 * wd) = 0u;
       if (wd == 0) {
@@ -286,10 +325,17 @@ static int launch_pack(const char* who, const int32_t* keep, const void* k, cons
   hipLaunchKernelGGL(pack_scan_kernel, dim3((unsigned)(B * Hkv)), dim3(kScanThreads), 0, st, keep, N_fixed,
                      (int)ngroups, (int)Hkv, seq, keep_sh, ws_off, ws_next, anchor_counts);
   if (int rc = check_launch(who)) return rc;
-  hipLaunchKernelGGL(pack_scatter_kernel, dim3((unsigned)((ngroups + 3) / 4), (unsigned)(B * Hkv)),
-                     dim3(256), 0, st, keep, (const uint16_t*)k, (const uint16_t*)v, sk_b, sk_h,
-                     sk_n, sv_b, sv_h, sv_n, (int)Hkv, N_fixed, (int)D, (int)ngroups, (int)(B * Hkv),
-                     seq, keep_sh, po, ws_off, ws_next, anchor_counts, num_packed);
+  const bool vec = (D & 7) == 0 && ((sk_b | sk_h | sk_n | sv_b | sv_h | sv_n | po.sp_b | po.sp_h | po.sp_n) & 7) == 0 &&
+                   (((uintptr_t)k | (uintptr_t)v | (uintptr_t)po.kp | (uintptr_t)po.vp) & 15) == 0;
+  const dim3 grid((unsigned)((ngroups + 3) / 4), (unsigned)(B * Hkv));
+  if (vec)
+    hipLaunchKernelGGL(pack_scatter_kernel<true>, grid, dim3(256), 0, st, keep, (const uint16_t*)k,
+                       (const uint16_t*)v, sk_b, sk_h, sk_n, sv_b, sv_h, sv_n, (int)Hkv, N_fixed, (int)D,
+                       (int)ngroups, (int)(B * Hkv), seq, keep_sh, po, ws_off, ws_next, anchor_counts, num_packed);
+  else
+    hipLaunchKernelGGL(pack_scatter_kernel<false>, grid, dim3(256), 0, st, keep, (const uint16_t*)k,
+                       (const uint16_t*)v, sk_b, sk_h, sk_n, sv_b, sv_h, sv_n, (int)Hkv, N_fixed, (int)D,
+                       (int)ngroups, (int)(B * Hkv), seq, keep_sh, po, ws_off, ws_next, anchor_counts, num_packed);
   return check_launch(who);
 }
 

@@ -134,6 +134,34 @@ def test_pack_exact(gpu, N, tau):
     assert torch.equal(packed.v_packed[:, :, :P].float().cpu(), torch.from_numpy(ref["v_packed"]))
 
 
+@pytest.mark.parametrize("D,pad", [(128, 2), (66, 0)], ids=["offset-rows", "D66"])
+def test_pack_exact_4byte_rows(gpu, D, pad):
+    """The 4-byte row copy of the scatter: key/value rows that are 4-byte but not 16-byte
+    aligned (views at a 2-element offset in rows of D + 4), and a head dimension that is
+    not a multiple of 8."""
+    from deltaattention_amd import ops
+    N = 2000
+    q, k, v = _bf16_inputs(1, 4, 3, N, D, seed=6)
+    announce(f"pack 4-byte rows D={D} pad={pad}")
+    if pad:
+        kb = torch.zeros((1, 3, N, D + 4), dtype=k.dtype)
+        vb = torch.zeros((1, 3, N, D + 4), dtype=v.dtype)
+        kb[..., pad:pad + D], vb[..., pad:pad + D] = k, v
+        kg, vg = kb.to(gpu)[..., pad:pad + D], vb.to(gpu)[..., pad:pad + D]
+    else:
+        kg, vg = k.to(gpu), v.to(gpu)
+    keep, _ = ops.select(kg.contiguous(), 8.0 * (D / 128) ** 0.5, 512)
+    packed = ops.pack(keep, kg, vg)
+    torch.cuda.synchronize()
+    ref = O.pack(k.float().numpy(), v.float().numpy(), keep.cpu().numpy())
+    P = int(packed.num_packed.item())
+    assert P == ref["P"]
+    assert (packed.timestamps[:, :, :P].cpu().numpy() == ref["timestamps"]).all()
+    assert (packed.counts[:, :, :P].cpu().numpy() == ref["counts"]).all()
+    assert torch.equal(packed.k_packed[:, :, :P].float().cpu(), torch.from_numpy(ref["k_packed"]))
+    assert torch.equal(packed.v_packed[:, :, :P].float().cpu(), torch.from_numpy(ref["v_packed"]))
+
+
 def test_pack_periodic_and_exact_capacity(gpu):
     """Periodic keep mask (modeling_llama.py:626-632) packed into buffers of exactly P rows."""
     from deltaattention_amd import ops
