@@ -501,6 +501,30 @@ def time_loop(fn, iters):
     return e0.elapsed_time(e1) / iters
 
 
+def cold_calls_ms(fn, runs=10, warm=3, flush_bytes=512 << 20):
+    """Median and mean ms of ``fn`` over ``runs`` calls after ``warm`` untimed ones, each
+    call preceded by writing a ``flush_bytes`` buffer (more than the 256 MB Infinity Cache
+    plus the L2s), so that every call reads its inputs from HBM.  HIP events bracket each
+    call on the stream the kernels run on."""
+    import statistics
+    import torch
+    st = torch.cuda.current_stream()
+    flush = torch.empty(flush_bytes, dtype=torch.uint8, device="cuda")
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    times = []
+    for i in range(warm + runs):
+        flush.fill_(i & 0xFF)
+        e0.record(st)
+        fn()
+        e1.record(st)
+        e1.synchronize()
+        if i >= warm:
+            times.append(e0.elapsed_time(e1))
+    del flush
+    return statistics.median(times), statistics.fmean(times)
+
+
 def sdpa_ms(q, k, v, iters):
     """torch's scaled_dot_product_attention (causal) on the same inputs, flash / memory-
     efficient backends only (the math backend would materialise N x N), K/V expanded to
@@ -578,8 +602,10 @@ def measure_layer(args, N, ratio, headline):
     ms_hybrid = time_loop(hybrid_only, iters)
     ms_dense = time_loop(dense_only, iters)
     ms_compress = time_loop(compress_only, iters)
+    cold_med, cold_mean = cold_calls_ms(compress_only)
     ms_sdpa = sdpa_ms(q, k, v, max(3, iters // 3)) if not args.no_sdpa else None
-    log(f"hybrid {ms_hybrid:.3f} ms  dense {ms_dense:.3f} ms  compress {ms_compress:.4f} ms  "
+    log(f"hybrid {ms_hybrid:.3f} ms  dense {ms_dense:.3f} ms  compress {ms_compress:.4f} ms "
+        f"(caches flushed: median {cold_med:.4f}, mean {cold_mean:.4f})  "
         f"sdpa {ms_sdpa if ms_sdpa is None else round(ms_sdpa, 3)} ms")
 
     fl = metrics.hybrid_flops(ts_h, c_h, P, N, Hq, D, W)
@@ -600,6 +626,9 @@ def measure_layer(args, N, ratio, headline):
         "compress_ms": round(ms_compress, 4),
         "compress_gbs": round(cbytes / (ms_compress * 1e-3) / 1e9, 1),
         "compress_hbm_frac": round(cbytes / (ms_compress * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
+        "compress_cold_ms_median": round(cold_med, 4),
+        "compress_cold_ms_mean": round(cold_mean, 4),
+        "compress_cold_gbs": round(cbytes / (cold_med * 1e-3) / 1e9, 1),
         "hybrid_tflops": round(hyb_tflops, 1),
         "hybrid_mfma_frac": round(hyb_tflops / BF16_PEAK_TFLOPS, 4),
         "dense_tflops": round(dense_tflops, 1),
