@@ -1079,7 +1079,10 @@ void attn_w64_kernel(AttnArgs a) {
   }
   __builtin_amdgcn_s_waitcnt(vmcnt_only(0));  // no load may land in LDS after the exit
 
-  // ---- finalize ----
+  // ---- finalize: each column block goes through the wave's own Q region of LDS (its
+  // last Q.K is done), 16-byte chunk c of row r at position c ^ (r & 15), and leaves as
+  // whole rows, four per store instruction, instead of 16 bytes of 32 rows ----
+  uint16_t* const obase = a.out + a.seq.base(b, a.so_b, a.so_n) + (int64_t)h * a.so_h;
 #pragma unroll
   for (int cb = 0; cb < 2; ++cb) {
     const float l_tot = halves_sum(l_i[cb]);
@@ -1088,19 +1091,35 @@ void attn_w64_kernel(AttnArgs a) {
       inv = l_tot > 0.0f ? 1.0f / l_tot : 1.0f;  // deltaFlashAttention.py:353-354
     else
       inv = 1.0f / l_tot;
-    const int row = r0w + 32 * cb + ql;
-    if (row < Nq) {
-      uint16_t* orow = a.out + a.seq.base(b, a.so_b, a.so_n) + (int64_t)h * a.so_h + (int64_t)row * a.so_n;
 #pragma unroll
-      for (int db = 0; db < 4; ++db)
+    for (int db = 0; db < 4; ++db)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          u32x2 w;
-          w[0] = E16<DT>::pack(o[cb][db][4 * j + 0] * inv, o[cb][db][4 * j + 1] * inv);
-          w[1] = E16<DT>::pack(o[cb][db][4 * j + 2] * inv, o[cb][db][4 * j + 3] * inv);
-          if (db * 32 + 8 * j + 4 * hl < a.D) *(u32x2*)(orow + db * 32 + 8 * j + 4 * hl) = w;
-        }
+      for (int j = 0; j < 4; ++j) {
+        u32x2 w;
+        w[0] = E16<DT>::pack(o[cb][db][4 * j + 0] * inv, o[cb][db][4 * j + 1] * inv);
+        w[1] = E16<DT>::pack(o[cb][db][4 * j + 2] * inv, o[cb][db][4 * j + 3] * inv);
+        // dims db * 32 + 8 j + 4 hl .. + 3 of row ql: half hl of chunk 4 db + j
+        *(u32x2*)(qs + ql * 256 + (((4 * db + j) ^ (ql & 15)) << 4) + 8 * hl) = w;
+      }
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
+    const int cq = lane & 15;
+    u32x4 rw[8];
+#pragma unroll
+    for (int it = 0; it < 8; ++it) {
+      const int r = 4 * it + (lane >> 4);
+      rw[it] = *(const u32x4*)(qs + r * 256 + ((cq ^ (r & 15)) << 4));
     }
+#pragma unroll
+    for (int it = 0; it < 8; ++it) {
+      const int row = r0w + 32 * cb + 4 * it + (lane >> 4);
+      if (row < Nq && cq * 8 < a.D) *(u32x4*)(obase + (int64_t)row * a.so_n + cq * 8) = rw[it];
+    }
+    // the reads of this block are done before the next block overwrites the region
+    __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
   }
 }
 
