@@ -1142,7 +1142,9 @@ struct SchedPrep {
   float* zeros;
   int wcap;
 };
-__global__ __launch_bounds__(256) void hybrid_schedule_kernel(const int32_t* __restrict__ ts,
+constexpr int kSchedThreads = 1024;
+constexpr int kSchedWaves = kSchedThreads / 64;
+__global__ __launch_bounds__(kSchedThreads) void hybrid_schedule_kernel(const int32_t* __restrict__ ts,
                                                               int64_t sts_b, int64_t sts_h,
                                                               int Hkv, int P_host,
                                                               const int32_t* P_dev, int Nk,
@@ -1150,7 +1152,7 @@ __global__ __launch_bounds__(256) void hybrid_schedule_kernel(const int32_t* __r
                                                               int32_t* __restrict__ sched,
                                                               SchedPrep prep) {
   __shared__ int32_t s_bmax[4096];
-  __shared__ int32_t s_wave[4];
+  __shared__ int32_t s_wave[kSchedWaves];
   const int tid = threadIdx.x, lane = tid & 63;
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar)
   const int bg = blockIdx.x;
@@ -1167,36 +1169,25 @@ __global__ __launch_bounds__(256) void hybrid_schedule_kernel(const int32_t* __r
     const int32_t* crow = (const int32_t*)prep.cnt + seq.base(b, prep.scnt_b, 1) + (int64_t)g * prep.scnt_h;
     float* wrow = prep.wts + (int64_t)bg * prep.wcap;
     int32_t* trow = prep.tsw ? prep.tsw + (int64_t)bg * prep.wcap : nullptr;
-    const int i0 = (blockIdx.y - 1) * 1024 + tid;
-    // rows at or beyond P are clamped to row P - 1 and masked after the load, so the
-    // loads of the four rows issue together (P = 0 loads nothing)
-    int32_t raw[4], tr[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int ic = min(i0 + 256 * j, P - 1);
-      raw[j] = P > 0 ? crow[ic] : 0;
-      tr[j] = P > 0 && trow ? row[ic] : INT_MAX;
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int i = i0 + 256 * j;
-      if (i >= prep.wcap) break;
-      float w = 0.0f;
-      int tv = INT_MAX;
-      if (i < P) {
-        w = prep.no_count ? 1.0f : (prep.cnt_is_float ? __int_as_float(raw[j]) : (float)raw[j]);
-        if (trow && w > 0.0f) tv = tr[j];
-      }
-      wrow[i] = w > 0.0f ? log2f(w) / prep.scale_log2 : -INFINITY;
-      if (trow) trow[i] = tv;
-    }
     if (bg == 0 && blockIdx.y == 1 && tid < kTileN) prep.zeros[tid] = 0.0f;
+    // the attention kernels read rows below nblk * 128 only
+    const int i = (blockIdx.y - 1) * kSchedThreads + tid;
+    if ((blockIdx.y - 1) * kSchedThreads >= nblk * kBlock || i >= prep.wcap) return;
+    float w = 0.0f;
+    int tv = INT_MAX;
+    if (i < P) {
+      const int32_t raw = crow[i];
+      w = prep.no_count ? 1.0f : (prep.cnt_is_float ? __int_as_float(raw) : (float)raw);
+      if (trow && w > 0.0f) tv = row[i];
+    }
+    wrow[i] = w > 0.0f ? log2f(w) / prep.scale_log2 : -INFINITY;
+    if (trow) trow[i] = tv;
     return;
   }
-  // wave w takes blocks 8w .. 8w + 7 of every 32, their loads in flight together:
+  // wave w takes blocks 8w .. 8w + 7 of every 8 kSchedWaves, their loads in flight together:
   // rows at or beyond P are clamped to row P - 1 and masked after the load (a guarded
   // load is waited for before the next one is issued); nblk > 0 implies P > 0
-  for (int jb0 = wid * 8; jb0 < nblk; jb0 += 32) {
+  for (int jb0 = wid * 8; jb0 < nblk; jb0 += 8 * kSchedWaves) {
     int m[8];
     int r0[8], r1[8];
 #pragma unroll
@@ -1218,7 +1209,7 @@ __global__ __launch_bounds__(256) void hybrid_schedule_kernel(const int32_t* __r
     }
   }
   __syncthreads();
-  const int per = (nblk + 255) / 256;
+  const int per = (nblk + kSchedThreads - 1) / kSchedThreads;
   const int j0 = min(tid * per, nblk), j1 = min(j0 + per, nblk);
   int mloc = INT_MIN;
   for (int j = j0; j < j1; ++j) mloc = max(mloc, s_bmax[j]);
@@ -1433,8 +1424,8 @@ static int hybrid_impl(const char* who, AttnArgs& a, const void* k_packed, const
     prep.zeros = (float*)(ws + wl.zeros_off);
     prep.wcap = wl.wcap;
   }
-  const unsigned prep_chunks = prep.wts ? (unsigned)((wl.wcap + 1023) / 1024) : 0u;
-  hipLaunchKernelGGL(hybrid_schedule_kernel, dim3((unsigned)(B * Hkv), 1 + prep_chunks), dim3(256), 0, st,
+  const unsigned prep_chunks = prep.wts ? (unsigned)((wl.wcap + kSchedThreads - 1) / kSchedThreads) : 0u;
+  hipLaunchKernelGGL(hybrid_schedule_kernel, dim3((unsigned)(B * Hkv), 1 + prep_chunks), dim3(kSchedThreads), 0, st,
                      timestamps, a.sts_b, a.sts_h, (int)Hkv, (int)P_bound, num_packed_dev, (int)Nk, a.seq,
                      a.nblk_cap, (int32_t*)ws, prep);
   if (int rc = check_launch("hybrid prefill (schedule)")) return rc;

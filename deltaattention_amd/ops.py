@@ -91,8 +91,8 @@ def select(k: torch.Tensor, threshold: float, chunk_size: int = 512, divide_to: 
     cs, nc = chunking(N, chunk_size, divide_to)
     use_cos = metric == "cosine"
     thr = float(threshold) if use_cos else float(threshold) ** 2
-    if keep is None:
-        keep = torch.zeros((B, H, N), dtype=torch.int32, device=k.device)
+    if keep is None:  # the chunks tile [0, N): the kernel writes every flag
+        keep = torch.empty((B, H, N), dtype=torch.int32, device=k.device)
     if chunk_counts is None:
         chunk_counts = torch.empty((B, H, nc), dtype=torch.int32, device=k.device)
     rc = lib().da_select(k.data_ptr(), dt, B, H, N, D, k.stride(0), k.stride(1), k.stride(2),
