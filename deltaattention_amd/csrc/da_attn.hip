@@ -810,26 +810,33 @@ void attn_w64_kernel(AttnArgs a) {
   // ---- Q^T of both column blocks in registers, loaded while the first tiles are in
   // flight; rows past Nq load row Nq - 1 and dims past D dims 0..7, zeroed after ----
   u32x4 qreg[kD / 16];
+  {
+    // both column blocks requested before either is used: one round trip, not two
+    u32x4 w[2][kD / 16];
 #pragma unroll
-  for (int cb = 0; cb < 2; ++cb) {
-    const int row = r0w + 32 * cb + ql;
-    const uint16_t* qrow = a.q + a.seq.base(b, a.sq_b, a.sq_n) + (int64_t)h * a.sq_h + (int64_t)min(row, Nq - 1) * a.sq_n;
-    u32x4 w[kD / 16];
+    for (int cb = 0; cb < 2; ++cb) {
+      const int row = r0w + 32 * cb + ql;
+      const uint16_t* qrow = a.q + a.seq.base(b, a.sq_b, a.sq_n) + (int64_t)h * a.sq_h + (int64_t)min(row, Nq - 1) * a.sq_n;
 #pragma unroll
-    for (int t = 0; t < kD / 16; ++t) {
-      const int d0 = 16 * t + 8 * hl;
-      w[t] = *(const u32x4*)(qrow + (d0 < a.D ? d0 : 0));
+      for (int t = 0; t < kD / 16; ++t) {
+        const int d0 = 16 * t + 8 * hl;
+        w[cb][t] = *(const u32x4*)(qrow + (d0 < a.D ? d0 : 0));
+      }
     }
     // redefined so that the loop does not see Q as an outstanding load (the S = K Q^T
     // blocks would otherwise wait for every memory load, the staging loads included)
 #pragma unroll
-    for (int t = 0; t < kD / 16; ++t) {
-      asm volatile("" : "+v"(w[t]));
-      const u32x4 qv = (row < Nq && 16 * t + 8 * hl < a.D) ? w[t] : u32x4{0, 0, 0, 0};
-      if (cb == 0)
-        qreg[t] = qv;
-      else
-        *(u32x4*)(qs + k_row + (((2 * t + hl) ^ k_swz) << 4)) = qv;
+    for (int cb = 0; cb < 2; ++cb) {
+      const int row = r0w + 32 * cb + ql;
+#pragma unroll
+      for (int t = 0; t < kD / 16; ++t) {
+        asm volatile("" : "+v"(w[cb][t]));
+        const u32x4 qv = (row < Nq && 16 * t + 8 * hl < a.D) ? w[cb][t] : u32x4{0, 0, 0, 0};
+        if (cb == 0)
+          qreg[t] = qv;
+        else
+          *(u32x4*)(qs + k_row + (((2 * t + hl) ^ k_swz) << 4)) = qv;
+      }
     }
   }
   if (T > 0) {
