@@ -258,8 +258,10 @@ class HybridCompressedCache(_CacheBase):
 
     def _plan(self, layer_idx, Hq):
         """The layer's DaDecodeStep block with the cache fields filled in, and its
-        workspace; rebuilt when the capacity grows (the tensors move)."""
-        plan = self._plans.get((layer_idx, Hq))
+        workspace; keyed by the cache tensors' addresses, so a block is never used after
+        the tensors move (capacity growth, or a caller replacing them)."""
+        key = (layer_idx, Hq, self.k_packed.data_ptr(), self.k_exact.data_ptr())
+        plan = self._plans.get(key)
         if plan is not None:
             return plan
         st = DecodeStep()
@@ -281,7 +283,7 @@ class HybridCompressedCache(_CacheBase):
         ws = torch.empty((max(1, ws_bytes),), dtype=torch.uint8, device=self.device)
         st.workspace, st.workspace_bytes = ws.data_ptr(), ws_bytes
         plan = (st, ws, ctypes.byref(st))
-        self._plans[(layer_idx, Hq)] = plan
+        self._plans[key] = plan
         return plan
 
     def decode_step(self, query_states, key_states, value_states, layer_idx, scaling=None):
