@@ -220,8 +220,12 @@ def test_decode_cache_matches_oracle(gpu, metric, tau, dtype):
             setattr(globVR, name, val)
 
 
-@pytest.mark.parametrize("metric,tau", [("euclidean", 9.5), ("cosine", 0.9)])
-def test_decode_step_equals_update_then_attention(gpu, metric, tau):
+@pytest.mark.parametrize("metric,tau,dtype,Hq,Hkv", [
+    ("euclidean", 9.5, torch.bfloat16, 8, 2),
+    ("cosine", 0.9, torch.bfloat16, 8, 2),
+    ("euclidean", 9.5, torch.float16, 16, 2),   # fp16 cache, GQA group 8
+], ids=["euclidean-bf16-G4", "cosine-bf16-G4", "euclidean-fp16-G8"])
+def test_decode_step_equals_update_then_attention(gpu, metric, tau, dtype, Hq, Hkv):
     """HybridCompressedCache.decode_step (one da_decode_step call per token) against
     cache.update + decode_attention on a twin cache: every step's output and the final
     cache state bit-identical, through ring fill, eviction into the packed cache and a
@@ -229,17 +233,15 @@ def test_decode_step_equals_update_then_attention(gpu, metric, tau):
     from types import SimpleNamespace
     from deltaattention_amd import globVR
     from deltaattention_amd.deltaDecoding import HybridCompressedCache, decode_attention
-    B, Hq, Hkv, W, steps = 2, 8, 2, 16, 96
-    q, k, v = _inputs(B, Hq, Hkv, steps, 11)
+    B, W, steps = 2, 16, 96
+    q, k, v = (t.to(dtype) for t in _inputs(B, Hq, Hkv, steps, 11))
     cfg = SimpleNamespace(hidden_size=Hq * 128, num_attention_heads=Hq, num_key_value_heads=Hkv,
                           num_hidden_layers=2, head_dim=128)
     saved = dict(vars(globVR))
     try:
         globVR.row_delta_threshold, globVR.row_similarity_metric = tau, metric
-        a = HybridCompressedCache(cfg, B, dtype=torch.bfloat16, exact_window_size=W,
-                                  initial_capacity=8)
-        b = HybridCompressedCache(cfg, B, dtype=torch.bfloat16, exact_window_size=W,
-                                  initial_capacity=8)
+        a = HybridCompressedCache(cfg, B, dtype=dtype, exact_window_size=W, initial_capacity=8)
+        b = HybridCompressedCache(cfg, B, dtype=dtype, exact_window_size=W, initial_capacity=8)
         qg, kg, vg = q.to(gpu), k.to(gpu), v.to(gpu)
         announce(f"decode_step {metric}: {steps} steps on layer 1, B={B} Hq={Hq} Hkv={Hkv} W={W}")
         for t in range(steps):
