@@ -1087,9 +1087,8 @@ void attn_w64_kernel(AttnArgs a) {
   __builtin_amdgcn_s_waitcnt(vmcnt_only(0));  // no load may land in LDS after the exit
 
   // ---- finalize: each column block goes through the wave's own Q region of LDS (its
-  // last Q.K is done), 16-byte chunk c of row r at position c ^ (r & 15) with its two
-  // 8-byte halves swapped in rows 16-31 (so that rows r and r + 16 use other banks), and
-  // leaves as whole rows, four per store instruction, instead of 16 bytes of 32 rows ----
+  // last Q.K is done), 16-byte chunk c of row r at position c ^ (r & 15), and leaves as
+  // whole rows, four per store instruction, instead of 16 bytes of 32 rows ----
   uint16_t* const obase = a.out + a.seq.base(b, a.so_b, a.so_n) + (int64_t)h * a.so_h;
 #pragma unroll
   for (int cb = 0; cb < 2; ++cb) {
@@ -1107,7 +1106,7 @@ void attn_w64_kernel(AttnArgs a) {
         w[0] = E16<DT>::pack(o[cb][db][4 * j + 0] * inv, o[cb][db][4 * j + 1] * inv);
         w[1] = E16<DT>::pack(o[cb][db][4 * j + 2] * inv, o[cb][db][4 * j + 3] * inv);
         // dims db * 32 + 8 j + 4 hl .. + 3 of row ql: half hl of chunk 4 db + j
-        *(u32x2*)(qs + ql * 256 + (((4 * db + j) ^ (ql & 15)) << 4) + 8 * (hl ^ (ql >> 4))) = w;
+        *(u32x2*)(qs + ql * 256 + (((4 * db + j) ^ (ql & 15)) << 4) + 8 * hl) = w;
       }
     __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront", "local");
     __builtin_amdgcn_wave_barrier();
@@ -1116,9 +1115,8 @@ void attn_w64_kernel(AttnArgs a) {
     u32x4 rw[8];
 #pragma unroll
     for (int it = 0; it < 8; ++it) {
-      const int r = 4 * it + (lane >> 4);  // rows 16-31 exactly when it >= 4
-      const u32x4 c = *(const u32x4*)(qs + r * 256 + ((cq ^ (r & 15)) << 4));
-      rw[it] = it < 4 ? c : u32x4{c[2], c[3], c[0], c[1]};
+      const int r = 4 * it + (lane >> 4);
+      rw[it] = *(const u32x4*)(qs + r * 256 + ((cq ^ (r & 15)) << 4));
     }
 #pragma unroll
     for (int it = 0; it < 8; ++it) {
