@@ -574,6 +574,11 @@ constexpr int vmcnt_only(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) 
 // The running maximum is updated lazily: only when a tile's maximum exceeds it by more
 // than 2^8 in probability (8 in log2 units) are O and l rescaled.
 constexpr float kLazyLog2 = 8.0f;
+// The 64-row kernel computes p against the current maximum before it looks at the
+// tile's maximum, and needs the latter only where a lane's sum of its 16 p exceeds
+// 16 * 2^8: below that bound every p is at most 2^8 * 16, and a rescale is not needed
+// (p stays far from fp32's range and keeps bf16's relative precision).
+constexpr float kLazySum = 16.0f * 256.0f;
 
 // ====================================================================================
 // Ping-pong kernel for GQA groups that are a multiple of 4 (the Llama-3 hot path).
@@ -856,7 +861,7 @@ void attn_w64_kernel(AttnArgs a) {
     constexpr bool odd = decltype(ODD)::value;
     const int tl = sec >> 1;
     const int sw = sec - grp_c;
-    // each wave issues its window's tile loads in its matrix section (after the P.V block)
+    // each wave issues its window's tile loads in its matrix section, after MFMA pair 6
     bool issued = odd != (grp_c != 0);
     auto issue_once = [&]() {
       if (!issued) {
@@ -940,9 +945,12 @@ void attn_w64_kernel(AttnArgs a) {
             }
           };
           static_for<issued(0)>(read);
-          issue_once();  // the tile loads go out while the first reads are in flight
           static_for<NM>([&](auto I) {
             constexpr int i = decltype(I)::value;
+            // the tile loads' scalar address work goes out between MFMA pairs 6 and 7,
+            // where it fills the matrix pipe's issue gaps (before pair 0 it delayed the
+            // first MFMA by about a hundred instructions)
+            if constexpr (i == 6) issue_once();
             if constexpr (i < NPV) {
               lgkm_wait<pending(i)>(vlo[i], vhi[i]);
               const u32x4 vw = __builtin_bit_cast(u32x4, __builtin_shufflevector(vlo[i], vhi[i], 0, 1, 2, 3, 4, 5, 6, 7));
@@ -1005,7 +1013,6 @@ void attn_w64_kernel(AttnArgs a) {
         // chains that fill each other's latencies), one ballot for both ----
         const char* ms = meta_of(t);
         const int key0 = key0_of(t);
-        float mx[2];
 #pragma unroll
         for (int cb = 0; cb < 2; ++cb) {
           const int row = r0w + 32 * cb + ql;
@@ -1016,36 +1023,13 @@ void attn_w64_kernel(AttnArgs a) {
               mask_dense32(s[cb], key0, row, hl, Nk, a.causal);
           }
         }
-#pragma unroll
-        for (int cb = 0; cb < 2; ++cb) {
-          float m = -INFINITY;
-#pragma unroll
-          for (int r = 0; r < 16; r += 2) m = __builtin_fmaxf(m, __builtin_fmaxf(s[cb][r], s[cb][r + 1]));
-          mx[cb] = halves_max(m);
-        }
-        // no NaN when m_used = -inf
-        const bool upd0 = mx[0] > m_used[0] + lazy_thr, upd1 = mx[1] > m_used[1] + lazy_thr;
-        if (__ballot(upd0 || upd1)) {
-          // alpha = 1 exactly where a lane keeps its maximum (also where that maximum
-          // is still -inf)
-#pragma unroll
-          for (int cb = 0; cb < 2; ++cb) {
-            const bool upd = cb == 0 ? upd0 : upd1;
-            const float m_new = upd ? mx[cb] : m_used[cb];
-            const float alpha = upd ? exp2_fast((m_used[cb] - m_new) * c) : 1.0f;
-#pragma unroll
-            for (int db = 0; db < 4; ++db)
-#pragma unroll
-              for (int r = 0; r < 16; ++r) o[cb][db][r] *= alpha;
-            l_i[cb] *= alpha;
-            m_used[cb] = m_new;
-          }
-        }
-#pragma unroll
-        for (int cb = 0; cb < 2; ++cb) {
+        // p against the current maximum first; only where a lane's sum of its 16 p
+        // exceeds kLazySum (some p above 2^8, a score above m_used + lazy_thr), or a lane
+        // has no maximum yet, is the tile's maximum taken and the column block redone
+        // with the lazy-rescale rule.  P in the 16-bit type for the P.V MFMAs; the row
+        // sum adds the fp32 p, as deltaFlashAttention.py:86-98
+        auto exps = [&](const int cb) {
           const float neg = (m_used[cb] == -INFINITY) ? 0.0f : -m_used[cb] * c;
-          // P in the 16-bit type for the P.V MFMAs; the row sum adds the fp32 p, as
-          // deltaFlashAttention.py:86-98
           float psa = 0.0f, psb = 0.0f;
 #pragma unroll
           for (int r4 = 0; r4 < 4; ++r4) {
@@ -1057,7 +1041,32 @@ void attn_w64_kernel(AttnArgs a) {
             psa += p[0] + p[1];
             psb += p[2] + p[3];
           }
-          l_i[cb] += psa + psb;
+          return psa + psb;
+        };
+#pragma unroll
+        for (int cb = 0; cb < 2; ++cb) {
+          float ps = exps(cb);
+          // !(x <= bound) also catches an infinite sum; a lane without a reference point
+          // yet (m_used = -inf) always takes the exact rule
+          if (__ballot(!(ps <= kLazySum) || m_used[cb] == -INFINITY)) {
+            float m = -INFINITY;
+#pragma unroll
+            for (int r = 0; r < 16; r += 2) m = __builtin_fmaxf(m, __builtin_fmaxf(s[cb][r], s[cb][r + 1]));
+            const float mx = halves_max(m);
+            // alpha = 1 exactly where a lane keeps its maximum (also where that maximum
+            // is still -inf); no NaN when m_used = -inf
+            const bool upd = mx > m_used[cb] + lazy_thr;
+            const float m_new = upd ? mx : m_used[cb];
+            const float alpha = upd ? exp2_fast((m_used[cb] - m_new) * c) : 1.0f;
+#pragma unroll
+            for (int db = 0; db < 4; ++db)
+#pragma unroll
+              for (int r = 0; r < 16; ++r) o[cb][db][r] *= alpha;
+            l_i[cb] *= alpha;
+            m_used[cb] = m_new;
+            ps = exps(cb);
+          }
+          l_i[cb] += ps;
         }
       }
     }
