@@ -803,9 +803,11 @@ void attn_w64_kernel(AttnArgs a) {
     for (int i = 0; i < 4; ++i) o[cb][i] = f32x16{};
   f32x16 s[2];
   u32x4 pw[2][2];
-  float m_used[2] = {-INFINITY, -INFINITY}, l_i[2] = {0.0f, 0.0f};
+  // mc: the running maximum times c, the reference point of p = 2^(s c - mc).  Until a
+  // lane has seen a finite score it is -FLT_MAX: every finite score then gives p = +inf
+  // (the exact rule takes over), a masked one p = 0, and s c - mc is never NaN
+  float mc[2] = {-__FLT_MAX__, -__FLT_MAX__}, l_i[2] = {0.0f, 0.0f};
   const float c = a.scale_log2;
-  const float lazy_thr = kLazyLog2 / c;
 
   if (T > 0) {
     dma_rows(true, 0);
@@ -1024,13 +1026,12 @@ void attn_w64_kernel(AttnArgs a) {
           }
         }
         // p against the current maximum first; only where a lane's sum of its 16 p
-        // exceeds kLazySum (some p above 2^8, a score above m_used + lazy_thr), or a lane
+        // exceeds kLazySum (some p above 2^8, a score above the maximum by 8 / c), or a lane
         // has no maximum yet, is the tile's maximum taken and the column block redone
         // with the lazy-rescale rule.  P in the 16-bit type for the P.V MFMAs; the row
         // sum adds the fp32 p, as deltaFlashAttention.py:86-98
-        auto exps = [&](const int cb) {
-          const float neg = (m_used[cb] == -INFINITY) ? 0.0f : -m_used[cb] * c;
-          float psa = 0.0f, psb = 0.0f;
+        auto exps = [&](const int cb, const float neg) {
+          float psa, psb;
 #pragma unroll
           for (int r4 = 0; r4 < 4; ++r4) {
             float p[4];
@@ -1038,33 +1039,31 @@ void attn_w64_kernel(AttnArgs a) {
             for (int e = 0; e < 4; ++e) p[e] = exp2_fast(__builtin_fmaf(s[cb][4 * r4 + e], c, neg));
             pw[cb][r4 >> 1][(r4 & 1) * 2 + 0] = E16<DT>::pack(p[0], p[1]);
             pw[cb][r4 >> 1][(r4 & 1) * 2 + 1] = E16<DT>::pack(p[2], p[3]);
-            psa += p[0] + p[1];
-            psb += p[2] + p[3];
+            psa = r4 == 0 ? p[0] + p[1] : psa + (p[0] + p[1]);
+            psb = r4 == 0 ? p[2] + p[3] : psb + (p[2] + p[3]);
           }
           return psa + psb;
         };
 #pragma unroll
         for (int cb = 0; cb < 2; ++cb) {
-          float ps = exps(cb);
-          // !(x <= bound) also catches an infinite sum; a lane without a reference point
-          // yet (m_used = -inf) always takes the exact rule
-          if (__ballot(!(ps <= kLazySum) || m_used[cb] == -INFINITY)) {
+          float ps = exps(cb, -mc[cb]);
+          // the bound also catches an infinite sum
+          if (__builtin_amdgcn_ballot_w64(ps > kLazySum)) {
             float m = -INFINITY;
 #pragma unroll
             for (int r = 0; r < 16; r += 2) m = __builtin_fmaxf(m, __builtin_fmaxf(s[cb][r], s[cb][r + 1]));
-            const float mx = halves_max(m);
-            // alpha = 1 exactly where a lane keeps its maximum (also where that maximum
-            // is still -inf); no NaN when m_used = -inf
-            const bool upd = mx > m_used[cb] + lazy_thr;
-            const float m_new = upd ? mx : m_used[cb];
-            const float alpha = upd ? exp2_fast((m_used[cb] - m_new) * c) : 1.0f;
+            const float mxc = halves_max(m) * c;
+            // alpha = 1 exactly where a lane keeps its maximum (also where it has none yet)
+            const bool upd = mxc > mc[cb] + kLazyLog2;
+            const float m_new = upd ? mxc : mc[cb];
+            const float alpha = upd ? exp2_fast(mc[cb] - m_new) : 1.0f;
 #pragma unroll
             for (int db = 0; db < 4; ++db)
 #pragma unroll
               for (int r = 0; r < 16; ++r) o[cb][db][r] *= alpha;
             l_i[cb] *= alpha;
-            m_used[cb] = m_new;
-            ps = exps(cb);
+            mc[cb] = m_new;
+            ps = exps(cb, -m_new);
           }
           l_i[cb] += ps;
         }
