@@ -571,8 +571,8 @@ __device__ __forceinline__ float halves_sum(float x) {
 // s_waitcnt immediate (gfx9 encoding) that waits for vmcnt <= n only.
 constexpr int vmcnt_only(int n) { return (n & 15) | ((n >> 4) << 14) | (7 << 4) | (15 << 8); }
 
-// The running maximum is updated lazily: only when a tile's maximum exceeds it by more
-// than 2^8 in probability (8 in log2 units) are O and l rescaled.
+// The 64-row kernel updates its running maximum lazily: only when a tile's maximum
+// exceeds it by more than 2^8 in probability (8 in log2 units) are O and l rescaled.
 constexpr float kLazyLog2 = 8.0f;
 // The 64-row kernel computes p against the current maximum before it looks at the
 // tile's maximum, and needs the latter only where a lane's sum of its 16 p exceeds
@@ -1011,8 +1011,8 @@ void attn_w64_kernel(AttnArgs a) {
 #pragma unroll
           for (int j = 0; j < 2; ++j) undefined(pw[cb][j]);
       } else {
-        // ---- softmax section for tile t: the two column blocks side by side (independent
-        // chains that fill each other's latencies), one ballot for both ----
+        // ---- softmax section for tile t: the two column blocks one after the other, one
+        // check each ----
         const char* ms = meta_of(t);
         const int key0 = key0_of(t);
 #pragma unroll
@@ -1026,10 +1026,10 @@ void attn_w64_kernel(AttnArgs a) {
           }
         }
         // p against the current maximum first; only where a lane's sum of its 16 p
-        // exceeds kLazySum (some p above 2^8, a score above the maximum by 8 / c), or a lane
-        // has no maximum yet, is the tile's maximum taken and the column block redone
-        // with the lazy-rescale rule.  P in the 16-bit type for the P.V MFMAs; the row
-        // sum adds the fp32 p, as deltaFlashAttention.py:86-98
+        // exceeds kLazySum (some p above 2^8, a score above the maximum by 8 / c; +inf
+        // while the lane has no maximum yet) is the tile's maximum taken and the column
+        // block redone with the lazy-rescale rule.  P in the 16-bit type for the P.V
+        // MFMAs; the row sum adds the fp32 p, as deltaFlashAttention.py:86-98
         auto exps = [&](const int cb, const float neg) {
           float psa, psb;
 #pragma unroll
