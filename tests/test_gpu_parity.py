@@ -193,6 +193,51 @@ def test_dense_vs_oracle(gpu, B, Hq, Hkv, N, causal):
     _close(out.float().cpu().numpy(), ref, f"dense N={N}")
 
 
+def _ramp_inputs(B, Hq, Hkv, N, D, seed, top):
+    """bf16 inputs whose scaled scores follow a ramp over the keys: from 0 to `top` for a
+    query along the ramp direction (top < 0: falling), plus unit noise.  A rising ramp
+    moves each row's maximum in most tiles, so the kernels' rescale path runs often; a
+    falling one leaves late keys with p far below 2^-126."""
+    g = torch.Generator().manual_seed(seed)
+    u = torch.randn(D, generator=g)
+    u = u / u.norm()
+    scale = D ** -0.5
+    qn = 8.0
+    q = torch.randn(B, Hq, N, D, generator=g) * 0.5 + qn * u
+    ramp = torch.linspace(0.0, 1.0, N).view(1, 1, N, 1) * (top / (scale * qn))
+    k = torch.randn(B, Hkv, N, D, generator=g) + ramp * u
+    v = torch.randn(B, Hkv, N, D, generator=g)
+    return q.to(torch.bfloat16), k.to(torch.bfloat16), v.to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("top", [200.0, 60.0, -200.0], ids=["rise200", "rise60", "fall200"])
+def test_dense_rescale_stress_vs_oracle(gpu, top):
+    """Scores that climb across the keys make the running maximum move in most tiles
+    (the grouped kernel's exact path and O rescale), and falling ones drive p to zero."""
+    from deltaattention_amd import ops
+    q, k, v = _ramp_inputs(1, 8, 2, 2048, 128, seed=11, top=top)
+    announce(f"dense rescale stress top={top}")
+    out = ops.dense_prefill(q.to(gpu), k.to(gpu), v.to(gpu), causal=True)
+    ref = O.dense_attention(q.float().numpy(), k.float().numpy(), v.float().numpy(), True)
+    _close(out.float().cpu().numpy(), ref, f"dense ramp {top}")
+
+
+@pytest.mark.parametrize("top,tau,variant", [
+    (200.0, 1e6, "hybrid"), (60.0, 16.0, "hybrid"), (200.0, 16.0, "sanity"),
+    (-200.0, 1e6, "hybrid"), (60.0, 16.0, "pure_phase1")])
+def test_delta_rescale_stress_vs_oracle(gpu, top, tau, variant):
+    from deltaattention_amd import ops
+    q, k, v = _ramp_inputs(1, 8, 2, 2048, 128, seed=12, top=top)
+    announce(f"delta rescale stress top={top} tau={tau} {variant}")
+    out = ops.delta_prefill(q.to(gpu), k.to(gpu), v.to(gpu), tau, 512, window=128, variant=variant)
+    kf, vf = k.float().numpy(), v.float().numpy()
+    keep, _ = OC.select_delta(kf, tau, 512)
+    p = O.pack(kf, vf, keep)
+    ref = O.hybrid_attention(q.float().numpy(), kf, vf, p["k_packed"], p["v_packed"],
+                             p["timestamps"], p["counts"], 128, variant=variant)
+    _close(out.float().cpu().numpy(), ref, f"delta ramp {top} {variant}")
+
+
 # --------------------------------------------------------------------------------------
 # hybrid prefill against the reference's own outputs (golden vectors, D=32 zero-padded)
 # --------------------------------------------------------------------------------------
