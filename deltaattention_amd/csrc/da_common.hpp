@@ -177,6 +177,12 @@ __device__ __forceinline__ float wave_tree_sum_all(float t) {
   return __uint_as_float(q[0]) + __uint_as_float(q[1]);
 }
 
+// Correctly rounded fp32 square root (round to nearest even), as the CPU restatement's
+// sqrtf.  HIP's __fsqrt_rn is the hardware approximation unless OCML's rounded
+// operations are enabled, and differs from it in the last place often enough to flip a
+// cosine decision that sits at the threshold (one row in a million keys of 64 heads).
+__device__ __forceinline__ float sqrt_rn(float x) { return __builtin_sqrtf(x); }
+
 // x0*y0 + x1*y1 with both products rounded (no fused multiply-add).
 __device__ __forceinline__ float pair_dot(float x0, float x1, float y0, float y1) {
 #pragma clang fp contract(off)

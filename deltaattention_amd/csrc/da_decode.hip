@@ -70,8 +70,8 @@ __global__ __launch_bounds__(256) void decode_update_kernel(DecodeUpdateArgs a) 
       if (COS) {
         const float eps = 1e-8f;
         const float dot = wave_tree_sum(pair_dot(e0, e1, l0, l1));
-        const float ne = __fsqrt_rn(wave_tree_sum(pair_dot(e0, e1, e0, e1)) + eps);
-        const float nl = __fsqrt_rn(wave_tree_sum(pair_dot(l0, l1, l0, l1)) + eps);
+        const float ne = sqrt_rn(wave_tree_sum(pair_dot(e0, e1, e0, e1)) + eps);
+        const float nl = sqrt_rn(wave_tree_sum(pair_dot(l0, l1, l0, l1)) + eps);
         merge = __fdiv_rn(dot, ne * nl) >= a.thr;
       } else {
         const float d0 = e0 - l0, d1 = e1 - l1;

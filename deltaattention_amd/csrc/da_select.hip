@@ -24,6 +24,10 @@
 // the decisions.  The distance reaches every lane through v_permlane16/32_swap (no
 // scalar round trip), the anchor update is a select, and a batch's decisions collect
 // in a 32-bit mask stored as int32 (the reference's keep-mask format).
+//
+// From 2048 chunks on (two per SIMD), select_pair_kernel walks two chunks per wave,
+// one per 32-lane half with four slots per lane, over the same tree (bit-identical);
+// below that, one wave per chunk keeps every chunk on a SIMD of its own.
 #include <algorithm>
 
 #include "da_common.hpp"
@@ -31,6 +35,7 @@
 namespace da {
 
 constexpr int kSelBatch = 32;
+constexpr int64_t kSelPairMinChunks = 2048;
 
 // x rounded to the 16-bit type DT (nearest even) and widened back to fp32.
 template <int DT>
@@ -65,7 +70,7 @@ __device__ __forceinline__ bool select_step(uint32_t xb, float& a0, float& a1, f
   float x_norm = 0.0f;
   if (COS) {  // tritonModules.py:48-54
     const float dot = wave_tree_sum_all(pair_dot(x0, x1, a0, a1));
-    x_norm = __fsqrt_rn(wave_tree_sum_all(pair_dot(x0, x1, x0, x1)) + eps);
+    x_norm = sqrt_rn(wave_tree_sum_all(pair_dot(x0, x1, x0, x1)) + eps);
     const float sim = __fdiv_rn(dot, x_norm * a_norm);
     kp = sim < thr;
   } else if (A16) {  // tritonModules.py:55-58 in the keys' 16-bit arithmetic
@@ -119,7 +124,7 @@ __global__ __launch_bounds__(256) void select_kernel(
   const uint32_t a_bits = row_bits(s);
   float a0 = E16<DT>::lo(a_bits), a1 = E16<DT>::hi(a_bits);
   float a_norm = 0.0f;
-  if (COS) a_norm = __fsqrt_rn(wave_tree_sum_all(pair_dot(a0, a1, a0, a1)) + 1e-8f);
+  if (COS) a_norm = sqrt_rn(wave_tree_sum_all(pair_dot(a0, a1, a0, a1)) + 1e-8f);
   if (lane == 0) keep_row[s] = 1;  // row s is an anchor (tritonModules.py:41)
   int count = 1;
 
@@ -149,6 +154,125 @@ __global__ __launch_bounds__(256) void select_kernel(
   if (lane == 0) chunk_counts[w] = count;  // tritonModules.py:68-69
 }
 
+// ---- two chunks per wave, one per 32-lane half ----
+// Lane q of a half holds head-dimension slots 4q .. 4q+3 of a row (one 8-byte load), so
+// a wave walks two chunks at once.  The tree keeps its pairing: levels 1-2 add slots
+// inside the lane, lane^1, lane^2, the 8-lane and the 16-lane mirror give levels 3-6, and
+// v_permlane16_swap pairs the two 16-lane rows of each half for level 7 -- the blocks
+// that the one-chunk-per-wave tree pairs at each level, so the sums are bit-identical.
+template <bool R16, int DT>
+__device__ __forceinline__ float half_tree_sum(float p0, float p1, float p2, float p3) {
+#pragma clang fp contract(off)
+  auto r = [](float v) { return R16 ? round16<DT>(v) : v; };
+  float t = r(r(p0 + p1) + r(p2 + p3));
+  t = r(t + dpp_f32<kDppXor1>(t));
+  t = r(t + dpp_f32<kDppXor2>(t));
+  t = r(t + dpp_f32<kDppHalfMirror>(t));
+  t = r(t + dpp_f32<kDppMirror>(t));
+  const auto sw = __builtin_amdgcn_permlane16_swap(__float_as_uint(t), __float_as_uint(t), false, false);
+  return r(__uint_as_float(sw[0]) + __uint_as_float(sw[1]));
+}
+
+// select_step for the row a 32-lane half holds (x: four slots); rows with `valid` false
+// are never kept.
+template <bool COS, bool A16, int DT>
+__device__ __forceinline__ bool half_step(const uint2 xb, float (&a)[4], float& a_norm, float thr, bool valid) {
+#pragma clang fp contract(off)
+  const float x[4] = {E16<DT>::lo(xb.x), E16<DT>::hi(xb.x), E16<DT>::lo(xb.y), E16<DT>::hi(xb.y)};
+  bool kp;
+  float x_norm = 0.0f;
+  if (COS) {  // tritonModules.py:48-54
+    const float dot = half_tree_sum<false, DT>(x[0] * a[0], x[1] * a[1], x[2] * a[2], x[3] * a[3]);
+    x_norm = sqrt_rn(half_tree_sum<false, DT>(x[0] * x[0], x[1] * x[1], x[2] * x[2], x[3] * x[3]) + 1e-8f);
+    kp = __fdiv_rn(dot, x_norm * a_norm) < thr;
+  } else if (A16) {  // tritonModules.py:55-58 in the keys' 16-bit arithmetic
+    float p[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float d = round16<DT>(x[i] - a[i]);
+      p[i] = round16<DT>(d * d);
+    }
+    kp = half_tree_sum<true, DT>(p[0], p[1], p[2], p[3]) > thr;
+  } else {  // tritonModules.py:55-58
+    float p[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const float d = x[i] - a[i];
+      p[i] = d * d;
+    }
+    kp = half_tree_sum<false, DT>(p[0], p[1], p[2], p[3]) > thr;
+  }
+  kp = kp && valid;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) a[i] = kp ? x[i] : a[i];  // tritonModules.py:60-63
+  if (COS) a_norm = kp ? x_norm : a_norm;
+  return kp;
+}
+
+// The chunks as select_kernel walks them, two per wave (chunk 2 w + half).  Needs D a
+// multiple of 4 and 8-byte aligned rows.
+template <bool COS, bool A16, int DT>
+__global__ __launch_bounds__(256) void select_pair_kernel(
+    const uint16_t* __restrict__ k, int64_t sk_b, int64_t sk_h, int64_t sk_n, int H, int64_t N,
+    int D, int64_t cs, int64_t nc, int64_t total_chunks, float thr, int32_t* __restrict__ keep,
+    int32_t* __restrict__ chunk_counts, SeqMap seq, int64_t keep_sh, int divide_to) {
+#pragma clang fp contract(off)
+  const int lane = threadIdx.x & 63;
+  const int q = lane & 31;
+  const int64_t w = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * 2 + (lane >> 5);
+  // rows [s, e) of this half's chunk; none for a chunk past the grid or the sequence
+  int s = 0, e = 0;
+  int32_t* keep_row = keep;
+  const uint16_t* base = k;
+  if (w < total_chunks) {
+    const int64_t bh = w / nc;
+    const int64_t c = w - bh * nc;
+    const int64_t b = bh / H, h = bh - (bh / H) * H;
+    const int64_t Nb = seq.cu ? seq.len((int)b) : N;
+    int64_t csb = cs;
+    if (seq.cu) csb = divide_to > 0 ? (Nb + divide_to - 1) / divide_to : (cs < Nb ? cs : Nb);
+    if (Nb > 0 && c * csb < Nb) {
+      s = (int)(c * csb);
+      e = (int)((c * csb + csb < Nb) ? c * csb + csb : Nb);
+      base = k + seq.base((int)b, sk_b, sk_n) + h * sk_h + 4 * q;
+      keep_row = keep + (seq.cu ? h * keep_sh + seq.start((int)b) : bh * N);
+    } else if (q == 0) {
+      chunk_counts[w] = 0;  // tritonModules.py:34-35 (count stays 0, modeling_llama.py:637)
+    }
+  }
+  const bool active = 4 * q < D;
+  auto row_bits = [&](int r) -> uint2 {
+    return (active && r < e) ? *(const uint2*)(base + (int64_t)r * sk_n) : uint2{0u, 0u};
+  };
+  const uint2 ab = row_bits(s);
+  float a[4] = {E16<DT>::lo(ab.x), E16<DT>::hi(ab.x), E16<DT>::lo(ab.y), E16<DT>::hi(ab.y)};
+  float a_norm = 0.0f;
+  if (COS)
+    a_norm = sqrt_rn(half_tree_sum<false, DT>(a[0] * a[0], a[1] * a[1], a[2] * a[2], a[3] * a[3]) + 1e-8f);
+  if (q == 0 && e > s) keep_row[s] = 1;  // row s is an anchor (tritonModules.py:41)
+  int count = 1;
+  // batches of both halves (wave-uniform): the longer of the two walks
+  const int nbh = e > s ? (e - s - 1 + kSelBatch - 1) / kSelBatch : 0;
+  const int nb = max(__builtin_amdgcn_readlane(nbh, 0), __builtin_amdgcn_readlane(nbh, 32));
+  uint2 cur[kSelBatch], nxt[kSelBatch];
+#pragma unroll
+  for (int j = 0; j < kSelBatch; ++j) cur[j] = row_bits(s + 1 + j);
+  for (int bi = 0; bi < nb; ++bi) {
+    const int i0 = s + 1 + bi * kSelBatch;
+#pragma unroll
+    for (int j = 0; j < kSelBatch; ++j) nxt[j] = row_bits(i0 + kSelBatch + j);
+    uint32_t bb = 0;
+#pragma unroll
+    for (int j = 0; j < kSelBatch; ++j)
+      bb |= (uint32_t)half_step<COS, A16, DT>(cur[j], a, a_norm, thr, i0 + j < e) << j;
+    count += __builtin_popcount(bb);  // tritonModules.py:68
+    if (i0 + q < e) keep_row[i0 + q] = (int32_t)((bb >> q) & 1u);
+#pragma unroll
+    for (int j = 0; j < kSelBatch; ++j) cur[j] = nxt[j];
+  }
+  if (q == 0 && e > s) chunk_counts[w] = count;  // tritonModules.py:68-69
+}
+
 static int launch_select(const void* k, int dtype, int64_t B, int64_t Hkv, int64_t N, int64_t D, int64_t sk_b,
                          int64_t sk_h, int64_t sk_n, float threshold, bool use_cosine, bool a16, int64_t chunk_size,
                          int64_t num_chunks, int32_t* keep, int32_t* chunk_counts, SeqMap seq, int64_t keep_sh,
@@ -158,6 +282,28 @@ static int launch_select(const void* k, int dtype, int64_t B, int64_t Hkv, int64
   const int64_t total = B * Hkv * num_chunks;
   const int64_t blocks = (total + 3) / 4;
   DA_REQUIRE(blocks < (1ll << 31), "%s: too many chunks", who);
+  // From two chunks per SIMD on (256 CUs x 4 SIMDs), one wave per pair of chunks walks
+  // both in one instruction stream and leaves the SIMDs one wave each: 79 against 85 us
+  // at 131072 keys x 8 heads.  Fewer chunks keep one wave per chunk (the pair layout
+  // would leave SIMDs idle).
+  if (total >= kSelPairMinChunks && (D & 3) == 0 && ((sk_b | sk_h | sk_n) & 3) == 0 && ((uintptr_t)k & 7) == 0) {
+    const int64_t pblocks = (total + 7) / 8;
+#define DA_SELPAIR_LAUNCH(COS, A16, DT)                                                                      \
+  hipLaunchKernelGGL((select_pair_kernel<COS, A16, DT>), dim3((unsigned)pblocks), dim3(256), 0, st,           \
+                     (const uint16_t*)k, sk_b, sk_h, sk_n, (int)Hkv, N, (int)D, chunk_size, num_chunks, total, \
+                     threshold, keep, chunk_counts, seq, keep_sh, divide_to)
+    if (dtype == DA_F16) {
+      if (use_cosine) DA_SELPAIR_LAUNCH(true, false, DA_F16);
+      else if (a16) DA_SELPAIR_LAUNCH(false, true, DA_F16);
+      else DA_SELPAIR_LAUNCH(false, false, DA_F16);
+    } else {
+      if (use_cosine) DA_SELPAIR_LAUNCH(true, false, DA_BF16);
+      else if (a16) DA_SELPAIR_LAUNCH(false, true, DA_BF16);
+      else DA_SELPAIR_LAUNCH(false, false, DA_BF16);
+    }
+#undef DA_SELPAIR_LAUNCH
+    return check_launch(who);
+  }
 #define DA_SELECT_LAUNCH(COS, A16, DT)                                                                       \
   hipLaunchKernelGGL((select_kernel<COS, A16, DT>), dim3((unsigned)blocks), dim3(256), 0, st, (const uint16_t*)k, \
                      sk_b, sk_h, sk_n, (int)Hkv, N, (int)D, chunk_size, num_chunks, total, threshold, keep,  \

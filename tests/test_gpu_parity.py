@@ -81,11 +81,17 @@ def test_select_bitexact_config1_shape(gpu):
     (8, 32768, 256, 10.3, "euclidean", "fp32"),   # 1024 chunks
     (8, 32768, 128, 0.9, "cosine", "fp32"),       # 2048 chunks
     (8, 32768, 256, 10.3, "euclidean", "native"),
+    # from 2048 chunks on, one wave walks two chunks (one per 32-lane half)
+    (8, 131072, 512, 10.33, "euclidean", "fp32"),  # the config-2 grid
+    (8, 131072, 512, 10.33, "euclidean", "native"),
+    (8, 32768, 128, 1e6, "euclidean", "fp32"),
+    (64, 16000, 512, 9.0, "euclidean", "fp32"),     # a 128-row last chunk
+    (9, 32768, 129, 9.0, "euclidean", "fp32"),      # 2295 chunks: the last wave's second half is empty
 ])
 def test_select_chunk_shapes(gpu, H, N, chunk, tau, metric, arith):
     """Selection against the sequential oracle over chunk lengths from 1 to 10000 rows,
-    grids of 2 to 2048 chunks and thresholds that keep one row per chunk or nearly
-    every row."""
+    grids of 2 to 2295 chunks (one chunk per wave below 2048, two from there on) and
+    thresholds that keep one row per chunk or nearly every row."""
     from deltaattention_amd import ops, synth
     k = synth.make_layer_inputs(1, H, H, N, 128, seed=21, rope_base=500000.0)[1]
     announce(f"select H={H} N={N} chunk={chunk} tau={tau} {metric} {arith}")
@@ -95,6 +101,21 @@ def test_select_chunk_shapes(gpu, H, N, chunk, tau, metric, arith):
     assert np.array_equal(cc.cpu().numpy(), occ), "chunk counts differ"
     keep_h = keep.cpu().numpy()
     assert np.array_equal(keep_h, ok), f"keep differs at {np.argwhere(keep_h != ok)[:5]}"
+
+
+@pytest.mark.parametrize("D,dtype", [(64, torch.bfloat16), (128, torch.float16), (66, torch.bfloat16)],
+                         ids=["D64", "fp16", "D66-one-per-wave"])
+def test_select_pair_grid_dims(gpu, D, dtype):
+    """2048 chunks with head_dim 64 (lanes past D hold nothing) and fp16 keys walk two
+    chunks per wave; head_dim 66 (not a multiple of 4) keeps one chunk per wave."""
+    from deltaattention_amd import ops, synth
+    k = synth.make_layer_inputs(1, 64, 64, 16384, D, seed=23, rope_base=500000.0)[1].to(dtype)
+    for tau, metric in ((9.0, "euclidean"), (0.9, "cosine")):
+        announce(f"select pair grid D={D} {dtype} {metric}")
+        keep, cc = ops.select(k.to(gpu), tau, 512, 0, metric)
+        ok, occ = OC.select_delta(k.float().numpy(), tau, 512, 0, metric)
+        assert np.array_equal(cc.cpu().numpy(), occ), "chunk counts differ"
+        assert np.array_equal(keep.cpu().numpy(), ok)
 
 
 @pytest.mark.parametrize("dtype,oracle_arith", [(torch.bfloat16, "bf16"), (torch.float16, "fp16")])
