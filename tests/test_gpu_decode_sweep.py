@@ -1,0 +1,91 @@
+"""Randomized decode parity: 8 configurations drawn with a fixed seed (batch, KV heads,
+GQA group, prefill length, window, steps, metric, threshold, 16-bit type, initial cache
+capacity), each a prefill hand-off followed by decode steps that alternate between
+cache.update + decode_attention and the one-call cache.decode_step.  The cache state is
+bit-exact against the oracle (deltaDecoding.py:9-104, 181-233) and the attention within
+max-abs 2e-2 (bf16) / 5e-3 (fp16) of it (deltaDecoding.py:236-362)."""
+from types import SimpleNamespace
+
+import numpy as np
+import pytest
+import torch
+
+from conftest import announce
+from oracle import delta_oracle as O
+from oracle import select_oracle_c as OC
+import test_gpu_dropin as T
+
+pytestmark = pytest.mark.gpu
+
+
+def _cases(n=8, seed=11):
+    rng = np.random.default_rng(seed)
+    out = []
+    for _ in range(n):
+        metric = "cosine" if rng.random() < 0.4 else "euclidean"
+        out.append(dict(
+            B=int(rng.choice([1, 1, 2])), Hkv=int(rng.choice([1, 2, 3])), G=int(rng.choice([1, 2, 4, 8])),
+            N=int(rng.integers(130, 2000)), W=int(rng.choice([16, 50, 128])), steps=int(rng.integers(20, 120)),
+            metric=metric, tau=float(rng.uniform(0.8, 0.97)) if metric == "cosine" else float(rng.uniform(7.0, 13.0)),
+            fp16=bool(rng.random() < 0.4), cap0=int(rng.choice([16, 64, 512])),
+            seed=int(rng.integers(0, 1000)), pattern=int(rng.integers(0, 1 << 30))))
+    return out
+
+
+CASES = _cases()
+
+
+def _id(c):
+    return (f"B{c['B']}-Hkv{c['Hkv']}-G{c['G']}-N{c['N']}-W{c['W']}-T{c['steps']}-{c['metric'][:3]}-"
+            f"{'f16' if c['fp16'] else 'bf16'}-cap{c['cap0']}")
+
+
+@pytest.mark.parametrize("c", CASES, ids=[_id(c) for c in CASES])
+def test_random_decode_vs_oracle(gpu, c):
+    from deltaattention_amd import attention, globVR
+    from deltaattention_amd.deltaDecoding import HybridCompressedCache, decode_attention
+    B, Hkv, N, W, steps = c["B"], c["Hkv"], c["N"], c["W"], c["steps"]
+    Hq = c["G"] * Hkv
+    dtype = torch.float16 if c["fp16"] else torch.bfloat16
+    announce(f"decode sweep {_id(c)} tau={c['tau']:.3f}")
+    q, k, v = (t.to(dtype) for t in T._inputs(B, Hq, Hkv, N + steps, c["seed"]))
+    cfg = SimpleNamespace(hidden_size=Hq * 128, num_attention_heads=Hq, num_key_value_heads=Hkv,
+                          num_hidden_layers=1, head_dim=128)
+    saved = dict(vars(globVR))
+    try:
+        globVR.packing_mode, globVR.chunk_size = "delta", 512
+        globVR.row_delta_threshold, globVR.row_similarity_metric = c["tau"], c["metric"]
+        globVR.time_internal = False
+        cache = HybridCompressedCache(cfg, B, dtype=dtype, exact_window_size=W, initial_capacity=c["cap0"])
+        qg, kg, vg = q.to(gpu), k.to(gpu), v.to(gpu)
+        attention.delta_prefill_attention(qg[:, :, :N], kg[:, :, :N], vg[:, :, :N], 0, cache)
+        kf, vf = k.float().numpy(), v.float().numpy()
+        keep, _ = OC.select_delta(kf[:, :, :N], c["tau"], 512, 0, c["metric"])
+        p = O.pack(kf[:, :, :N], vf[:, :, :N], keep)
+        st = T._oracle_cache_from_prefill(p, kf[:, :, :N], vf[:, :, :N], W, cache.capacity + 4096)
+        fused = np.random.default_rng(c["pattern"]).random(steps) < 0.5
+        worst = 0.0
+        for t in range(steps):
+            sl = slice(N + t, N + t + 1)
+            if fused[t]:
+                out = cache.decode_step(qg[:, :, sl], kg[:, :, sl], vg[:, :, sl], 0)
+            else:
+                cache.update(kg[:, :, sl], vg[:, :, sl], 0)
+                out = decode_attention(qg[:, :, sl], cache, 0)
+            O.decode_update(st, kf[:, :, sl], vf[:, :, sl], c["tau"], c["metric"])
+            if t % 17 == 0 or t == steps - 1:
+                ref = O.decode_attention(q.float().numpy()[:, :, N + t], st)
+                worst = max(worst, float(np.abs(out[:, :, 0].float().cpu().numpy() - ref).max()))
+        n = int(cache.packed_lengths[0].max().item())
+        assert (cache.packed_lengths[0].cpu().numpy() == st["lengths"]).all()
+        assert (cache.packed_counts[0, :, :, :n].cpu().numpy() == st["counts"][:, :, :n]).all()
+        assert (cache.packed_timestamps[0, :, :, :n].cpu().numpy() == st["timestamps"][:, :, :n]).all()
+        assert torch.equal(cache.k_packed[0, :, :, :n].float().cpu(), torch.from_numpy(st["k_packed"][:, :, :n]))
+        assert torch.equal(cache.v_packed[0, :, :, :n].float().cpu(), torch.from_numpy(st["v_packed"][:, :, :n]))
+        assert torch.equal(cache.k_exact[0].float().cpu(), torch.from_numpy(st["k_exact"]))
+        assert cache.get_seq_length(0) == N + steps
+        print(f"{_id(c)}: attention max-abs {worst:.3e}", flush=True)
+        assert worst <= (5e-3 if c["fp16"] else 2e-2)
+    finally:
+        for name, val in saved.items():
+            setattr(globVR, name, val)
