@@ -132,23 +132,25 @@ def test_varlen_select_pack_bitexact(gpu, chunk, divide_to):
         assert np.array_equal(packed.v_packed[s:s + P].permute(1, 0, 2).float().cpu().numpy(), ref["v_packed"][0])
 
 
-def test_varlen_select_pair_grid(gpu):
-    """A ragged batch whose grid reaches 2048 chunks (8 sequences x 8 KV heads x 32 chunks)
-    takes the two-chunks-per-wave walk; halves past a sequence's last chunk write a zero
-    count.  Keep rows and chunk counts against the oracle on each sequence alone."""
+@pytest.mark.parametrize("chunk,divide_to", [(512, 0), (0, 32)])
+def test_varlen_select_pair_grid(gpu, chunk, divide_to):
+    """A ragged batch whose grid reaches 2048 chunks (8 sequences x 8 KV heads x 32 chunks,
+    by chunk size or by divide_to) takes the two-chunks-per-wave walk; halves past a
+    sequence's last chunk write a zero count.  Keep rows and chunk counts against the
+    oracle on each sequence alone."""
     from deltaattention_amd import ops
     from oracle import select_oracle_c as OC
     lens = [16384, 9000, 300, 12000, 5, 16384, 7000, 1]
     q, k, v, cu = _batch(lens, hq=8, hkv=8)
     tau = 9.0
-    announce(f"varlen select pair grid lens {lens}")
-    keep, cc = ops.select_varlen(k, cu, tau, 512, 0)
+    announce(f"varlen select pair grid lens {lens} chunk={chunk} divide_to={divide_to}")
+    keep, cc = ops.select_varlen(k, cu, tau, chunk, divide_to)
     torch.cuda.synchronize()
     keep_h, cc_h = keep.cpu().numpy(), cc.cpu().numpy()
     assert cc_h.shape[-1] * cc_h.shape[0] * cc_h.shape[1] >= 2048
     for b, (s, e) in enumerate(zip(cu[:-1], cu[1:])):
         kf = _per_seq(k, s, e).float().cpu().numpy()
-        okeep, occ = OC.select_delta(kf, tau, 512, 0)
+        okeep, occ = OC.select_delta(kf, tau, chunk, divide_to)
         assert np.array_equal(keep_h[:, s:e], okeep[0]), f"keep of sequence {b}"
         assert np.array_equal(cc_h[b, :, :occ.shape[-1]], occ[0]) and (cc_h[b, :, occ.shape[-1]:] == 0).all()
 
