@@ -736,7 +736,7 @@ void attn_w64_kernel(AttnArgs a) {
   const int skb = __builtin_amdgcn_readfirstlane((int)(2 * a.sk_n));
   const int svpb = __builtin_amdgcn_readfirstlane((int)(2 * a.svp_n));
   const int svb = __builtin_amdgcn_readfirstlane((int)(2 * a.sv_n));
-  auto dma_rows = [&](bool isK, int t_raw) {
+  auto dma_rows = [&](bool isK, int t_raw, unsigned st) {
     const int t = min(t_raw, T - 1);
     const bool ph1 = t < n1;
     const int key0 = key0_of(t);
@@ -747,13 +747,14 @@ void attn_w64_kernel(AttnArgs a) {
     const int range = clamp0_uniform(limit - key0, kWTK) * snb;
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<void*>(base), (short)0, range, kBufferDword3);
-    char* dst = isK ? kst0 + ((unsigned)t_raw % 3u) * kWKBytes : vst0 + ((unsigned)t_raw % 3u) * kWVBytes;
+    char* dst = isK ? kst0 + st : vst0 + st;
     const int rowt = wid_s * 4 + (lane >> 4);
     const int pos = lane & 15;
     const int chunk = pos ^ (isK ? (rowt & 15) : 4 * (rowt & 3));
-    // rowt < 32 and snb < 2^24 (the host limits sequence strides to 2^23 elements); a
-    // chunk at or past the head dimension reads past the range (zeros), without a branch
-    const int off = __mul24(rowt, snb) + chunk * 16 + (chunk * 8 < a.D ? 0 : range);
+    // rowt < 32 and snb < 2^24 (the host limits sequence strides to 2^23 elements), so the
+    // unsigned 24-bit multiply is exact (a signed one would read snb >= 2^23 as negative);
+    // a chunk at or past the head dimension reads past the range (zeros), without a branch
+    const int off = (int)__umul24((unsigned)rowt, (unsigned)snb) + chunk * 16 + (chunk * 8 < a.D ? 0 : range);
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)(dst + wid_s * 1024), 16,
                                              off, 0, 0, 0);
   };
@@ -780,9 +781,9 @@ void attn_w64_kernel(AttnArgs a) {
                                                lane * 4, 0, 0, 0);
     }
   };
-  auto dma_issue = [&](int tk, int tv) {
-    dma_rows(true, tk);
-    dma_rows(false, tv);
+  auto dma_issue = [&](int tk, int tv, unsigned kst, unsigned vst) {
+    dma_rows(true, tk, kst);
+    dma_rows(false, tv, vst);
     if (wid_s == 0) dma_meta(tk);
   };
 
@@ -791,10 +792,9 @@ void attn_w64_kernel(AttnArgs a) {
   // fragments of 16 keys x 32 head dims (db) read with ds_read_b64_tr_b16 from rows
   // whose chunks sit at c ^ 4 (r & 3).  Both are recomputed in each matrix section
   // (made opaque there) rather than held in registers ----
-  int k_row = ql * 256, k_swz = ql & 15;
-  int v_q = (lane & 15) >> 2;
-  int v_lane = (4 * ((lane >> 4) >> 1) + v_q) * 256 + ((2 * ((lane >> 4) & 1) + ((lane & 3) >> 1)) << 4) +
-                     8 * (lane & 1);
+  int k_lane = ql * 256 + (((hl ^ ql) & 1) << 4) + ((ql & 14) << 4);
+  int v_lane = (4 * ((lane >> 4) >> 1) + ((lane & 15) >> 2)) * 256 +
+               ((2 * ((lane >> 4) & 1) + ((lane & 3) >> 1)) << 4) + 8 * (lane & 1) + 64 * ((lane & 15) >> 2);
 
   f32x16 o[2][4];
 #pragma unroll
@@ -809,10 +809,11 @@ void attn_w64_kernel(AttnArgs a) {
   float mc[2] = {-__FLT_MAX__, -__FLT_MAX__}, l_i[2] = {0.0f, 0.0f};
   const float c = a.scale_log2;
 
+  unsigned stA = 0, stB = kWKBytes, stC = 2 * kWKBytes;
   if (T > 0) {
-    dma_rows(true, 0);
+    dma_rows(true, 0, stA);
     if (wid_s == 0) dma_meta(0);
-    dma_issue(1, 0);
+    dma_issue(1, 0, stB, stA);
   }
   // ---- Q^T of both column blocks in registers, loaded while the first tiles are in
   // flight; rows past Nq load row Nq - 1 and dims past D dims 0..7, zeroed after ----
@@ -842,7 +843,7 @@ void attn_w64_kernel(AttnArgs a) {
         if (cb == 0)
           qreg[t] = qv;
         else
-          *(u32x4*)(qs + k_row + (((2 * t + hl) ^ k_swz) << 4)) = qv;
+          *(u32x4*)(qs + ql * 256 + (((2 * t + hl) ^ (ql & 15)) << 4)) = qv;
       }
     }
   }
@@ -867,7 +868,7 @@ void attn_w64_kernel(AttnArgs a) {
     bool issued = odd != (grp_c != 0);
     auto issue_once = [&]() {
       if (!issued) {
-        dma_issue(tl + 2, tl + 1);
+        dma_issue(tl + 2, tl + 1, stC, stB);
         issued = true;
       }
     };
@@ -910,24 +911,18 @@ void attn_w64_kernel(AttnArgs a) {
           };
           uint32_t va[4] = {0, 0, 0, 0};
           if constexpr (PV) {
-            const uint32_t vb = lds_addr(vst0) + ((unsigned)(t - 1) % 3u) * kWVBytes;
+            const uint32_t vb = lds_addr(vst0) + stC;
             // opaque: otherwise the offsets are hoisted out of the loop into registers
-            asm volatile("" : "+v"(v_lane), "+v"(v_q));
+            asm volatile("" : "+v"(v_lane));
+            const uint32_t vl = vb + v_lane;
 #pragma unroll
-            for (int db = 0; db < 4; ++db) va[db] = vb + v_lane + 64 * (db ^ v_q);
+            for (int db = 0; db < 4; ++db) va[db] = vl ^ (64u * db);
           }
           uint32_t kla = 0, qla = 0, bla = 0;
-          int kx = 0;
           if constexpr (QK) {
-            asm volatile("" : "+v"(k_row), "+v"(k_swz));
-            // chunk 2 j + hl of the lane's row sits at ((2 j + hl) ^ k_swz) * 16 =
-            // ((32 j) ^ kx) + klo with kx = (k_swz & 14) * 16, klo = (hl ^ k_swz & 1) * 16.
-            // The stage and Q bases are multiples of 256, so the address of chunk 2 j + hl
-            // is (base + klo + kx) ^ (32 j): one XOR per read.
-            kx = (k_swz & 14) << 4;
-            const int klo = k_row + (((hl ^ k_swz) & 1) << 4) + kx;
-            kla = lds_addr(kst0 + ((unsigned)t % 3u) * kWKBytes) + klo;
-            qla = lds_addr(qs) + klo;
+            asm volatile("" : "+v"(k_lane));
+            kla = lds_addr(kst0) + stA + k_lane;
+            qla = lds_addr(qs) + k_lane;
             bla = lds_addr(meta_of(t) + kWCnt) + 16 * hl;
           }
           i16x4 vlo[8], vhi[8];
@@ -1081,15 +1076,23 @@ void attn_w64_kernel(AttnArgs a) {
   };
   using False = std::integral_constant<bool, false>;
   using True = std::integral_constant<bool, true>;
+  auto rotate_stages = [&]() {
+    const unsigned t0 = stA;
+    stA = stB;
+    stB = stC;
+    stC = t0;
+  };
   if (grp == 0) {
     for (int w = 0; w < nwin; ++w) {
       section(2 * w, std::integral_constant<int, 0>{}, False{});
       section(2 * w + 1, std::integral_constant<int, 0>{}, True{});
+      rotate_stages();
     }
   } else {
     for (int w = 0; w < nwin; ++w) {
       section(2 * w, std::integral_constant<int, 1>{}, False{});
       section(2 * w + 1, std::integral_constant<int, 1>{}, True{});
+      rotate_stages();
     }
   }
   __builtin_amdgcn_s_waitcnt(vmcnt_only(0));  // no load may land in LDS after the exit

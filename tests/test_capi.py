@@ -96,6 +96,16 @@ def test_attention_rejects_bad_shapes():
     assert lib.da_hybrid_prefill(*args, 3, fake, 1, 1, 4, 2, 64, 64, 128, st3, 10, None, 0,
                                  f, 0, 0, fake, 1 << 20, None) == -1
     assert b"sequence strides" in lib.da_last_error()
+    # sequence strides from 2^23 elements on are refused (the kernel's per-row byte offset
+    # is a 24-bit product); 2^23 - 8 is accepted and reaches the workspace check
+    big = [0, 0, 1 << 23]
+    st4 = _native.strides_array(rows + big + rows * 4 + [0, 0, 1, 0, 0, 1])
+    assert lib.da_hybrid_prefill(*args, 3, fake, 1, 1, 4, 2, 64, 64, 128, st4, 10, None, 0,
+                                 f, 0, 0, fake, 1 << 20, None) == -1
+    assert b"sequence strides" in lib.da_last_error()
+    st5 = _native.strides_array(rows + [0, 0, (1 << 23) - 8] + rows * 4 + [0, 0, 1, 0, 0, 1])
+    assert lib.da_hybrid_prefill(*args, 3, fake, 1, 1, 4, 2, 64, 64, 128, st5, 10, None, 0,
+                                 f, 0, 0, None, 0, None) == -4
 
 
 def test_decode_rejects_misaligned_values():

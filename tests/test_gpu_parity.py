@@ -458,3 +458,48 @@ def test_mixed_dtypes_are_rejected(gpu):
     q, k, v = _bf16_inputs(1, 4, 1, 256, 128, seed=1)
     with pytest.raises(TypeError):
         ops.dense_prefill(q.to(gpu), k.half().to(gpu), v.to(gpu))
+
+
+# --------------------------------------------------------------------------------------
+# key / value rows 2^22 + 8 elements apart: byte pitch 2^23 + 16, past the signed 24-bit
+# range of the staging's row-offset product (an unsigned product is exact up to 2^24)
+# --------------------------------------------------------------------------------------
+def test_attention_with_sequence_stride_past_2_pow_22(gpu):
+    from deltaattention_amd import ops
+    B, Hq, Hkv, N, D, W = 1, 4, 1, 160, 128, 32
+    stride = (1 << 22) + 8
+    q, k, v = _bf16_inputs(B, Hq, Hkv, N, D, seed=23)
+    announce(f"dense + hybrid, K/V/K^/V^ sequence stride {stride} elements, N={N} Hq={Hq}")
+
+    def spread(t):
+        # [B, 1, N, D] rows placed `stride` elements apart in one large buffer
+        buf = torch.zeros(N * stride, dtype=t.dtype, device=gpu)
+        view = buf.as_strided((B, Hkv, N, D), (N * stride, N * stride, stride, 1))
+        view.copy_(t.to(gpu))
+        return view, buf
+
+    kd, kbuf = spread(k)
+    vd, vbuf = spread(v)
+    qd = q.to(gpu)
+    out = ops.dense_prefill(qd, kd, vd, causal=True)
+    torch.cuda.synchronize()
+    want = O.dense_attention(q.float().numpy(), k.float().numpy(), v.float().numpy(), True)
+    _close(out.float().cpu().numpy(), want, "dense, stride 2^22+8")
+
+    tau = 9.0
+    keep, _ = ops.select(kd, tau, 64)
+    packed = ops.pack(keep, kd, vd)
+    P = int(packed.num_packed.item())
+    kp, kpbuf = spread(packed.k_packed[:, :, :N].float().cpu().to(torch.bfloat16))
+    vp, vpbuf = spread(packed.v_packed[:, :, :N].float().cpu().to(torch.bfloat16))
+    out_h = ops.hybrid_prefill(qd, kd, vd, kp, vp, packed.timestamps, packed.counts, window=W,
+                               num_packed_dev=packed.num_packed)
+    torch.cuda.synchronize()
+    kf, vf = k.float().numpy(), v.float().numpy()
+    okeep, _ = OC.select_delta(kf, tau, 64)
+    p = O.pack(kf, vf, okeep)
+    assert p["P"] == P
+    want_h = O.hybrid_attention(q.float().numpy(), kf, vf, p["k_packed"], p["v_packed"], p["timestamps"],
+                                p["counts"], W)
+    _close(out_h.float().cpu().numpy(), want_h, "hybrid, stride 2^22+8")
+    del kbuf, vbuf, kpbuf, vpbuf
