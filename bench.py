@@ -8,9 +8,13 @@ two-phase hybrid prefill, on synthetic inputs already resident in HBM (the work 
 reference times as time_get_row_delta + time_delta_mm_pattern,
 modeling_llama.py:612-754).
 
-Default workload is config 1 (N = 32768, r = 4); ``--config 2`` runs N = 131072 with
-``--ratio`` in {2, 4, 8}.  The threshold tau is calibrated on the seeded keys so that the
-realised compression is r (smallest tau with keep rate <= 1/r).
+The default run measures config 1 (N = 32768, r = 4) as the headline and adds to the same
+JSON line: config 2 (N = 131072) at r = 2, 4 and 8, the config-4 ragged batch, the
+config-3 end-to-end 32-layer prefill, the selection in both arithmetic definitions, the
+on-box MFMA and copy ceilings, and the CPU baseline (config 1 and config 0 in full).
+``--config 2`` runs N = 131072 alone with ``--ratio`` in {2, 4, 8}.  The threshold tau is
+calibrated on the seeded keys so that the realised compression is r (smallest tau with
+keep rate <= 1/r), in the selection arithmetic that is timed.
 
 ``--only {delta,hybrid,dense,compress}`` runs just that part for K steps (used for
 rocprofv3 captures) and prints a short line instead of the JSON record.
@@ -18,6 +22,7 @@ rocprofv3 captures) and prints a short line instead of the JSON record.
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import platform
@@ -49,6 +54,9 @@ def parse_args():
     ap.add_argument("--seed", type=int, default=0)
     ap.add_argument("--dtype", choices=("bf16", "fp16"), default="bf16",
                     help="16-bit type of Q, K, V (configs 1 and 2); bf16 is the headline")
+    ap.add_argument("--select-arith", choices=("native", "fp32"), default="native",
+                    help="Euclidean distance of the anchor selection: the keys' own 16-bit "
+                         "arithmetic as the reference computes it (tritonModules.py:55-58), or fp32")
     ap.add_argument("--only", choices=("delta", "hybrid", "dense", "compress", "copy", "convert"), default=None,
                     help="run one part for K steps (copy: a 1 GiB device copy; convert: 1 GiB of fp32 "
                          "read and written as bf16 by a vectorized elementwise kernel -- the "
@@ -60,12 +68,11 @@ def parse_args():
     ap.add_argument("--decode-tokens", type=int, default=200)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-128k", action="store_true",
-                    help="config 1 only: skip the config-2 (N=131072, r=4) measurement that the "
-                         "default run adds to the JSON line as config2_r4")
+                    help="config 1 only: skip the config-2 (N=131072, r=2/4/8) measurements")
+    ap.add_argument("--no-e2e", action="store_true",
+                    help="config 1 only: skip the config-3 end-to-end and config-4 ragged-batch parts")
     ap.add_argument("--no-sdpa", action="store_true",
                     help="skip timing torch's scaled_dot_product_attention as a second dense control")
-    ap.add_argument("--cpu-sample-blocks", type=int, default=24,
-                    help="query blocks (all heads) the CPU baseline runs")
     return ap.parse_args()
 
 
@@ -88,66 +95,69 @@ def _cpu_model() -> str:
     return platform.processor() or platform.machine()
 
 
-def cpu_baseline(q, k, v, tau, window, alg_total, dense_total, sample_blocks):
-    """Time the CPU restatement of the reference math (the oracle, a 'port') on a bounded
-    sample of the layer, on the host cores of the GPU box:
-
-    * delta: selection + packing over every KV head in full, then the hybrid attention for
-      ``sample_blocks`` evenly spaced query blocks of every query head, extrapolated to
-      the layer by the exact algorithmic-FLOP ratio;
-    * dense: the blockwise eager attention (modeling_llama.py:235-276 without the N x N
-      matrix) on the same query blocks, extrapolated by the dense FLOP ratio.
-
-    The full layer would take about a minute of CPU time per leg; the sample keeps the
-    default benchmark run within a few minutes."""
+def cpu_baseline(q, k, v, tau, window, arith):
+    """Time the reference's attention math on the GPU box's host cores, in full (no
+    sampling or extrapolation): the CPU restatement of the delta step (selection by the
+    C oracle in the same arithmetic as the GPU step, packing, then the hybrid attention)
+    and of the dense eager attention (modeling_llama.py:235-276), both with torch's
+    fused CPU attention (oracle/cpu_baseline.py), for config 1 (the given layer) and
+    config 0 (B=1, 8 heads, head_dim 64, N=2048, fp32, r=4)."""
     import numpy as np
-    from threadpoolctl import threadpool_limits
+    import torch
+    from oracle import cpu_baseline as CB
     from oracle import delta_oracle as O
     from oracle import select_oracle_c as OC
-    from deltaattention_amd import metrics
+    from deltaattention_amd import synth
 
     cores = min(16, os.cpu_count() or 1)
-    qf = q.float().cpu().numpy()
-    kf = k.float().cpu().numpy()
-    vf = v.float().cpu().numpy()
-    B, Hq, N, D = qf.shape
-    with threadpool_limits(limits=cores):
+    prev_threads = torch.get_num_threads()
+    torch.set_num_threads(cores)
+    o_arith = "fp32" if arith == "fp32" else ("fp16" if k.dtype == torch.float16 else "bf16")
+
+    def delta_and_dense(qc, kc, vc, tau_, W, sel_arith):
+        kf, vf = kc.float().numpy(), vc.float().numpy()
         t0 = time.perf_counter()
-        keep, _ = OC.select_delta(kf, tau, 512)
+        keep, _ = OC.select_delta(kf, tau_, 512, arith=sel_arith)
         p = O.pack(kf, vf, keep)
-        t_compress = time.perf_counter() - t0
-        nqb = (N + 127) // 128
-        blocks = sorted(set(np.linspace(0, nqb - 1, sample_blocks).round().astype(int).tolist()))
-        t0 = time.perf_counter()
-        O.hybrid_attention(qf, kf, vf, p["k_packed"], p["v_packed"], p["timestamps"], p["counts"],
-                           window, q_blocks=blocks)
-        t_sample = time.perf_counter() - t0
-        t0 = time.perf_counter()
-        O.dense_attention(qf, kf, vf, True, q_blocks=blocks)
-        t_dense_sample = time.perf_counter() - t0
-    # algorithmic FLOPs of the sampled blocks
-    n_safe, last, ds = metrics.hybrid_schedule(p["timestamps"], p["P"], N, N, window)
-    G = Hq // kf.shape[1]
-    c = p["anchor_counts"].reshape(B, -1, 1)
-    start = np.arange(nqb)[None, None] * 128
-    rows = np.minimum(128, N - start)
-    pairs = rows * np.minimum(n_safe * 128, c) + rows * (start - ds + 1) + rows * (rows - 1) // 2
-    sample_flops = 4.0 * D * float(pairs[:, :, blocks].sum() * G)
-    t_attn = t_sample * alg_total / sample_flops
-    st = np.asarray(blocks) * 128
-    rb = np.minimum(128, N - st)
-    dense_sample_flops = 4.0 * D * float((rb * st + rb * (rb + 1) // 2).sum()) * B * Hq
-    t_dense = t_dense_sample * dense_total / dense_sample_flops
-    ms = 1e3 * (t_compress + t_attn)
-    return {"value": round(ms, 1), "unit": "ms/layer", "cores": cores, "kind": "port",
+        t1 = time.perf_counter()
+        CB.hybrid_attention(qc, kc, vc, p["k_packed"], p["v_packed"], p["timestamps"], p["counts"], W)
+        t2 = time.perf_counter()
+        CB.dense_attention(qc, kc, vc, True)
+        t3 = time.perf_counter()
+        return (t1 - t0), (t2 - t1), (t3 - t2), p["P"]
+
+    try:
+        qc, kc, vc = q.cpu(), k.cpu(), v.cpu()
+        t_comp, t_hyb, t_dense, P1 = delta_and_dense(qc, kc, vc, tau, window, o_arith)
+        del qc, kc, vc
+        # config 0: the CPU-runnable case of BASELINE.json, fp32, tau calibrated to r = 4 on
+        # its keys by the oracle's selection
+        q0, k0, v0 = synth.make_layer_inputs(1, 8, 8, 2048, 64, rope_base=10000.0, seed=0,
+                                            dtype=torch.float32)
+        k0f = k0.numpy()
+        lo, hi = 0.0, 64.0
+        for _ in range(30):
+            mid = 0.5 * (lo + hi)
+            if OC.select_delta(k0f, mid, 512)[1].sum() > k0f.shape[1] * k0f.shape[2] / 4.0:
+                lo = mid
+            else:
+                hi = mid
+        c0 = delta_and_dense(q0, k0, v0, hi, 128, "fp32")  # fp32 keys: fp32 arithmetic
+    finally:
+        torch.set_num_threads(prev_threads)
+    return {"value": round(1e3 * (t_comp + t_hyb), 1), "unit": "ms/layer", "cores": cores, "kind": "port",
             "dense_value": round(1e3 * t_dense, 1),
+            "select_pack_ms": round(1e3 * t_comp, 1), "hybrid_ms": round(1e3 * t_hyb, 1),
+            "config0": {"delta_ms": round(1e3 * (c0[0] + c0[1]), 2), "dense_ms": round(1e3 * c0[2], 2),
+                        "tau": round(hi, 4), "P": int(c0[3]),
+                        "workload": "B=1 Hq=Hkv=8 D=64 N=2048 fp32 r=4, RoPE 1e4, fp32 selection"},
             "host_cpu_count": os.cpu_count(), "host_cpu": _cpu_model(),
-            "sample": (f"oracle select+pack over all {B * kf.shape[1]} KV heads in full "
-                       f"({1e3 * t_compress:.0f} ms) + hybrid attention for {len(blocks)} of {nqb} "
-                       f"query blocks x {Hq} heads ({t_sample:.1f} s), extrapolated by the "
-                       f"algorithmic-FLOP ratio; dense_value: blockwise dense attention on the same "
-                       f"blocks ({t_dense_sample:.1f} s), extrapolated by the dense FLOP ratio; "
-                       f"numpy/BLAS threads={cores}")}
+            "sample": (f"config 1 in full, no extrapolation: the CPU restatement (oracle/) of the delta "
+                       f"step -- C-oracle selection ({o_arith} arithmetic, as the GPU step) + numpy "
+                       f"packing ({1e3 * t_comp:.0f} ms, P={P1}) + the hybrid attention over every "
+                       f"query block through torch's fused CPU attention ({t_hyb:.1f} s) -- and the "
+                       f"dense eager attention through the same ({t_dense:.1f} s); config 0 likewise "
+                       f"(key 'config0'); torch threads={cores}")}
 
 
 def traffic_bytes(args, N, r_real, ratio):
@@ -170,53 +180,65 @@ def traffic_bytes(args, N, r_real, ratio):
         return None
 
 
-def run_config3(args):
+def config3_record(args, warmup, steps):
     """Config 3: 32-layer Llama-3-8B prefill of one 65536-token sequence, random bf16
     weights ~ N(0, 0.02), uniform token ids; PATH 1 (delta) and PATH 2 (dense) through
-    the same model (modeling swap, llama_swap).  Prints one JSON line."""
+    the same model (modeling swap, llama_swap), ``warmup`` untimed and ``steps`` timed
+    prefills per path.  Returns the record."""
     import torch
     from deltaattention_amd import globVR, llama_swap
     dev = torch.device("cuda:0")
-    N = args.seq or 65536
+    N = args.seq if args.config == 3 and args.seq else 65536
     cfg = llama_swap.llama3_8b_config(llama_swap.DELTA, num_layers=args.e2e_layers)
     log(f"config 3: {args.e2e_layers} layers, N={N}, building the model ...")
+    t0 = time.perf_counter()
     model = llama_swap.random_llama(cfg, dev, seed=args.seed)
     g = torch.Generator().manual_seed(args.seed)
     ids = torch.randint(0, cfg.vocab_size, (1, N), generator=g).to(dev)
-    if args.e2e_mode == "periodic":
-        globVR.packing_mode = "periodic"
-        globVR.target_keep_rate = 1.0 / args.ratio
-    else:
-        globVR.packing_mode = "delta"
-        globVR.row_delta_threshold = args.tau
-        globVR.chunk_size = 512
-    globVR.dense_window_size = args.window
+    torch.cuda.synchronize()
+    log(f"model built in {time.perf_counter() - t0:.1f} s")
+    saved = dict(vars(globVR))
     res = {}
-    for name in (llama_swap.DELTA, llama_swap.DENSE):
-        llama_swap.set_implementation(model, name)
-        with torch.no_grad():
-            for _ in range(args.warmup):
-                model(ids, use_cache=False)
-            torch.cuda.synchronize()
-            times, att = [], []
-            for _ in range(args.steps):
-                llama_swap.reset_attention_time()
+    try:
+        if args.e2e_mode == "periodic":
+            globVR.packing_mode = "periodic"
+            globVR.target_keep_rate = 1.0 / args.ratio
+        else:
+            globVR.packing_mode = "delta"
+            globVR.row_delta_threshold = args.tau
+            globVR.chunk_size = 512
+        globVR.row_delta_arith = args.select_arith
+        globVR.dense_window_size = args.window
+        for name in (llama_swap.DELTA, llama_swap.DENSE):
+            llama_swap.set_implementation(model, name)
+            with torch.no_grad():
+                for _ in range(warmup):
+                    model(ids, use_cache=False)
                 torch.cuda.synchronize()
-                t0 = time.perf_counter()
-                model(ids, use_cache=False)
-                torch.cuda.synchronize()
-                times.append(time.perf_counter() - t0)
-                att.append(llama_swap.attention_time_ms())
-        ms = 1e3 * sum(times) / len(times)
-        res[name] = (ms, sum(att) / len(att))
-        log(f"{name}: {ms:.1f} ms per prefill, attention {res[name][1]:.1f} ms")
+                times, att = [], []
+                for _ in range(steps):
+                    llama_swap.reset_attention_time()
+                    torch.cuda.synchronize()
+                    t0 = time.perf_counter()
+                    model(ids, use_cache=False)
+                    torch.cuda.synchronize()
+                    times.append(time.perf_counter() - t0)
+                    att.append(llama_swap.attention_time_ms())
+            ms = 1e3 * sum(times) / len(times)
+            res[name] = (ms, sum(att) / len(att))
+            log(f"{name}: {ms:.1f} ms per prefill, attention {res[name][1]:.1f} ms")
+    finally:
+        for name, val in saved.items():
+            setattr(globVR, name, val)
+        del model
+        torch.cuda.empty_cache()
     ms_delta, att_delta = res[llama_swap.DELTA]
     ms_dense, att_dense = res[llama_swap.DENSE]
-    rec = {
+    return {
         "metric": "prefill tokens/s, full Llama-3-8B (32 layers), delta attention",
         "value": round(N / (ms_delta * 1e-3), 1),
         "unit": "tokens/s",
-        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "n_gpus": 1, "steps": steps, "warmup": warmup,
         "ms_per_step": round(ms_delta, 2), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "bf16",
         "data": (f"synthetic: random bf16 weights N(0,0.02), {N} uniform token ids, seed "
@@ -232,8 +254,12 @@ def run_config3(args):
         "attention_share_dense": round(att_dense / ms_dense, 4),
         "attention_ms_dense": round(att_dense, 2),
         "speedup_vs_dense": round(ms_dense / ms_delta, 3),
+        "attention_speedup_vs_dense": round(att_dense / att_delta, 3),
     }
-    print(json.dumps(rec), flush=True)
+
+
+def run_config3(args):
+    print(json.dumps(config3_record(args, args.warmup, args.steps)), flush=True)
 
 
 def run_decode(args):
@@ -252,10 +278,11 @@ def run_decode(args):
     B, Hq, Hkv, D, W = 1, 32, 8, 128, args.window
     q, k, v = synth.make_layer_inputs(B, Hq, Hkv, N, D, rope_base=500000.0, seed=args.seed,
                                       device=dev, qv_on_device=True)
-    tau, r_real = synth.calibrate_threshold(k, args.ratio)
+    tau, r_real = synth.calibrate_threshold(k, args.ratio, arith=args.select_arith)
     globVR.row_similarity_metric = "euclidean"
     globVR.row_delta_threshold = tau
-    keep, _ = ops.select(k, tau, 512)
+    globVR.row_delta_arith = args.select_arith
+    keep, _ = ops.select(k, tau, 512, arith=args.select_arith)
     packed = ops.pack(keep, k, v).trimmed()
     P = packed.k_packed.shape[2]
     cfg = types.SimpleNamespace(head_dim=D, num_key_value_heads=Hkv, num_hidden_layers=1,
@@ -372,12 +399,12 @@ def run_decode(args):
     print(json.dumps(rec), flush=True)
 
 
-def run_config4(args):
+def config4_record(args, warmup, steps):
     """Config 4: a packed ragged batch of 8 sequences with N_b ~ U[4096, 32768] tokens,
     AR(1) keys with rho ~ U[0.6, 0.95] per (sequence, KV head), one tau calibrated to r
     on the whole batch.  ops.delta_prefill_varlen runs every sequence as a B = 1 delta
     prefill with one launch per stage over the whole batch (cu_seqlens on the device),
-    against the dense varlen prefill (one launch).  Prints one JSON line."""
+    against the dense varlen prefill (one launch).  Returns the record."""
     import numpy as np
     import torch
     from deltaattention_amd import ops, synth
@@ -398,46 +425,90 @@ def run_config4(args):
     cu = [0] + np.cumsum(lens).tolist()
     T = cu[-1]
     log(f"config 4: lens {lens}, {T} tokens")
-    tau, _ = synth.calibrate_threshold(k.permute(1, 0, 2).unsqueeze(0), args.ratio)
+    tau, _ = synth.calibrate_threshold(k.permute(1, 0, 2).unsqueeze(0), args.ratio, arith=args.select_arith)
     vb = ops.varlen_batch(cu, T, dev)
-    keep, _ = ops.select_varlen(k, vb, tau, 512)
+    keep, _ = ops.select_varlen(k, vb, tau, 512, arith=args.select_arith)
     r_real = T * Hkv / int(keep.sum().item())
 
     def delta():
-        return ops.delta_prefill_varlen(q, k, v, vb, tau, 512, window=args.window)
+        return ops.delta_prefill_varlen(q, k, v, vb, tau, 512, window=args.window, arith=args.select_arith)
 
     def dense():
         return ops.dense_prefill_varlen(q, k, v, vb)
 
     res = {}
     for name, fn in (("delta", delta), ("dense", dense)):
-        for _ in range(args.warmup):
+        for _ in range(warmup):
             fn()
         torch.cuda.synchronize()
         t0 = time.perf_counter()
-        for _ in range(args.steps):
+        for _ in range(steps):
             fn()
         torch.cuda.synchronize()
-        res[name] = 1e3 * (time.perf_counter() - t0) / args.steps
+        res[name] = 1e3 * (time.perf_counter() - t0) / steps
         log(f"{name}: {res[name]:.2f} ms per batch")
-    rec = {
+    return {
         "metric": "ragged-batch prefill attention tokens/s (8 sequences, varlen), delta",
         "value": round(T / (res["delta"] * 1e-3), 1),
         "unit": "tokens/s",
-        "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "n_gpus": 1, "steps": steps, "warmup": warmup,
         "ms_per_step": round(res["delta"], 3), "higher_is_better": True, "scaling": "weak",
         "vs_baseline": None, "dtype": "bf16",
         "data": (f"synthetic: AR(1) keys with rho~U[0.6,0.95] per sequence and KV head, RoPE "
                  f"base 5e5, Gaussian Q/V, seed {args.seed}; Euclidean tau={tau:.4f} calibrated "
-                 f"to r={args.ratio:g} on the batch (realised {r_real:.3f}), chunk 512, W={args.window}"),
+                 f"to r={args.ratio:g} on the batch (realised {r_real:.3f}, {args.select_arith} "
+                 f"selection), chunk 512, W={args.window}"),
         "config": {"workload": f"config4: varlen B=8 lens {lens}, Hq={Hq} Hkv={Hkv} D={D} bf16 causal",
                    "seq_len": T, "global_batch": 8, "parallelism": "none (1 GPU)"},
+        "delta_ms_per_batch": round(res["delta"], 3),
         "dense_tokens_per_s": round(T / (res["dense"] * 1e-3), 1),
-        "dense_ms_per_step": round(res["dense"], 3),
+        "dense_ms_per_batch": round(res["dense"], 3),
         "speedup_vs_dense": round(res["dense"] / res["delta"], 3),
         "realised_ratio": round(r_real, 3),
     }
-    print(json.dumps(rec), flush=True)
+
+
+def run_config4(args):
+    print(json.dumps(config4_record(args, args.warmup, args.steps)), flush=True)
+
+
+def measure_peaks():
+    """On-box ceilings for the roofline fractions: the bf16 MFMA rate of an issue loop
+    with no memory traffic (libdeltaattn_diag.so: 1024 workgroups x 8 waves x 32 MFMAs per
+    round), and the HBM bandwidth of a 4 GiB device-to-device copy (bytes read + written),
+    each the best of 5 timed launches after a warm-up."""
+    import torch
+    here = os.path.dirname(os.path.abspath(__file__))
+    lib = ctypes.CDLL(os.path.join(here, "deltaattention_amd", "libdeltaattn_diag.so"))
+    lib.diag_mfma_loop.restype = ctypes.c_int
+    lib.diag_mfma_loop.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
+    grid, iters = 1024, 2000
+    sink = torch.empty(grid * 512, dtype=torch.float32, device="cuda")
+    stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
+
+    def mfma():
+        rc = lib.diag_mfma_loop(ctypes.c_void_p(sink.data_ptr()), iters, grid, stream)
+        if rc != 0:
+            raise RuntimeError(f"diag_mfma_loop failed ({rc})")
+
+    mfma()
+    best = min(time_loop(mfma, 1) for _ in range(5))
+    flops = grid * 8 * iters * 32 * 32768.0
+    n = 1 << 31  # 2^31 bf16 elements: 4 GiB
+    src = torch.empty(n, dtype=torch.bfloat16, device="cuda").fill_(1.0)
+    dst = torch.empty_like(src)
+    copy = lambda: dst.copy_(src)
+    copy()
+    best_copy = min(time_loop(copy, 1) for _ in range(5))
+    del src, dst, sink
+    torch.cuda.empty_cache()
+    mfma_tf = flops / (best * 1e-3) / 1e12
+    copy_gbs = 2.0 * n * 2 / (best_copy * 1e-3) / 1e9
+    log(f"peaks: MFMA loop {mfma_tf:.0f} TFLOP/s, copy {copy_gbs:.0f} GB/s")
+    return {"mfma_bf16_tflops": round(mfma_tf, 1), "mfma_frac_of_published": round(mfma_tf / BF16_PEAK_TFLOPS, 4),
+            "copy_gbs": round(copy_gbs, 1), "copy_frac_of_published": round(copy_gbs / HBM_PEAK_GBS, 4),
+            "note": "MFMA: v_mfma_f32_32x32x16_bf16 issue loop, no memory traffic; copy: 4 GiB "
+                    "device-to-device, read + write bytes"}
 
 
 def main():
@@ -464,14 +535,48 @@ def main():
     if args.only:
         run_only(args)
         return
+    import torch
+    t_start = time.perf_counter()
     N = args.seq or (32768 if args.config == 1 else 131072)
     head = measure_layer(args, N, args.ratio, headline=True)
     rec = head.pop("record")
-    if args.config == 1 and not args.no_128k and not args.seq:
-        log("config 2 (N=131072, r=4) ...")
-        extra = measure_layer(args, 131072, 4.0, headline=False)
-        extra.pop("record", None)
-        rec["config2_r4"] = extra
+    cpu_inputs = head.pop("cpu_inputs")
+    torch.cuda.empty_cache()
+    full = args.config == 1 and not args.seq
+    if full and not args.no_128k:
+        # config 2: one set of N = 131072 inputs, tau calibrated per ratio; the dense and
+        # SDPA controls do not depend on r and are timed once
+        q, k, v = layer_inputs(args, 131072)
+        shared = {}
+        for r in (4.0, 2.0, 8.0):
+            log(f"config 2 (N=131072, r={r:g}) ...")
+            extra = measure_layer(args, 131072, r, headline=False, inputs=(q, k, v), shared=shared)
+            rec[f"config2_r{int(r)}"] = extra
+        del q, k, v, shared
+        torch.cuda.empty_cache()
+    if full and not args.no_e2e:
+        c4 = config4_record(args, warmup=3, steps=10)
+        rec["config4"] = {key: c4[key] for key in (
+            "delta_ms_per_batch", "dense_ms_per_batch", "speedup_vs_dense", "value", "unit",
+            "dense_tokens_per_s", "realised_ratio", "steps", "warmup")}
+        rec["config4"]["workload"] = c4["config"]["workload"]
+        torch.cuda.empty_cache()
+        c3 = config3_record(args, warmup=1, steps=1)
+        rec["config3"] = {key: c3[key] for key in (
+            "value", "unit", "ms_per_step", "dense_tokens_per_s", "dense_ms_per_step", "speedup_vs_dense",
+            "attention_ms_delta", "attention_share_delta", "attention_ms_dense", "attention_share_dense",
+            "attention_speedup_vs_dense", "steps", "warmup")}
+        rec["config3"]["workload"] = c3["config"]["workload"] + f", anchors {args.e2e_mode} r={args.ratio:g}"
+        torch.cuda.empty_cache()
+    if full:
+        rec["peaks_measured"] = measure_peaks()
+        pk = rec["peaks_measured"]
+        rec["roofline"]["frac_of_measured_peak"] = round(rec["roofline"]["achieved"] / pk["mfma_bf16_tflops"], 4)
+        rec["compress_frac_of_measured_copy"] = round(rec["compress_gbs"] / pk["copy_gbs"], 4)
+    if not args.no_cpu_baseline:
+        log("cpu baseline (config 1 and config 0 in full) ...")
+        rec["cpu_baseline"] = cpu_baseline(*cpu_inputs, args.window, args.select_arith)
+    rec["bench_wall_s"] = round(time.perf_counter() - t_start, 1)
     print(json.dumps(rec), flush=True)
 
 
@@ -547,25 +652,29 @@ def sdpa_ms(q, k, v, iters):
         del ke, ve
 
 
-def measure_layer(args, N, ratio, headline):
+def measure_layer(args, N, ratio, headline, inputs=None, shared=None):
     """One Llama-3-8B attention layer (B=1, Hq=32, Hkv=8, D=128) at N tokens and
     compression r: the contract's timed steps of the full delta step (select -> pack ->
     hybrid) when ``headline``, then per-part HIP-event timings of the hybrid, dense,
-    compression and torch SDPA launches, the roofline of the hybrid kernel and (headline
-    only) the CPU baseline.  Returns a dict; ``record`` holds the JSON line's fields."""
+    compression, selection and torch SDPA launches and the roofline of the hybrid
+    kernel.  ``shared`` carries the r-independent dense / SDPA timings between calls at
+    the same N.  Returns a dict; with ``headline``, ``record`` holds the JSON line's
+    fields and ``cpu_inputs`` the layer for the CPU baseline."""
     import torch
     from deltaattention_amd import metrics, ops, synth
     W = args.window
+    arith = args.select_arith
+    other = "fp32" if arith == "native" else "native"
     B, Hq, Hkv, D = 1, 32, 8, 128
-    log(f"layer: N={N} r={ratio} W={W}")
-    q, k, v = layer_inputs(args, N)
-    tau, r_real = synth.calibrate_threshold(k, ratio)
+    log(f"layer: N={N} r={ratio} W={W} select={arith}")
+    q, k, v = inputs if inputs is not None else layer_inputs(args, N)
+    tau, r_real = synth.calibrate_threshold(k, ratio, arith=arith)
     log(f"calibrated tau={tau:.4f} realised r={r_real:.3f}")
 
     def step():
-        return ops.delta_prefill(q, k, v, tau, 512, window=W)
+        return ops.delta_prefill(q, k, v, tau, 512, window=W, arith=arith)
 
-    keep, _ = ops.select(k, tau, 512)
+    keep, _ = ops.select(k, tau, 512, arith=arith)
     packed = ops.pack(keep, k, v)
     torch.cuda.synchronize()
     P = int(packed.num_packed.item())
@@ -582,7 +691,7 @@ def measure_layer(args, N, ratio, headline):
         ops.dense_prefill(q, k, v, causal=True, out=out_d)
 
     def compress_only():
-        kk, _ = ops.select(k, tau, 512)
+        kk, _ = ops.select(k, tau, 512, arith=arith)
         ops.pack(kk, k, v, out=packed)
 
     steps = args.steps if headline else max(3, min(args.steps, 10))
@@ -597,15 +706,25 @@ def measure_layer(args, N, ratio, headline):
     log(f"delta step {ms_step:.3f} ms")
 
     iters = max(3, steps)
+    shared = {} if shared is None else shared
     for _ in range(2):
-        hybrid_only(); dense_only(); compress_only()
+        hybrid_only(); compress_only()
     ms_hybrid = time_loop(hybrid_only, iters)
-    ms_dense = time_loop(dense_only, iters)
+    if "dense_ms" not in shared:
+        dense_only()
+        shared["dense_ms"] = time_loop(dense_only, iters)
+        shared["sdpa_ms"] = sdpa_ms(q, k, v, max(3, iters // 3)) if not args.no_sdpa else None
+    ms_dense, ms_sdpa = shared["dense_ms"], shared["sdpa_ms"]
     ms_compress = time_loop(compress_only, iters)
     cold_med, cold_mean = cold_calls_ms(compress_only)
-    ms_sdpa = sdpa_ms(q, k, v, max(3, iters // 3)) if not args.no_sdpa else None
+    # the selection kernel alone, in the timed arithmetic and in the other definition (its
+    # own tau, calibrated to the same r)
+    tau_o, _ = synth.calibrate_threshold(k, ratio, arith=other)
+    sel = {arith: time_loop(lambda: ops.select(k, tau, 512, arith=arith), iters),
+           other: time_loop(lambda: ops.select(k, tau_o, 512, arith=other), iters)}
     log(f"hybrid {ms_hybrid:.3f} ms  dense {ms_dense:.3f} ms  compress {ms_compress:.4f} ms "
-        f"(caches flushed: median {cold_med:.4f}, mean {cold_mean:.4f})  "
+        f"(caches flushed: median {cold_med:.4f}, mean {cold_mean:.4f})  select native "
+        f"{1e3 * sel['native']:.1f} us fp32 {1e3 * sel['fp32']:.1f} us  "
         f"sdpa {ms_sdpa if ms_sdpa is None else round(ms_sdpa, 3)} ms")
 
     fl = metrics.hybrid_flops(ts_h, c_h, P, N, Hq, D, W)
@@ -616,6 +735,7 @@ def measure_layer(args, N, ratio, headline):
     best_dense = min(ms_dense, ms_sdpa) if ms_sdpa else ms_dense
     res = {
         "seq_len": N, "ratio": ratio, "realised_ratio": round(r_real, 3), "tau": round(tau, 4),
+        "select_arith": arith,
         "delta_ms_per_layer": round(ms_step, 4),
         "speedup_vs_dense": round(ms_dense / ms_step, 3),
         "kernel_speedup_vs_dense": round(ms_dense / ms_hybrid, 3),
@@ -623,12 +743,15 @@ def measure_layer(args, N, ratio, headline):
         "sdpa_ms_per_layer": None if ms_sdpa is None else round(ms_sdpa, 4),
         "speedup_vs_best_dense": round(best_dense / ms_step, 3),
         "hybrid_kernel_ms": round(ms_hybrid, 4),
+        "hybrid_algorithmic_flops": fl["algorithmic"],
         "compress_ms": round(ms_compress, 4),
         "compress_gbs": round(cbytes / (ms_compress * 1e-3) / 1e9, 1),
         "compress_hbm_frac": round(cbytes / (ms_compress * 1e-3) / 1e9 / HBM_PEAK_GBS, 4),
         "compress_cold_ms_median": round(cold_med, 4),
         "compress_cold_ms_mean": round(cold_mean, 4),
         "compress_cold_gbs": round(cbytes / (cold_med * 1e-3) / 1e9, 1),
+        "select_native_us": round(1e3 * sel["native"], 2),
+        "select_fp32_us": round(1e3 * sel["fp32"], 2),
         "hybrid_tflops": round(hyb_tflops, 1),
         "hybrid_mfma_frac": round(hyb_tflops / BF16_PEAK_TFLOPS, 4),
         "dense_tflops": round(dense_tflops, 1),
@@ -637,6 +760,15 @@ def measure_layer(args, N, ratio, headline):
     if not headline:
         res["traffic"] = traffic_bytes(args, N, r_real, ratio)
         return res
+    # the whole step in the other selection definition, for comparison
+    for _ in range(3):
+        ops.delta_prefill(q, k, v, tau_o, 512, window=W, arith=other)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        ops.delta_prefill(q, k, v, tau_o, 512, window=W, arith=other)
+    torch.cuda.synchronize()
+    res[f"delta_ms_per_layer_{other}"] = round(1e3 * (time.perf_counter() - t0) / steps, 4)
     rec = {
         "metric": "prefill attn ms/layer + speedup vs dense FA at 32K/128K, Llama-3-8B GQA",
         "value": round(ms_step, 4),
@@ -651,7 +783,7 @@ def measure_layer(args, N, ratio, headline):
         "dtype": args.dtype,
         "data": (f"synthetic: AR(1) keys rho=0.9 sigma=0.44 + RoPE base 5e5, Gaussian Q/V, "
                  f"seed {args.seed}; Euclidean tau={tau:.4f} calibrated to r={ratio:g} "
-                 f"(realised {r_real:.3f}), chunk 512, W={W}"),
+                 f"(realised {r_real:.3f}) in the {arith} selection arithmetic, chunk 512, W={W}"),
         "config": {"workload": (f"config{args.config}: delta prefill attention, one layer, "
                                 f"B={B} Hq={Hq} Hkv={Hkv} D={D} N={N} {args.dtype} causal r={ratio:g}"),
                    "seq_len": N, "global_batch": B, "parallelism": "none (1 GPU)"},
@@ -661,12 +793,9 @@ def measure_layer(args, N, ratio, headline):
                      "kernel": "attn_w64_kernel<hybrid> (da_hybrid_prefill)",
                      "algorithmic_flops": fl["algorithmic"]},
     }
-    rec.update({k2: v2 for k2, v2 in res.items() if k2 not in ("seq_len",)})
-    if not args.no_cpu_baseline:
-        log("cpu baseline (oracle sample) ...")
-        rec["cpu_baseline"] = cpu_baseline(q, k, v, tau, W, fl["algorithmic"], dense_fl,
-                                           args.cpu_sample_blocks)
+    rec.update({k2: v2 for k2, v2 in res.items() if k2 not in ("seq_len", "hybrid_algorithmic_flops")})
     res["record"] = rec
+    res["cpu_inputs"] = (q.cpu(), k.cpu(), v.cpu(), tau)
     return res
 
 
@@ -677,17 +806,17 @@ def run_only(args):
     N = args.seq or (32768 if args.config == 1 else 131072)
     W = args.window
     q, k, v = layer_inputs(args, N)
-    tau, r_real = synth.calibrate_threshold(k, args.ratio)
-    keep, _ = ops.select(k, tau, 512)
+    tau, r_real = synth.calibrate_threshold(k, args.ratio, arith=args.select_arith)
+    keep, _ = ops.select(k, tau, 512, arith=args.select_arith)
     packed = ops.pack(keep, k, v)
     out = torch.empty_like(q)
     fns = {
-        "delta": lambda: ops.delta_prefill(q, k, v, tau, 512, window=W),
+        "delta": lambda: ops.delta_prefill(q, k, v, tau, 512, window=W, arith=args.select_arith),
         "hybrid": lambda: ops.hybrid_prefill(q, k, v, packed.k_packed, packed.v_packed,
                                              packed.timestamps, packed.counts, window=W,
                                              num_packed_dev=packed.num_packed, out=out),
         "dense": lambda: ops.dense_prefill(q, k, v, causal=True, out=out),
-        "compress": lambda: ops.pack(ops.select(k, tau, 512)[0], k, v, out=packed),
+        "compress": lambda: ops.pack(ops.select(k, tau, 512, arith=args.select_arith)[0], k, v, out=packed),
     }
     if args.only == "copy":
         src = torch.randint(0, 1000, (1 << 29,), dtype=torch.int16, device=q.device)  # 1 GiB

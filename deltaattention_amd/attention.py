@@ -87,7 +87,7 @@ def keep_mask(key_states: torch.Tensor):
                                     chunk_size=fixed if fixed > 0 else 0,
                                     divide_to=0 if fixed > 0 else divide_to,
                                     metric=getattr(globVR, "row_similarity_metric", "euclidean"),
-                                    arith=getattr(globVR, "row_delta_arith", "fp32"))
+                                    arith=getattr(globVR, "row_delta_arith", "native"))
     return keep, chunk_counts.sum(dim=-1, dtype=torch.int32)
 
 
@@ -154,7 +154,7 @@ def delta_decode_handoff(key_states: torch.Tensor, value_states: torch.Tensor, l
                          chunk_size=fixed if fixed > 0 else 0,
                          divide_to=0 if fixed > 0 else divide_to,
                          metric=getattr(globVR, "row_similarity_metric", "euclidean"),
-                         arith=getattr(globVR, "row_delta_arith", "fp32"))
+                         arith=getattr(globVR, "row_delta_arith", "native"))
     packed = ops.pack(keep, key_states, value_states)               # :836-866
     _handoff(past_key_value, layer_idx, packed, key_states, value_states)   # :868-879
 

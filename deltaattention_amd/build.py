@@ -16,6 +16,9 @@ from concurrent.futures import ThreadPoolExecutor
 HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libdeltaattn.so")
+# bench.py's on-box ceilings (an MFMA issue loop); not part of the product ABI
+DIAG_SRC = os.path.join(HERE, "diag", "peaks.hip")
+DIAG_LIB = os.path.join(HERE, "libdeltaattn_diag.so")
 ARCH = os.environ.get("DELTAATTN_ARCH", "gfx950")
 
 # -packed-fp32-ops: never emit v_pk_{add,mul,fma}_f32.
@@ -130,8 +133,31 @@ def compile_checked(src: str, obj: str, verbose: bool = False) -> list[dict]:
     return kernels
 
 
+def _link(objs: list[str], lib: str) -> None:
+    tmp_lib = lib + ".tmp"
+    cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp_lib, *objs]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError("link failed:\n" + r.stdout + r.stderr)
+    os.replace(tmp_lib, lib)
+
+
+def build_diag(verbose: bool = False) -> str:
+    """Compile libdeltaattn_diag.so (the MFMA issue loop bench.py measures the on-box
+    bf16 ceiling with), under the same register-only check; returns its path."""
+    with tempfile.TemporaryDirectory(prefix="deltaattn_diag_") as tmp:
+        obj = os.path.join(tmp, "peaks.o")
+        ks = compile_checked(DIAG_SRC, obj, verbose=verbose)
+        if verbose:
+            for k in ks:
+                print(resource_line(k), file=sys.stderr)
+        _link([obj], DIAG_LIB)
+    return DIAG_LIB
+
+
 def build(verbose: bool = False) -> str:
-    """Compile every HIP source and link libdeltaattn.so; returns its path.  Raises
+    """Compile every HIP source and link libdeltaattn.so (and the diagnostics library);
+    returns the product library's path.  Raises
     ResourceError (and links nothing) if any kernel uses scratch memory, spills VGPRs or
     has a dynamic stack; prints one resource line per kernel when ``verbose``."""
     srcs = sources()
@@ -146,12 +172,8 @@ def build(verbose: bool = False) -> str:
             for _, ks in results:
                 for k in ks:
                     print(resource_line(k), file=sys.stderr)
-        tmp_lib = LIB + ".tmp"
-        cmd = [_hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-o", tmp_lib, *objs]
-        r = subprocess.run(cmd, capture_output=True, text=True)
-        if r.returncode != 0:
-            raise RuntimeError("link failed:\n" + r.stdout + r.stderr)
-        os.replace(tmp_lib, LIB)
+        _link(objs, LIB)
+    build_diag(verbose=verbose)
     return LIB
 
 

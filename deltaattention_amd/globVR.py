@@ -19,7 +19,8 @@ row_similarity_metric = "cos"
 divide_to = 1
 chunk_size = 0                  # 0 = use divide_to; >0 = fixed tokens per chunk
 packing_mode = "delta"          # "delta" | "random" | "periodic"
-row_delta_arith = "fp32"        # Euclidean distance in "fp32" or the keys' "native" 16-bit arithmetic
+row_delta_arith = "native"      # Euclidean distance in the keys' "native" 16-bit arithmetic
+                                # (tritonModules.py:55-58) or in "fp32"
 target_keep_rate = 0.5          # used by the random and periodic packing modes
 
 # hybrid kernel variants (modeling_llama.py:716-749)

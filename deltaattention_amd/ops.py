@@ -73,15 +73,16 @@ def _select_flags(metric: str, arith: str) -> int:
 def select(k: torch.Tensor, threshold: float, chunk_size: int = 512, divide_to: int = 0,
            metric: str = "euclidean", keep: Optional[torch.Tensor] = None,
            chunk_counts: Optional[torch.Tensor] = None,
-           arith: str = "fp32") -> Tuple[torch.Tensor, torch.Tensor]:
+           arith: str = "native") -> Tuple[torch.Tensor, torch.Tensor]:
     """Delta-mode anchor selection (tritonModules.py:7-69 via modeling_llama.py:634-653).
 
     ``metric == "cosine"`` selects the cosine test (keep iff cos < threshold); every
     other string is Euclidean (keep iff ||k - anchor||^2 > threshold^2), exactly as
-    modeling_llama.py:639-642.  ``arith="native"`` evaluates the Euclidean distance in
-    the keys' own 16-bit arithmetic (every difference, square and tree addition rounded,
-    as the reference's Triton code does on bf16 / fp16 keys, tritonModules.py:55-58);
-    the default "fp32" keeps them in fp32.  Both reduce over the same fixed tree.
+    modeling_llama.py:639-642.  The default ``arith="native"`` evaluates the Euclidean
+    distance in the keys' own 16-bit arithmetic (every difference, square and tree
+    addition rounded, as the reference's Triton code does on bf16 / fp16 keys,
+    tritonModules.py:55-58); "fp32" keeps them in fp32.  Both reduce over the same fixed
+    tree.
     Returns keep [B, Hkv, N] int32 and chunk counts [B, Hkv, num_chunks] int32.
     """
     _require_device(k)
@@ -250,7 +251,7 @@ def delta_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, threshold: 
                   window: int = 128, scale: Optional[float] = None, variant: str = "hybrid",
                   no_count: bool = False, keep: Optional[torch.Tensor] = None,
                   return_packed: bool = False, out: Optional[torch.Tensor] = None,
-                  arith: str = "fp32"):
+                  arith: str = "native"):
     """select -> pack -> hybrid prefill with P kept on the device (no host sync).
 
     Restates PATH 1 of LlamaAttention.forward (modeling_llama.py:600-749) for the delta
@@ -311,7 +312,7 @@ def _check_varlen(q, k, v):
 
 
 def select_varlen(k: torch.Tensor, cu_seqlens, threshold: float, chunk_size: int = 512,
-                  divide_to: int = 0, metric: str = "euclidean", arith: str = "fp32",
+                  divide_to: int = 0, metric: str = "euclidean", arith: str = "native",
                   max_seqlen: Optional[int] = None) -> Tuple[torch.Tensor, torch.Tensor]:
     """Delta-mode selection of every sequence of a ragged batch in one launch: k [T, Hkv, D]
     -> keep [Hkv, T] int32, chunk counts [B, Hkv, max_chunks] int32.  Each sequence is
@@ -431,7 +432,7 @@ def delta_prefill_varlen(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_s
                          threshold: float, chunk_size: int = 512, divide_to: int = 0,
                          metric: str = "euclidean", window: int = 128,
                          scale: Optional[float] = None, variant: str = "hybrid",
-                         no_count: bool = False, arith: str = "fp32",
+                         no_count: bool = False, arith: str = "native",
                          max_seqlen: Optional[int] = None, return_packed: bool = False):
     """Delta prefill of a packed ragged batch: q [T, Hq, D], k, v [T, Hkv, D] with the
     sequences at cu_seqlens -> out [T, Hq, D].

@@ -72,16 +72,18 @@ def make_layer_inputs(batch: int, q_heads: int, kv_heads: int, seq_len: int, hea
 
 def calibrate_threshold(k: torch.Tensor, ratio: float, chunk_size: int = 512,
                         metric: str = "euclidean", iters: int = 40,
-                        lo: float = 0.0, hi: Optional[float] = None) -> Tuple[float, float]:
+                        lo: float = 0.0, hi: Optional[float] = None,
+                        arith: str = "native") -> Tuple[float, float]:
     """Smallest Euclidean tau whose realised keep rate is <= 1/ratio, by bisection with
-    the GPU selection kernel.  Returns (tau, realised ratio N*H / sum c)."""
+    the GPU selection kernel in the given arithmetic.  Returns (tau, realised ratio
+    N*H / sum c)."""
     from . import ops
 
     target = 1.0 / ratio
     total = k.shape[0] * k.shape[1] * k.shape[2]
 
     def keep_rate(tau):
-        _, cc = ops.select(k, tau, chunk_size, 0, metric)
+        _, cc = ops.select(k, tau, chunk_size, 0, metric, arith=arith)
         return float(cc.sum().item()) / total
 
     if hi is None:

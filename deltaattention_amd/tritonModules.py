@@ -55,13 +55,14 @@ class _ChunkedEval(KernelLauncher):
 
 
 def _flags(use_cosine: bool) -> int:
-    """da_select flags: the cosine test, or the Euclidean distance in fp32 or (with
-    globVR.row_delta_arith == "native") in the keys' 16-bit arithmetic."""
+    """da_select flags: the cosine test, or the Euclidean distance in the keys' 16-bit
+    arithmetic as the replaced kernel computes it (tritonModules.py:55-58; the default,
+    globVR.row_delta_arith == "native") or in fp32 (globVR.row_delta_arith == "fp32")."""
     from . import globVR
     from ._native import DA_SELECT_ARITH16, DA_SELECT_COSINE
     if use_cosine:
         return DA_SELECT_COSINE
-    return DA_SELECT_ARITH16 if getattr(globVR, "row_delta_arith", "fp32") == "native" else 0
+    return DA_SELECT_ARITH16 if getattr(globVR, "row_delta_arith", "native") == "native" else 0
 
 
 class _ScatterPack(KernelLauncher):

@@ -26,3 +26,11 @@ def gpu():
 def announce(msg: str) -> None:
     """Name the case before a GPU step, so a fault that ends the process is attributable."""
     print(f"[case] {msg}", flush=True)
+
+
+def oracle_arith(keys) -> str:
+    """The oracle's name for the product's default selection arithmetic on these keys:
+    "native" evaluates the Euclidean distance in the keys' own 16-bit type
+    (tritonModules.py:55-58), which the oracle calls "bf16" or "fp16"."""
+    import torch
+    return "fp16" if keys.dtype == torch.float16 else "bf16"

@@ -24,7 +24,7 @@ import numpy as np
 import pytest
 import torch
 
-from conftest import announce
+from conftest import announce, oracle_arith
 from oracle import delta_oracle as O
 from oracle import select_oracle_c as OC
 
@@ -57,7 +57,7 @@ def _rows(blocks, N):
 def _check_select_pack(kg, vg, tau, keep, packed, what):
     """Keep mask, chunk counts and every packed tensor bit-exact against the oracle."""
     kf, vf = kg.float().cpu().numpy(), vg.float().cpu().numpy()
-    ref_keep, _ = OC.select_delta(kf, tau, 512)
+    ref_keep, _ = OC.select_delta(kf, tau, 512, arith=oracle_arith(kg))
     got_keep = keep.cpu().numpy()
     assert np.array_equal(got_keep, ref_keep), f"{what}: keep differs at {np.argwhere(got_keep != ref_keep)[:5]}"
     ref = O.pack(kf, vf, ref_keep)
@@ -152,7 +152,7 @@ def test_other_head_dims(gpu, D):
         out, packed = ops.delta_prefill(q, k, v, 8.0 * (D / 128) ** 0.5, 512, window=128,
                                         return_packed=True)
         kf, vf = k.float().cpu().numpy(), v.float().cpu().numpy()
-        keep, _ = OC.select_delta(kf, 8.0 * (D / 128) ** 0.5, 512)
+        keep, _ = OC.select_delta(kf, 8.0 * (D / 128) ** 0.5, 512, arith=oracle_arith(k))
         p = O.pack(kf, vf, keep)
         want = O.hybrid_attention(q.float().cpu().numpy(), kf, vf, p["k_packed"], p["v_packed"],
                                   p["timestamps"], p["counts"], 128)
@@ -265,7 +265,7 @@ def test_config4_varlen(gpu):
         n = e - s
         sl = lambda x: x[s:e].permute(1, 0, 2).unsqueeze(0)
         kf, vf = sl(k).float().cpu().numpy(), sl(v).float().cpu().numpy()
-        keep, _ = OC.select_delta(kf, tau, 512)
+        keep, _ = OC.select_delta(kf, tau, 512, arith=oracle_arith(k))
         ref = O.pack(kf, vf, keep)
         blocks = _spread((n + 127) // 128, 3)
         rows = _rows(blocks, n)

@@ -10,7 +10,7 @@ import numpy as np
 import pytest
 import torch
 
-from conftest import announce
+from conftest import announce, oracle_arith
 from oracle import delta_oracle as O
 from oracle import select_oracle_c as OC
 import test_gpu_dropin as T
@@ -60,7 +60,7 @@ def test_random_decode_vs_oracle(gpu, c):
         qg, kg, vg = q.to(gpu), k.to(gpu), v.to(gpu)
         attention.delta_prefill_attention(qg[:, :, :N], kg[:, :, :N], vg[:, :, :N], 0, cache)
         kf, vf = k.float().numpy(), v.float().numpy()
-        keep, _ = OC.select_delta(kf[:, :, :N], c["tau"], 512, 0, c["metric"])
+        keep, _ = OC.select_delta(kf[:, :, :N], c["tau"], 512, 0, c["metric"], arith=oracle_arith(k))
         p = O.pack(kf[:, :, :N], vf[:, :, :N], keep)
         st = T._oracle_cache_from_prefill(p, kf[:, :, :N], vf[:, :, :N], W, cache.capacity + 4096)
         fused = np.random.default_rng(c["pattern"]).random(steps) < 0.5

@@ -4,7 +4,7 @@ import numpy as np
 import pytest
 import torch
 
-from conftest import announce
+from conftest import announce, oracle_arith
 from oracle import delta_oracle as O
 from oracle import select_oracle_c as OC
 
@@ -63,7 +63,7 @@ def test_select_and_pack_kernel_objects(gpu):
     chunked_eval_kernel[(bsz * H, num_chunks)](
         kg, keep_mask, chunk_counts, 9.0 ** 2, *kg.stride(), *keep_mask.stride(),
         *chunk_counts.stride(), q_len, D, chunk_size, num_heads=H, BLOCK_D=128, USE_COSINE=False)
-    ok, occ = OC.select_delta(k.float().numpy(), 9.0, 512)
+    ok, occ = OC.select_delta(k.float().numpy(), 9.0, 512, arith=oracle_arith(k))
     assert (keep_mask.cpu().numpy() == ok).all() and (chunk_counts.cpu().numpy() == occ).all()
     index_map = (torch.cumsum(keep_mask, dim=-1) - 1).to(torch.int32)
     P = int(chunk_counts.sum(-1).max().item())
@@ -136,7 +136,7 @@ def test_delta_prefill_attention_glue(gpu, mode):
         announce(f"delta_prefill_attention mode={mode}")
         out = attention.delta_prefill_attention(q.to(gpu), k.to(gpu), v.to(gpu))
         kf, vf = k.float().numpy(), v.float().numpy()
-        keep = OC.select_delta(kf, 9.0, 512)[0] if mode == "delta" else O.select_periodic(1, 2, 1500, 0.3)
+        keep = OC.select_delta(kf, 9.0, 512, arith=oracle_arith(k))[0] if mode == "delta" else O.select_periodic(1, 2, 1500, 0.3)
         p = O.pack(kf, vf, keep)
         ref = O.hybrid_attention(q.float().numpy(), kf, vf, p["k_packed"], p["v_packed"],
                                  p["timestamps"], p["counts"], 128)
@@ -193,7 +193,7 @@ def test_decode_cache_matches_oracle(gpu, metric, tau, dtype):
         announce(f"decode {metric}: prefill hand-off")
         attention.delta_prefill_attention(qg[:, :, :N], kg[:, :, :N], vg[:, :, :N], 0, cache)
         kf, vf = k.float().numpy(), v.float().numpy()
-        keep, _ = OC.select_delta(kf[:, :, :N], tau, 512, 0, metric)
+        keep, _ = OC.select_delta(kf[:, :, :N], tau, 512, 0, metric, arith=oracle_arith(k))
         p = O.pack(kf[:, :, :N], vf[:, :, :N], keep)
         st = _oracle_cache_from_prefill(p, kf[:, :, :N], vf[:, :, :N], W, cache.capacity + 4096)
         outs = []

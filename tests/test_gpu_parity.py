@@ -9,7 +9,7 @@ import numpy as np
 import pytest
 import torch
 
-from conftest import announce
+from conftest import announce, oracle_arith
 from oracle import delta_oracle as O
 from oracle import select_oracle_c as OC
 
@@ -52,7 +52,7 @@ def test_select_bitexact(gpu, metric, tau, chunk, divide_to):
     announce(f"select {metric} tau={tau} chunk={chunk} divide_to={divide_to} N=3000")
     keep, cc = ops.select(k.to(gpu), tau, chunk, divide_to, metric)
     torch.cuda.synchronize()
-    ok, occ = OC.select_delta(k.float().numpy(), tau, chunk, divide_to, metric)
+    ok, occ = OC.select_delta(k.float().numpy(), tau, chunk, divide_to, metric, arith=oracle_arith(k))
     keep_h = keep.cpu().numpy()
     cc_h = cc.cpu().numpy()
     assert (cc_h == occ).all(), "chunk counts differ"
@@ -66,7 +66,7 @@ def test_select_bitexact_config1_shape(gpu):
     for tau in (8.0, 11.0):
         announce(f"select config1 N=32768 tau={tau}")
         keep, cc = ops.select(k.to(gpu), tau, 512)
-        ok, occ = OC.select_delta(k.float().numpy(), tau, 512)
+        ok, occ = OC.select_delta(k.float().numpy(), tau, 512, arith=oracle_arith(k))
         assert (cc.cpu().numpy() == occ).all()
         assert (keep.cpu().numpy() == ok).all()
 
@@ -113,7 +113,7 @@ def test_select_pair_grid_dims(gpu, D, dtype):
     for tau, metric in ((9.0, "euclidean"), (0.9, "cosine")):
         announce(f"select pair grid D={D} {dtype} {metric}")
         keep, cc = ops.select(k.to(gpu), tau, 512, 0, metric)
-        ok, occ = OC.select_delta(k.float().numpy(), tau, 512, 0, metric)
+        ok, occ = OC.select_delta(k.float().numpy(), tau, 512, 0, metric, arith=oracle_arith(k))
         assert np.array_equal(cc.cpu().numpy(), occ), "chunk counts differ"
         assert np.array_equal(keep.cpu().numpy(), ok)
 
@@ -132,7 +132,7 @@ def test_select_native_arith_bitexact(gpu, dtype, oracle_arith):
         ok, occ = OC.select_delta(kk.float().numpy(), tau, chunk, div, arith=oracle_arith)
         assert np.array_equal(cc.cpu().numpy(), occ)
         assert np.array_equal(keep.cpu().numpy(), ok)
-    k32, _ = OC.select_delta(kc.float().numpy(), 10.3327, 512)
+    k32, _ = OC.select_delta(kc.float().numpy(), 10.3327, 512, arith="fp32")
     assert not np.array_equal(k32, ok)
 
 
@@ -252,7 +252,7 @@ def test_delta_rescale_stress_vs_oracle(gpu, top, tau, variant):
     announce(f"delta rescale stress top={top} tau={tau} {variant}")
     out = ops.delta_prefill(q.to(gpu), k.to(gpu), v.to(gpu), tau, 512, window=128, variant=variant)
     kf, vf = k.float().numpy(), v.float().numpy()
-    keep, _ = OC.select_delta(kf, tau, 512)
+    keep, _ = OC.select_delta(kf, tau, 512, arith=oracle_arith(k))
     p = O.pack(kf, vf, keep)
     ref = O.hybrid_attention(q.float().numpy(), kf, vf, p["k_packed"], p["v_packed"],
                              p["timestamps"], p["counts"], 128, variant=variant)
@@ -313,7 +313,7 @@ def test_delta_prefill_vs_oracle(gpu, B, Hq, Hkv, N, tau, W, variant, no_count):
     out = ops.delta_prefill(q.to(gpu), k.to(gpu), v.to(gpu), tau, 512, window=W, variant=variant,
                             no_count=no_count)
     kf, vf = k.float().numpy(), v.float().numpy()
-    keep, _ = OC.select_delta(kf, tau, 512)
+    keep, _ = OC.select_delta(kf, tau, 512, arith=oracle_arith(k))
     p = O.pack(kf, vf, keep)
     ref = O.hybrid_attention(q.float().numpy(), kf, vf, p["k_packed"], p["v_packed"],
                              p["timestamps"], p["counts"], W, variant=variant, no_count=no_count)
@@ -404,7 +404,7 @@ def test_select_bitexact_fp16(gpu, metric, tau):
     _, k, _ = _f16_inputs(2, 4, 2, 1500, 128, seed=21)
     announce(f"select fp16 {metric} tau={tau}")
     keep, counts = ops.select(k.to(gpu), tau, 512, 0, metric)
-    ref_keep, ref_counts = OC.select_delta(k.float().numpy(), tau, 512, 0, metric)
+    ref_keep, ref_counts = OC.select_delta(k.float().numpy(), tau, 512, 0, metric, arith=oracle_arith(k))
     assert np.array_equal(keep.cpu().numpy(), ref_keep)
     assert np.array_equal(counts.cpu().numpy(), ref_counts)
 
@@ -422,7 +422,7 @@ def test_delta_prefill_fp16_vs_oracle(gpu, B, Hq, Hkv, N, tau, W, variant):
     out = ops.delta_prefill(q.to(gpu), k.to(gpu), v.to(gpu), tau, 512, window=W, variant=variant)
     assert out.dtype == torch.float16
     kf, vf = k.float().numpy(), v.float().numpy()
-    keep, _ = OC.select_delta(kf, tau, 512)
+    keep, _ = OC.select_delta(kf, tau, 512, arith=oracle_arith(k))
     p = O.pack(kf, vf, keep)
     ref = O.hybrid_attention(q.float().numpy(), kf, vf, p["k_packed"], p["v_packed"],
                              p["timestamps"], p["counts"], W, variant=variant)
@@ -496,7 +496,7 @@ def test_attention_with_sequence_stride_past_2_pow_22(gpu):
                                num_packed_dev=packed.num_packed)
     torch.cuda.synchronize()
     kf, vf = k.float().numpy(), v.float().numpy()
-    okeep, _ = OC.select_delta(kf, tau, 64)
+    okeep, _ = OC.select_delta(kf, tau, 64, arith=oracle_arith(k))
     p = O.pack(kf, vf, okeep)
     assert p["P"] == P
     want_h = O.hybrid_attention(q.float().numpy(), kf, vf, p["k_packed"], p["v_packed"], p["timestamps"],

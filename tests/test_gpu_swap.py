@@ -169,7 +169,7 @@ def test_model_prefill_then_decode_compressed_cache(gpu, monkeypatch, impl, time
     assert torch.isfinite(h).all()
     assert cache.get_seq_length(0) == N and cache.get_seq_length(1) == N
     k0, v0 = (t.float().cpu().numpy() for t in rec["prefill"])
-    keep, _ = OC.select_delta(k0, tau, 512)
+    keep, _ = OC.select_delta(k0, tau, 512, arith="bf16")  # the model and cache are bf16
     p = O.pack(k0, v0, keep)
     st = _oracle_cache_from_prefill(p, k0, v0, W, cache.capacity + steps)
     _assert_cache_equals(cache, st, "after the prefill hand-off")

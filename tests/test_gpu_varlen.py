@@ -5,7 +5,7 @@ import numpy as np
 import pytest
 import torch
 
-from conftest import announce
+from conftest import announce, oracle_arith
 from oracle import delta_oracle as O
 
 pytestmark = pytest.mark.gpu
@@ -57,7 +57,7 @@ def test_varlen_delta_matches_oracle(gpu):
         qb = q[s:e].permute(1, 0, 2)[None].float().cpu().numpy()
         kb = k[s:e].permute(1, 0, 2)[None].float().cpu().numpy()
         vb = v[s:e].permute(1, 0, 2)[None].float().cpu().numpy()
-        keep, _ = O.select_delta(kb, tau, 512)
+        keep, _ = O.select_delta(kb, tau, 512, arith=oracle_arith(k))
         p = O.pack(kb, vb, keep)
         ref = O.hybrid_attention(qb, kb, vb, p["k_packed"], p["v_packed"], p["timestamps"],
                                  p["counts"], 128)
@@ -119,7 +119,7 @@ def test_varlen_select_pack_bitexact(gpu, chunk, divide_to):
             continue
         kf = _per_seq(k, s, e).float().cpu().numpy()
         vf = _per_seq(v, s, e).float().cpu().numpy()
-        okeep, occ = OC.select_delta(kf, tau, chunk, divide_to)
+        okeep, occ = OC.select_delta(kf, tau, chunk, divide_to, arith=oracle_arith(k))
         assert np.array_equal(keep_h[:, s:e], okeep[0]), f"keep of sequence {b}"
         assert np.array_equal(cc_h[b, :, :occ.shape[-1]], occ[0]) and (cc_h[b, :, occ.shape[-1]:] == 0).all()
         ref = O.pack(kf, vf, okeep)
@@ -150,7 +150,7 @@ def test_varlen_select_pair_grid(gpu, chunk, divide_to):
     assert cc_h.shape[-1] * cc_h.shape[0] * cc_h.shape[1] >= 2048
     for b, (s, e) in enumerate(zip(cu[:-1], cu[1:])):
         kf = _per_seq(k, s, e).float().cpu().numpy()
-        okeep, occ = OC.select_delta(kf, tau, chunk, divide_to)
+        okeep, occ = OC.select_delta(kf, tau, chunk, divide_to, arith=oracle_arith(k))
         assert np.array_equal(keep_h[:, s:e], okeep[0]), f"keep of sequence {b}"
         assert np.array_equal(cc_h[b, :, :occ.shape[-1]], occ[0]) and (cc_h[b, :, occ.shape[-1]:] == 0).all()
 

@@ -8,7 +8,7 @@ import numpy as np
 import pytest
 import torch
 
-from conftest import announce
+from conftest import announce, oracle_arith
 from oracle import delta_oracle as O
 from oracle import select_oracle_c as OC
 
@@ -31,7 +31,7 @@ def layer(gpu):
     keep, _ = ops.select(kg, 10.0, 512)
     p = ops.pack(keep, kg, vg).trimmed()
     kf, vf = k.float().numpy(), v.float().numpy()
-    okeep, _ = OC.select_delta(kf, 10.0, 512)
+    okeep, _ = OC.select_delta(kf, 10.0, 512, arith=oracle_arith(kg))
     ref = O.pack(kf, vf, okeep)
     assert p.k_packed.shape[2] == ref["P"]
     return dict(q=qg, k=kg, v=vg, p=p, qf=q.float().numpy(), kf=kf, vf=vf, ref=ref)

@@ -438,3 +438,42 @@ def test_round_p_decode_closed_form():
         out = O.decode_attention(q[:, :, 1], st, scale=scale, round_p=round_p)
         assert out.shape == (1, 1, D)
         assert abs(out[0, 0, 0] - num / (1.0 + p1)) < 1e-6, (round_p, out[0, 0, 0])
+
+
+# --------------------------------------------------------------------------------------
+# the torch-CPU baseline (bench.py's cpu_baseline leg) computes the oracle's attention
+# --------------------------------------------------------------------------------------
+@pytest.mark.parametrize("case", ["A", "B", "D"])
+def test_cpu_baseline_hybrid_matches_golden(case):
+    """The blockwise exact softmax over each block's weighted key multiset reproduces the
+    reference's own kernels' outputs (double counting and the padding reset included)."""
+    from oracle import cpu_baseline as CB
+    d = _golden(case)
+    if bool(d["no_count"]):
+        pytest.skip("the baseline times the counted hybrid variant")
+    p = O.pack(d["k"], d["v"], d["keep"])
+    out = CB.hybrid_attention(d["q"], d["k"], d["v"], p["k_packed"], p["v_packed"], p["timestamps"],
+                              p["counts"], int(d["window"])).numpy()
+    assert np.abs(out - d["out_hybrid"]).max() < 1e-5
+
+
+@pytest.mark.parametrize("N,Hq,Hkv,W,tau", [(700, 8, 2, 128, 6.0), (384, 4, 4, 0, 7.5), (1000, 4, 1, 300, 5.0)])
+def test_cpu_baseline_matches_oracle(N, Hq, Hkv, W, tau):
+    from oracle import cpu_baseline as CB
+    q, k, v = _layer(N=N, Hq=Hq, Hkv=Hkv)
+    keep, _ = O.select_delta(k, tau, 128)
+    p = O.pack(k, v, keep)
+    want = O.hybrid_attention(q, k, v, p["k_packed"], p["v_packed"], p["timestamps"], p["counts"], W)
+    got = CB.hybrid_attention(q, k, v, p["k_packed"], p["v_packed"], p["timestamps"], p["counts"], W).numpy()
+    assert np.abs(got - want).max() < 1e-5
+    for causal in (True, False):
+        got_d = CB.dense_attention(q, k, v, causal).numpy()
+        assert np.abs(got_d - O.dense_bruteforce(q, k, v, causal)).max() < 1e-5
+
+
+def test_cpu_baseline_keep_all_is_dense():
+    from oracle import cpu_baseline as CB
+    q, k, v = _layer(N=512, Hq=4, Hkv=2)
+    p = O.pack(k, v, np.ones(k.shape[:3], np.int32))
+    got = CB.hybrid_attention(q, k, v, p["k_packed"], p["v_packed"], p["timestamps"], p["counts"], 128).numpy()
+    assert np.abs(got - O.dense_bruteforce(q, k, v)).max() < 1e-5
