@@ -98,6 +98,7 @@ struct AttnArgs {
   int rows_per_wg;  // 32 * (4 / hpw)
   int n_row_groups;
   int units;        // B * Hkv * (G / hpw)
+  int* queue;       // 8 work-queue counters (persistent attn_w64_kernel grid) or null
 };
 
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -202,8 +203,7 @@ __device__ __forceinline__ void store_tile(const TileRegs& r, char* stage, int t
 // them; the entries of 256 blocks are loaded together, so the usual case is one round
 // trip to memory.  Needs all 64 lanes of the wave.
 __device__ __forceinline__ void safe_prefix(const int32_t* __restrict__ bmax, const int32_t* __restrict__ pmax,
-                                            int nblk, int thr, int& n_safe, int& last) {
-  const int lane = threadIdx.x & 63;
+                                            int nblk, int thr, int& n_safe, int& last, int lane) {
   int n = 0, prev_last = -1;
   last = -1;
   for (int base = 0; base < nblk; base += 256) {
@@ -281,7 +281,7 @@ __device__ __forceinline__ void attn_body(const AttnArgs& a) {
     const int32_t* bmax = a.sched + (int64_t)bg * 2 * a.nblk_cap;
     const int32_t* pmax = bmax + a.nblk_cap;
     int n_safe, last;
-    safe_prefix(bmax, pmax, nblk, start_m - a.window, n_safe, last);
+    safe_prefix(bmax, pmax, nblk, start_m - a.window, n_safe, last, lane);
     ds = max(0, ((last + 1) / kBlock) * kBlock);
     if (VARIANT == kHybrid) n1 = n_safe * (kBlock / kTileN);
     kend = min(Nk, wg_end);
@@ -608,7 +608,9 @@ constexpr int kWVBytes = kWTK * kD * 2;          // 8 KiB
 constexpr int kWMetaSlot = 64 * 8;               // weights[64] fp32, timestamps[64] int32
 constexpr int kWCnt = 0, kWTs = 64 * 4;          // offsets inside a meta slot
 constexpr int kWQBytes = 32 * kD * 2;          // Q of one 32-row column block, per wave
-constexpr int kWLds = 3 * kWKBytes + 3 * kWVBytes + 4 * kWMetaSlot + 8 * kWQBytes;
+// the persistent grid's item broadcast (two ints) after the Q regions
+constexpr int kWItemSlot = 3 * kWKBytes + 3 * kWVBytes + 4 * kWMetaSlot + 8 * kWQBytes;
+constexpr int kWLds = kWItemSlot + 16;  // item: queue, index, queues found empty
 // K stages and Q blocks start at multiples of 256 bytes (the kernel has no static LDS, so
 // its dynamic LDS starts at address 0): the K / Q fragment addresses are formed by XOR.
 static_assert(kWKBytes % 256 == 0 && (3 * kWKBytes + 3 * kWVBytes + 4 * kWMetaSlot) % 256 == 0 &&
@@ -635,35 +637,34 @@ __device__ __forceinline__ void mask_pure32(f32x16& s, const int* tl, int row, i
   }
 }
 
+// Units of work queue q (one queue per XCD): the contiguous range [ulo, uhi) of the
+// units, in the order of the static grid below.
+__device__ __forceinline__ void queue_units(int q, int units, int& ulo, int& uhi) {
+  ulo = (q * units) >> 3;
+  uhi = ((q + 1) * units) >> 3;
+}
+
+// One (unit, row group) of attn_w64_kernel: 4 query heads of one (batch, KV head) over
+// the logical 128-row query block rg.  Ends with every LDS read of the window loop done
+// (its last barrier) and every load landed; the finalize uses only the wave's own Q
+// region, so the next item may start staging at once.
 template <int VARIANT, int DT>
-__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
-void attn_w64_kernel(AttnArgs a) {
+__device__ __forceinline__ void attn_w64_item(const AttnArgs& a, const int unit, const int rg) {
   extern __shared__ __attribute__((aligned(16))) char smem[];
   char* const kst0 = smem;
   char* const vst0 = smem + 3 * kWKBytes;
   char* const meta0 = smem + 3 * kWKBytes + 3 * kWVBytes;
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wid = tid >> 6;  // uniform per wave
+  // opaque per item: what derives from the thread index is formed here, not hoisted out
+  // of the persistent grid's item loop into registers held across items
+  int tid = threadIdx.x;
+  asm volatile("" : "+v"(tid));
+  const int lane = tid & 63;
+  const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform per wave
   // Q of column block 1, lane-private: each lane reads back only the 16-byte chunks it
   // wrote (the K fragment layout), so the 32 registers it would take stay free
   char* const qs = meta0 + 4 * kWMetaSlot + wid * kWQBytes;
   const int grp = wid >> 2, hw = wid & 3;
   const int hl = lane >> 5, ql = lane & 31;
-
-  // ---- workgroup -> (unit, row group).  A unit is 4 query heads of one (batch, KV
-  // head), g-major.  When the units split evenly over the 8 XCDs (workgroup i runs on
-  // XCD i mod 8), each XCD takes a contiguous range of units and walks their row groups
-  // longest first, so a unit's K/V stay in one XCD's L2 ----
-  const int wg = blockIdx.x;
-  int unit, rg;
-  if ((a.units & 7) == 0) {
-    const int xcd = wg & 7, idx = wg >> 3, upx = a.units >> 3;
-    unit = xcd * upx + idx / a.n_row_groups;
-    rg = a.n_row_groups - 1 - idx % a.n_row_groups;
-  } else {
-    unit = wg % a.units;
-    rg = a.n_row_groups - 1 - wg / a.units;
-  }
   const int hunits = a.G >> 2;
   const int gb = unit / hunits;  // g * B + b
   const int hu = unit - gb * hunits;
@@ -689,7 +690,7 @@ void attn_w64_kernel(AttnArgs a) {
     const int32_t* bmax = a.sched + (int64_t)bg * 2 * a.nblk_cap;
     const int32_t* pmax = bmax + a.nblk_cap;
     int n_safe, last;
-    safe_prefix(bmax, pmax, nblk, start_m - a.window, n_safe, last);
+    safe_prefix(bmax, pmax, nblk, start_m - a.window, n_safe, last, lane);
     ds = max(0, ((last + 1) / kBlock) * kBlock);
     if (VARIANT == kHybrid) n1 = n_safe * (kBlock / kWTK);
     kend = min(Nk, wg_end);
@@ -769,16 +770,19 @@ void attn_w64_kernel(AttnArgs a) {
     const int key0 = ph1 ? t * kWTK : 0;
     const int nrows = ph1 ? clamp0_uniform(a.wcap - key0, kWTK) : kWTK;
     char* dst = meta_of(t_raw);
+    // the lane's offset, formed here from an opaque lane index rather than held
+    int mlane = lane;
+    asm volatile("" : "+v"(mlane));
     const __amdgpu_buffer_rsrc_t rc = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<void*>(uniform_ptr(ph1 ? w_row + key0 : a.zeros)), (short)0,
         nrows * 4, kBufferDword3);
     __builtin_amdgcn_raw_ptr_buffer_load_lds(rc, (__attribute__((address_space(3))) void*)(dst + kWCnt), 4,
-                                             lane * 4, 0, 0, 0);
+                                             mlane * 4, 0, 0, 0);
     if (kPureV) {
       const __amdgpu_buffer_rsrc_t rt = __builtin_amdgcn_make_buffer_rsrc(
           const_cast<void*>(uniform_ptr(tsw_row + key0)), (short)0, nrows * 4, kBufferDword3);
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rt, (__attribute__((address_space(3))) void*)(dst + kWTs), 4,
-                                               lane * 4, 0, 0, 0);
+                                               mlane * 4, 0, 0, 0);
     }
   };
   auto dma_issue = [&](int tk, int tv, unsigned kst, unsigned vst) {
@@ -1141,6 +1145,88 @@ void attn_w64_kernel(AttnArgs a) {
   }
 }
 
+// Work distribution.  Static (a.queue null, the dense control): workgroup i runs on XCD
+// i mod 8 and takes one item; when the units split evenly over the 8 XCDs, each XCD gets
+// a contiguous range of units and walks their row groups longest first, so a unit's K/V
+// stay in one XCD's L2.  Persistent (a.queue set, the hybrid, sanity and pure Phase 1
+// variants, whose schedule kernel zeroes the 8 counters just before): one workgroup per
+// CU loops over items.  Queue q holds the units of XCD q's static share in the same
+// order (unit by unit, longest row group first) and a.queue[q] counts the items taken;
+// a workgroup takes from the queue of the XCD it runs on and, once that is empty, from
+// the others, so the XCDs, whose clocks differ by several per cent, finish together,
+// and no dispatch gap lies between two items on a CU.  Every counter only grows, so each
+// workgroup's loop ends after at most 8 empty takes; workgroups never wait on each other.
+template <int VARIANT, int DT>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void attn_w64_kernel(AttnArgs a) {
+  extern __shared__ __attribute__((aligned(16))) char smem[];
+  int* const slot = (int*)(smem + kWItemSlot);
+  const int tid = threadIdx.x;
+  const int n_rg = a.n_row_groups;
+  const bool persistent = a.queue != nullptr;
+  unsigned xcc = 0;
+  if (persistent) {
+    asm volatile("s_getreg_b32 %0, hwreg(HW_REG_XCC_ID)" : "=s"(xcc));
+    if (tid == 0) slot[2] = 0;  // queues found empty so far, from this XCD's own
+  }
+  for (int first = 1;; first = 0) {
+    int unit, rg;
+    if (!persistent) {
+      if (!first) break;
+      const int wg = blockIdx.x;
+      if ((a.units & 7) == 0) {
+        const int xcd = wg & 7, idx = wg >> 3, upx = a.units >> 3;
+        unit = xcd * upx + idx / n_rg;
+        rg = n_rg - 1 - idx % n_rg;
+      } else {
+        unit = wg % a.units;
+        rg = n_rg - 1 - wg / a.units;
+      }
+    } else {
+      if (tid == 0) {
+        int q = 0, k = -1, qi = slot[2];
+        while (qi < 8) {
+          q = (int)((xcc + qi) & 7);
+          int ulo, uhi;
+          queue_units(q, a.units, ulo, uhi);
+          const int taken = atomicAdd(a.queue + q, 1);
+          if (taken < (uhi - ulo) * n_rg) {
+            k = taken;
+            break;
+          }
+          ++qi;
+        }
+        slot[0] = q;
+        slot[1] = k;
+        slot[2] = qi;
+      }
+      lds_barrier();
+      const int q = __builtin_amdgcn_readfirstlane(slot[0]);
+      const int k = __builtin_amdgcn_readfirstlane(slot[1]);
+      lds_barrier();  // the slot is read before thread 0 writes it again
+      if (k < 0) break;
+      int ulo, uhi;
+      queue_units(q, a.units, ulo, uhi);
+      const int j = k / n_rg;
+      unit = ulo + j;
+      rg = n_rg - 1 - (k - j * n_rg);
+    }
+#if defined(__HIP_DEVICE_COMPILE__)
+    // the argument block read through the kernel-argument segment's address, made
+    // opaque per item: its fields are loaded inside each item instead of being held in
+    // scalar registers across the loop (the block is the kernel's only argument, at
+    // offset 0)
+    const __attribute__((address_space(4))) AttnArgs* ap =
+        (const __attribute__((address_space(4))) AttnArgs*)__builtin_amdgcn_kernarg_segment_ptr();
+    asm volatile("" : "+s"(ap));
+    const AttnArgs ai = *ap;
+    attn_w64_item<VARIANT, DT>(ai, unit, rg);
+#else
+    attn_w64_item<VARIANT, DT>(a, unit, rg);
+#endif
+  }
+}
+
 // Per (batch, kv head): maxima of packed blocks of 128 timestamps (lanes at or
 // beyond P read seq_len_k + 1, deltaFlashAttention.py:70) and their prefix maxima.
 // Blocks with blockIdx.y = 0 do that; those with blockIdx.y = 1 + c (when wts is set)
@@ -1168,10 +1254,12 @@ __global__ __launch_bounds__(kSchedThreads) void hybrid_schedule_kernel(const in
                                                               const int32_t* P_dev, int Nk,
                                                               SeqMap seq, int nblk_cap,
                                                               int32_t* __restrict__ sched,
-                                                              SchedPrep prep) {
+                                                              SchedPrep prep, int* __restrict__ queue) {
   __shared__ int32_t s_bmax[4096];
   __shared__ int32_t s_wave[kSchedWaves];
   const int tid = threadIdx.x, lane = tid & 63;
+  // the attention kernel's work-queue counters start at zero
+  if (queue && blockIdx.x == 0 && blockIdx.y == 0 && tid < 8) queue[tid] = 0;
   const int wid = __builtin_amdgcn_readfirstlane(tid >> 6);  // wave-uniform (scalar)
   const int bg = blockIdx.x;
   const int b = bg / Hkv, g = bg - (bg / Hkv) * Hkv;
@@ -1271,6 +1359,19 @@ static int allow_lds(size_t bytes) {
   return DA_OK;
 }
 
+// Compute units of the current device (cached per device).
+static int cu_count() {
+  static int n[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (!n[dev]) {
+    int v = 0;
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
+    n[dev] = v;
+  }
+  return n[dev];
+}
+
 template <int V, int DT>
 static int allow_lds_w64(size_t bytes) {
   static int done = 0;
@@ -1289,7 +1390,10 @@ static int launch_attn_t(AttnArgs& a, hipStream_t st) {
     a.rows_per_wg = 128;
     a.n_row_groups = (a.Nq + 127) / 128;
     const size_t lds = kWLds;
-    const unsigned grid = (unsigned)((int64_t)a.n_row_groups * a.units);
+    const int64_t items = (int64_t)a.n_row_groups * a.units;
+    // persistent: one workgroup per CU (the LDS of one fills a CU) takes items until the
+    // queues are empty; static: one workgroup per item
+    const unsigned grid = (unsigned)(a.queue ? std::min<int64_t>(items, cu_count()) : items);
     if (int rc = allow_lds_w64<V, DT>(lds)) return rc;
     hipLaunchKernelGGL((attn_w64_kernel<V, DT>), dim3(grid), dim3(512), lds, st, a);
     return check_launch("attention kernel (ping-pong)");
@@ -1360,11 +1464,11 @@ using namespace da;
 
 // Workspace of da_hybrid_prefill: the schedule ([B*Hkv][2][nblk] int32), then, each at
 // a 256-byte boundary, the key biases ([B*Hkv][wcap] fp32), the timestamps of the pure
-// Phase-1 variant ([B*Hkv][wcap] int32) and 64 zeros; nblk = ceil(num_packed / 128)
-// (at least 1), wcap = 128 nblk.
+// Phase-1 variant ([B*Hkv][wcap] int32), 64 zeros and the attention kernel's 8
+// work-queue counters; nblk = ceil(num_packed / 128) (at least 1), wcap = 128 nblk.
 struct HybridWs {
   int nblk, wcap;
-  int64_t w_off, ts_off, zeros_off, total;
+  int64_t w_off, ts_off, zeros_off, queue_off, total;
 };
 static int64_t round256(int64_t x) { return (x + 255) & ~(int64_t)255; }
 static HybridWs hybrid_ws(int64_t B, int64_t Hkv, int64_t num_packed) {
@@ -1375,7 +1479,8 @@ static HybridWs hybrid_ws(int64_t B, int64_t Hkv, int64_t num_packed) {
   w.w_off = round256(B * Hkv * 2 * nblk * (int64_t)sizeof(int32_t));
   w.ts_off = w.w_off + round256(B * Hkv * w.wcap * (int64_t)sizeof(float));
   w.zeros_off = w.ts_off + round256(B * Hkv * w.wcap * (int64_t)sizeof(int32_t));
-  w.total = w.zeros_off + 256;
+  w.queue_off = w.zeros_off + 256;
+  w.total = w.queue_off + 256;
   return w;
 }
 
@@ -1443,9 +1548,11 @@ static int hybrid_impl(const char* who, AttnArgs& a, const void* k_packed, const
     prep.wcap = wl.wcap;
   }
   const unsigned prep_chunks = prep.wts ? (unsigned)((wl.wcap + kSchedThreads - 1) / kSchedThreads) : 0u;
+  // the grouped kernel's persistent grid takes its items from 8 counters in the workspace
+  a.queue = a.hpw == 4 ? (int*)(ws + wl.queue_off) : nullptr;
   hipLaunchKernelGGL(hybrid_schedule_kernel, dim3((unsigned)(B * Hkv), 1 + prep_chunks), dim3(kSchedThreads), 0, st,
                      timestamps, a.sts_b, a.sts_h, (int)Hkv, (int)P_bound, num_packed_dev, (int)Nk, a.seq,
-                     a.nblk_cap, (int32_t*)ws, prep);
+                     a.nblk_cap, (int32_t*)ws, prep, a.queue);
   if (int rc = check_launch("hybrid prefill (schedule)")) return rc;
   const int kv = variant == DA_VARIANT_HYBRID ? kHybrid : (variant == DA_VARIANT_SANITY ? kSanity : kPure);
   return launch_attn(kv, dtype, a, st);

@@ -159,12 +159,13 @@ def test_workspace_sizes():
     def hybrid_ws(B, H, P):
         nblk = max(1, (P + 127) // 128)
         wcap = 128 * nblk
-        # schedule, fp32 weights, timestamps, 64 ones (each region 256-byte aligned)
-        return r256(B * H * 2 * nblk * 4) + 2 * r256(B * H * wcap * 4) + 256
+        # schedule, fp32 weights, timestamps, 64 zeros, 8 work-queue counters (each region
+        # 256-byte aligned)
+        return r256(B * H * 2 * nblk * 4) + 2 * r256(B * H * wcap * 4) + 256 + 256
 
     assert lib.da_hybrid_workspace_size(1, 8, 8192) == hybrid_ws(1, 8, 8192)
     assert lib.da_hybrid_workspace_size(2, 8, 1) == hybrid_ws(2, 8, 1)
-    assert lib.da_hybrid_workspace_size(1, 8, 8192) == 4096 + 2 * 8 * 8192 * 4 + 256
+    assert lib.da_hybrid_workspace_size(1, 8, 8192) == 4096 + 2 * 8 * 8192 * 4 + 512
 
 
 def test_ops_refuse_cpu_tensors():
