@@ -102,8 +102,9 @@ __global__ __launch_bounds__(256) void decode_update_kernel(DecodeUpdateArgs a) 
 }
 
 constexpr int kDecSlice = 64;
-constexpr int kDecMaxG = 8;
-constexpr int kDecD = 128;
+constexpr int kDecMaxG = 8;     // query heads one wave scores (a larger group is split)
+constexpr int kDecMaxGroup = 64;
+constexpr int kDecD = 128;      // the largest head dimension; partials keep this stride
 
 struct DecodeAttnArgs {
   const uint16_t* q;
@@ -122,9 +123,10 @@ struct DecodeAttnArgs {
   float scale;
   uint16_t* out;
   int64_t so_b, so_h;
-  float* part;      // [B*Hkv][nslice][G][D + 2]: max, sum, P.V partial
+  float* part;      // [B*Hkv][nslice][G][kDecD + 2]: max, sum, P.V partial
   int nslice;
   int B, Hq, Hkv, G;
+  int D;            // head dimension: a multiple of 8, at most kDecD
 };
 
 __device__ __forceinline__ float wave_max_all(float v) {
@@ -138,20 +140,31 @@ __device__ __forceinline__ float wave_sum_all(float v) {
   return v;
 }
 
-// One wave per (batch, kv head, 64-key slice).  After the length of the list, lane t's
-// whole 256-byte key row and the group's query rows are loaded together; the slice's
-// 64 value rows are issued as soon as the scores are done and arrive during the
-// softmax.  Lane t scores key j0 + t for every query head of the group (q broadcast
-// from LDS); the slice max and sum are wave reductions; for P.V lane l owns dims 2l
-// and 2l + 1.  Small slices keep many waves in flight per CU: the kernel is
-// latency-bound at decode sizes, and holding K and V rows at once would halve the
-// waves per SIMD.
+// One wave per (batch, kv head, 64-key slice, sub-group of at most G query heads of
+// the KV head's group: blockIdx.z picks heads G z .. G z + G - 1; where the last
+// sub-group runs past the group, its extra slots repeat the group's last head and store
+// the same values to the same place).  After the length of the list, lane t's whole key row and the sub-group's
+// query rows are loaded together; the slice's 64 value rows are issued as soon as the
+// scores are done and arrive during the softmax.  Lane t scores key j0 + t for every
+// query head of the sub-group (q broadcast from LDS); the slice max and sum are wave
+// reductions; for P.V lane l owns dims 2l and 2l + 1.  Outputs past the head dimension
+// are not stored.
+// Small slices keep many waves in flight per CU: the kernel is latency-bound at decode
+// sizes, and holding K and V rows at once would halve the waves per SIMD.
 template <int G, int DT>
 __global__ __launch_bounds__(64) void decode_attn_kernel(DecodeAttnArgs a) {
   __shared__ float s_q[G][kDecD];
   __shared__ float s_p[G][kDecSlice];
   const int lane = threadIdx.x;
   const int bg = blockIdx.x, slice = blockIdx.y;
+  const int hh0 = blockIdx.z * G;  // first query head of the sub-group
+  auto head = [&](int hh) { return min(hh0 + hh, a.G - 1); };
+  const int D = a.D;
+  // Loads stay unconditional: key chunks past the head dimension repeat its last chunk
+  // and meet zero query elements, value lanes past it read its last pair and their
+  // partials are never stored
+  const int dlast8 = D / 8 - 1;
+  const int vdim = min(2 * lane, D - 2);
   const int b = bg / a.Hkv, g = bg - (bg / a.Hkv) * a.Hkv;
   int plen = a.lengths[bg];
   plen = plen < 0 ? 0 : (plen > a.capacity ? (int)a.capacity : plen);
@@ -169,7 +182,7 @@ __global__ __launch_bounds__(64) void decode_attn_kernel(DecodeAttnArgs a) {
     const uint16_t* krow = j < plen ? a.kp + b * a.sp_b + g * a.sp_h + (int64_t)j * a.sp_s
                                     : a.kx + b * a.sx_b + g * a.sx_h + (int64_t)(j - plen) * a.sx_s;
 #pragma unroll
-    for (int c8 = 0; c8 < kDecD / 8; ++c8) kw[c8] = *(const u32x4*)(krow + 8 * c8);
+    for (int c8 = 0; c8 < kDecD / 8; ++c8) kw[c8] = *(const u32x4*)(krow + 8 * min(c8, dlast8));
     if (j < plen) cnt = a.counts[b * a.sc_b + g * a.sc_h + j];
   }
   constexpr int kQPerLane = G * kDecD / 64;
@@ -177,7 +190,7 @@ __global__ __launch_bounds__(64) void decode_attn_kernel(DecodeAttnArgs a) {
 #pragma unroll
   for (int it = 0; it < kQPerLane; ++it) {
     const int i = lane + 64 * it, hh = i / kDecD, d = i - hh * kDecD;
-    qh[it] = a.q[b * a.sq_b + (int64_t)(g * G + hh) * a.sq_h + d];
+    qh[it] = d < D ? a.q[b * a.sq_b + (int64_t)(g * a.G + head(hh)) * a.sq_h + d] : (uint16_t)0;
   }
 #pragma unroll
   for (int it = 0; it < kQPerLane; ++it) {
@@ -222,11 +235,11 @@ __global__ __launch_bounds__(64) void decode_attn_kernel(DecodeAttnArgs a) {
     const int jk = j0 + u;
     const uint16_t* vrow = jk < plen ? a.vp + b * a.sp_b + g * a.sp_h + (int64_t)jk * a.sp_s
                                      : a.vx + b * a.sx_b + g * a.sx_h + (int64_t)(jk - plen) * a.sx_s;
-    vw[u] = jk < total ? *(const uint32_t*)(vrow + 2 * lane) : 0u;
+    vw[u] = jk < total ? *(const uint32_t*)(vrow + vdim) : 0u;
   }
 
   // ---- per-head slice max and sum; weights rounded to the cache's type, to LDS ----
-  float* part = a.part + ((int64_t)bg * a.nslice + slice) * G * (kDecD + 2);
+  float* part = a.part + ((int64_t)bg * a.nslice + slice) * a.G * (kDecD + 2);
 #pragma unroll
   for (int hh = 0; hh < G; ++hh) {
     if (hh < G) {
@@ -235,8 +248,8 @@ __global__ __launch_bounds__(64) void decode_attn_kernel(DecodeAttnArgs a) {
       const float l = wave_sum_all(p);
       s_p[hh][lane] = E16<DT>::one(E16<DT>::bits(p));  // p rounded to the cache's type
       if (lane == 0) {
-        part[hh * (kDecD + 2)] = m;
-        part[hh * (kDecD + 2) + 1] = l;
+        part[head(hh) * (kDecD + 2)] = m;
+        part[head(hh) * (kDecD + 2) + 1] = l;
       }
     }
   }
@@ -250,17 +263,16 @@ __global__ __launch_bounds__(64) void decode_attn_kernel(DecodeAttnArgs a) {
   for (int u = 0; u < kDecSlice; ++u) {
     const float v0 = E16<DT>::lo(vw[u]), v1 = E16<DT>::hi(vw[u]);
 #pragma unroll
-    for (int hh = 0; hh < G; ++hh)
-      if (hh < G) {
-        av[hh][0] = __builtin_fmaf(s_p[hh][u], v0, av[hh][0]);
-        av[hh][1] = __builtin_fmaf(s_p[hh][u], v1, av[hh][1]);
-      }
+    for (int hh = 0; hh < G; ++hh) {
+      av[hh][0] = __builtin_fmaf(s_p[hh][u], v0, av[hh][0]);
+      av[hh][1] = __builtin_fmaf(s_p[hh][u], v1, av[hh][1]);
+    }
   }
 #pragma unroll
   for (int hh = 0; hh < G; ++hh)
-    if (hh < G) {
-      part[hh * (kDecD + 2) + 2 + 2 * lane] = av[hh][0];
-      part[hh * (kDecD + 2) + 3 + 2 * lane] = av[hh][1];
+    {
+      part[head(hh) * (kDecD + 2) + 2 + 2 * lane] = av[hh][0];
+      part[head(hh) * (kDecD + 2) + 3 + 2 * lane] = av[hh][1];
     }
 }
 
@@ -288,8 +300,8 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeAttnArgs a) {
   const int total = plen + a.exact_len;
   const int ns = (total + kDecSlice - 1) / kDecSlice;
   const float* base = a.part + (int64_t)bg * a.nslice * a.G * (kDecD + 2) + hh * (kDecD + 2);
-  // 32-bit offsets within one (batch, KV head): nslice * G * (D + 2) stays below 2^31
-  // under the launch's limits on slices and group size
+  // 32-bit offsets within one (batch, KV head): nslice * G * (kDecD + 2) stays below
+  // 2^31 under the launch's limits (16384 slices, groups of at most 64: 1.4e8)
   const int sstride = a.G * (kDecD + 2);
   // the first batch of P.V partials goes out first: it does not depend on the maxima.
   // Slice indexes past the last are clamped to a slice that exists and masked when
@@ -351,7 +363,7 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeAttnArgs a) {
   }
   s_acc[q][dl] = acc;
   __syncthreads();
-  if (q == 0) {
+  if (q == 0 && d < a.D) {
     float o = acc;
 #pragma unroll
     for (int p = 1; p < kCombPhases; ++p) o += s_acc[p][dl];
@@ -414,8 +426,13 @@ extern "C" int da_decode_update(const void* new_k, const void* new_v, int dtype,
 }
 
 template <int DT>
-static int launch_decode(DecodeAttnArgs& a, dim3 agrid, int64_t n_heads, hipStream_t st) {
-  switch (a.G) {
+static int launch_decode(DecodeAttnArgs& a, int64_t n_heads, hipStream_t st) {
+  // a group above kDecMaxG query heads is split into ceil(G / kDecMaxG) sub-groups of
+  // equal size (the last one smaller when G does not divide), one wave each
+  const int nsub = (a.G + kDecMaxG - 1) / kDecMaxG;
+  const int gw = (a.G + nsub - 1) / nsub;
+  const dim3 agrid((unsigned)(a.B * a.Hkv), (unsigned)a.nslice, (unsigned)nsub);
+  switch (gw) {
     case 1: hipLaunchKernelGGL((decode_attn_kernel<1, DT>), agrid, dim3(64), 0, st, a); break;
     case 2: hipLaunchKernelGGL((decode_attn_kernel<2, DT>), agrid, dim3(64), 0, st, a); break;
     case 3: hipLaunchKernelGGL((decode_attn_kernel<3, DT>), agrid, dim3(64), 0, st, a); break;
@@ -437,7 +454,7 @@ extern "C" int64_t da_decode_workspace_size(int64_t B, int64_t Hq, int64_t capac
 
 // Validation and launch shared by da_decode_attention and da_decode_attention_noalloc:
 // `part` is the slice-partials buffer (caller workspace or the static scratch).
-static int decode_attention_impl(const void* q, int dtype, int64_t B, int64_t Hq, int64_t Hkv,
+static int decode_attention_impl(const void* q, int dtype, int64_t B, int64_t Hq, int64_t Hkv, int64_t D,
                                  int64_t sq_b, int64_t sq_h, const void* k_packed, const void* v_packed,
                                  int64_t sp_b, int64_t sp_h, int64_t sp_s, const int32_t* counts,
                                  int64_t sc_b, int64_t sc_h, const int32_t* lengths, int64_t capacity,
@@ -452,9 +469,8 @@ static int decode_attention_impl(const void* q, int dtype, int64_t B, int64_t Hq
   a.exact_len = (int)exact_len; a.scale = scale; a.out = (uint16_t*)out; a.so_b = so_b; a.so_h = so_h;
   a.part = part;
   a.nslice = (int)((capacity + window + kDecSlice - 1) / kDecSlice);
-  a.B = (int)B; a.Hq = (int)Hq; a.Hkv = (int)Hkv; a.G = (int)(Hq / Hkv);
-  const dim3 agrid((unsigned)(B * Hkv), (unsigned)a.nslice);
-  return dtype == DA_F16 ? launch_decode<DA_F16>(a, agrid, B * Hq, st) : launch_decode<DA_BF16>(a, agrid, B * Hq, st);
+  a.B = (int)B; a.Hq = (int)Hq; a.Hkv = (int)Hkv; a.G = (int)(Hq / Hkv); a.D = (int)D;
+  return dtype == DA_F16 ? launch_decode<DA_F16>(a, B * Hq, st) : launch_decode<DA_BF16>(a, B * Hq, st);
 }
 
 // Argument checks common to both decode attention entry points.
@@ -468,9 +484,10 @@ static int decode_attention_check(const void* q, int dtype, int64_t B, int64_t H
              "%s: null pointer", who);
   if (dtype != DA_BF16 && dtype != DA_F16)
     return set_error(DA_ERR_UNSUPPORTED, "%s: the cache must be bf16 or fp16", who);
-  if (D != kDecD) return set_error(DA_ERR_UNSUPPORTED, "%s: head_dim must be 128", who);
+  if (D <= 0 || D > kDecD || (D & 7))
+    return set_error(DA_ERR_UNSUPPORTED, "%s: head_dim must be a multiple of 8 in [8, %d]", who, kDecD);
   DA_REQUIRE(B > 0 && Hq > 0 && Hkv > 0 && Hq % Hkv == 0, "%s: bad head counts", who);
-  if (Hq / Hkv > kDecMaxG) return set_error(DA_ERR_UNSUPPORTED, "%s: GQA group above %d", who, kDecMaxG);
+  if (Hq / Hkv > kDecMaxGroup) return set_error(DA_ERR_UNSUPPORTED, "%s: GQA group above %d", who, kDecMaxGroup);
   DA_REQUIRE(window > 0 && exact_len >= 0 && exact_len <= window && capacity > 0, "%s: bad cache lengths", who);
   // key rows are read 16 bytes at a time, value rows 4 bytes per lane
   DA_REQUIRE(((sp_b | sp_h | sp_s | sx_b | sx_h | sx_s) & 7) == 0 && (((uintptr_t)k_packed | (uintptr_t)k_exact) & 15) == 0,
@@ -498,7 +515,7 @@ extern "C" int da_decode_attention(const void* q, int dtype, int64_t B, int64_t 
   const int64_t need = da_decode_workspace_size(B, Hq, capacity, window);
   if (!workspace || workspace_bytes < need)
     return set_error(DA_ERR_WORKSPACE, "%s: workspace of %lld bytes required", who, (long long)need);
-  return decode_attention_impl(q, dtype, B, Hq, Hkv, sq_b, sq_h, k_packed, v_packed, sp_b, sp_h, sp_s, counts,
+  return decode_attention_impl(q, dtype, B, Hq, Hkv, D, sq_b, sq_h, k_packed, v_packed, sp_b, sp_h, sp_s, counts,
                                sc_b, sc_h, lengths, capacity, k_exact, v_exact, sx_b, sx_h, sx_s, window,
                                exact_len, scale, out, so_b, so_h, (float*)workspace, (hipStream_t)stream);
 }
@@ -522,7 +539,7 @@ extern "C" int da_decode_step(const DaDecodeStep* s, void* stream) {
                                   s->capacity, s->exact_seq_len, s->total_seq_len, s->window, s->threshold,
                                   s->use_cosine, stream, who))
     return rc;
-  return decode_attention_impl(s->q, s->dtype, s->B, s->Hq, s->Hkv, s->sq_b, s->sq_h, s->k_packed, s->v_packed,
+  return decode_attention_impl(s->q, s->dtype, s->B, s->Hq, s->Hkv, s->D, s->sq_b, s->sq_h, s->k_packed, s->v_packed,
                                s->sp_b, s->sp_h, s->sp_s, s->counts, s->sc_b, s->sc_h, s->lengths, s->capacity,
                                s->k_exact, s->v_exact, s->sx_b, s->sx_h, s->sx_s, s->window, exact_len, s->scale,
                                s->out, s->so_b, s->so_h, (float*)s->workspace, (hipStream_t)stream);
@@ -583,7 +600,7 @@ extern "C" int da_decode_attention_noalloc(const void* q, int dtype, int64_t B, 
                      who, (long long)need, (long long)DA_DECODE_SCRATCH_BYTES);
   void* part = nullptr;
   if (int rc = scratch_for_current_device(&part, who)) return rc;
-  return decode_attention_impl(q, dtype, B, Hq, Hkv, sq_b, sq_h, k_packed, v_packed, sp_b, sp_h, sp_s, counts,
+  return decode_attention_impl(q, dtype, B, Hq, Hkv, D, sq_b, sq_h, k_packed, v_packed, sp_b, sp_h, sp_s, counts,
                                sc_b, sc_h, lengths, capacity, k_exact, v_exact, sx_b, sx_h, sx_s, window,
                                exact_len, scale, out, so_b, so_h, (float*)part, (hipStream_t)stream);
 }

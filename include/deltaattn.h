@@ -229,7 +229,8 @@ int da_decode_update(const void* new_k, const void* new_v, int dtype, int64_t B,
  * head h / (Hq / Hkv).
  * Scores over the packed anchors [0, lengths[b*Hkv + g]) get + log(count); then the
  * ring slots [0, exact_len) (exact_len = min(exact_seq_len, W)).  out: [B, Hq, D]
- * (strides so_b, so_h).  D must be 128, Hq / Hkv <= 8.
+ * (strides so_b, so_h).  D: a multiple of 8 up to 128 (the reference's BLOCK_D masking,
+ * deltaDecoding.py:255-268); Hq / Hkv <= 64 (groups above 8 are scored in sub-groups).
  */
 int64_t da_decode_workspace_size(int64_t B, int64_t Hq, int64_t capacity, int64_t window);
 int da_decode_attention(const void* q, int dtype, int64_t B, int64_t Hq, int64_t Hkv, int64_t D,

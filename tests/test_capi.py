@@ -124,6 +124,27 @@ def test_decode_rejects_misaligned_values():
             assert rc == -1 and "value rows" in _err()
 
 
+def test_decode_shape_limits():
+    """Decode attention takes head dims that are multiples of 8 up to 128 and GQA groups up
+    to 64; other shapes are refused as unsupported before any launch (the accepted ones
+    reach the workspace check)."""
+    lib = _native.lib()
+    a = ctypes.c_void_p(1 << 20)
+    f = ctypes.c_float(0.1)
+    cap, W = 64, 16
+
+    def call(Hq, Hkv, D, ws=None, ws_bytes=0):
+        st_p, st_x = (Hkv * cap * D, cap * D, D), (Hkv * W * D, W * D, D)
+        return lib.da_decode_attention(a, 1, 1, Hq, Hkv, D, Hq * D, D, a, a, *st_p, a, Hkv * cap, cap, a, cap,
+                                       a, a, *st_x, W, 0, f, a, Hq * D, D, ws, ws_bytes, None)
+
+    for D in (4, 100, 136):
+        assert call(8, 8, D) == -2 and "head_dim" in _err(), D
+    assert call(65, 1, 64) == -2 and "GQA group" in _err()
+    for Hq, Hkv, D in ((8, 8, 64), (8, 2, 96), (16, 1, 128), (64, 1, 8), (9, 1, 96)):
+        assert call(Hq, Hkv, D) == -4 and "workspace" in _err(), (Hq, Hkv, D)
+
+
 def test_varlen_entry_points_reject_bad_arguments():
     lib = _native.lib()
     fake = ctypes.c_void_p(1 << 20)

@@ -3,7 +3,11 @@ GQA group, prefill length, window, steps, metric, threshold, 16-bit type, initia
 capacity), each a prefill hand-off followed by decode steps that alternate between
 cache.update + decode_attention and the one-call cache.decode_step.  The cache state is
 bit-exact against the oracle (deltaDecoding.py:9-104, 181-233) and the attention within
-max-abs 2e-2 (bf16) / 5e-3 (fp16) of it (deltaDecoding.py:236-362)."""
+max-abs 2e-2 (bf16) / 5e-3 (fp16) of it (deltaDecoding.py:236-362).
+
+The same flow at head dimensions below 128 (the reference's decode kernels mask the
+head dimension to BLOCK_D, deltaDecoding.py:20,28-29,255-268; config 0 has d = 64) and
+at GQA groups above 8, which the attention scores in sub-groups of at most 8 heads."""
 from types import SimpleNamespace
 
 import numpy as np
@@ -40,17 +44,49 @@ def _id(c):
             f"{'f16' if c['fp16'] else 'bf16'}-cap{c['cap0']}")
 
 
+# (B, Hkv, G, D, N, W, steps, metric, tau at D = 128, fp16): config 0's shape (8 KV heads,
+# no GQA, d = 64), d = 96 under GQA 4, and groups of 9, 12 and 16 query heads (sub-groups
+# of 5 + 4 with one repeated slot, 6 + 6 and 8 + 8)
+DIM_CASES = [
+    dict(B=1, Hkv=8, G=1, D=64, N=1500, W=128, steps=40, metric="euclidean", tau=9.0, fp16=False),
+    dict(B=2, Hkv=2, G=4, D=96, N=900, W=50, steps=60, metric="cosine", tau=0.9, fp16=True),
+    dict(B=1, Hkv=2, G=4, D=96, N=1200, W=128, steps=50, metric="euclidean", tau=10.0, fp16=False),
+    dict(B=1, Hkv=1, G=12, D=64, N=700, W=16, steps=40, metric="euclidean", tau=8.0, fp16=False),
+    dict(B=1, Hkv=2, G=16, D=128, N=800, W=128, steps=30, metric="cosine", tau=0.75, fp16=False),
+    dict(B=2, Hkv=1, G=9, D=96, N=600, W=50, steps=30, metric="euclidean", tau=11.0, fp16=True),
+]
+for _i, _c in enumerate(DIM_CASES):
+    _c.update(cap0=64, seed=100 + _i, pattern=7919 * (_i + 1))
+
+
+def _dim_id(c):
+    return f"D{c['D']}-G{c['G']}-Hkv{c['Hkv']}-B{c['B']}-{c['metric'][:3]}-{'f16' if c['fp16'] else 'bf16'}"
+
+
 @pytest.mark.parametrize("c", CASES, ids=[_id(c) for c in CASES])
 def test_random_decode_vs_oracle(gpu, c):
-    from deltaattention_amd import attention, globVR
+    _run_case(gpu, c, _id(c))
+
+
+@pytest.mark.parametrize("c", DIM_CASES, ids=[_dim_id(c) for c in DIM_CASES])
+def test_decode_head_dims_and_large_groups(gpu, c):
+    # the Euclidean threshold scales with the distance, i.e. with sqrt(D)
+    c = dict(c, tau=c["tau"] * (c["D"] / 128) ** 0.5 if c["metric"] == "euclidean" else c["tau"])
+    _run_case(gpu, c, _dim_id(c))
+
+
+def _run_case(gpu, c, name):
+    from deltaattention_amd import attention, globVR, synth
     from deltaattention_amd.deltaDecoding import HybridCompressedCache, decode_attention
     B, Hkv, N, W, steps = c["B"], c["Hkv"], c["N"], c["W"], c["steps"]
+    D = c.get("D", 128)
     Hq = c["G"] * Hkv
     dtype = torch.float16 if c["fp16"] else torch.bfloat16
-    announce(f"decode sweep {_id(c)} tau={c['tau']:.3f}")
-    q, k, v = (t.to(dtype) for t in T._inputs(B, Hq, Hkv, N + steps, c["seed"]))
-    cfg = SimpleNamespace(hidden_size=Hq * 128, num_attention_heads=Hq, num_key_value_heads=Hkv,
-                          num_hidden_layers=1, head_dim=128)
+    announce(f"decode {name} tau={c['tau']:.3f}")
+    q, k, v = (t.to(dtype) for t in synth.make_layer_inputs(B, Hq, Hkv, N + steps, D, seed=c["seed"],
+                                                              rope_base=10000.0))
+    cfg = SimpleNamespace(hidden_size=Hq * D, num_attention_heads=Hq, num_key_value_heads=Hkv,
+                          num_hidden_layers=1, head_dim=D)
     saved = dict(vars(globVR))
     try:
         globVR.packing_mode, globVR.chunk_size = "delta", 512
@@ -84,7 +120,7 @@ def test_random_decode_vs_oracle(gpu, c):
         assert torch.equal(cache.v_packed[0, :, :, :n].float().cpu(), torch.from_numpy(st["v_packed"][:, :, :n]))
         assert torch.equal(cache.k_exact[0].float().cpu(), torch.from_numpy(st["k_exact"]))
         assert cache.get_seq_length(0) == N + steps
-        print(f"{_id(c)}: attention max-abs {worst:.3e}", flush=True)
+        print(f"{name}: attention max-abs {worst:.3e}, packed {n} of {N + steps}", flush=True)
         assert worst <= (5e-3 if c["fp16"] else 2e-2)
     finally:
         for name, val in saved.items():
