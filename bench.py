@@ -37,7 +37,10 @@ def parse_args():
     ap = argparse.ArgumentParser(description=__doc__.split("\n\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=30)
-    ap.add_argument("--warmup", type=int, default=5)
+    # the power manager settles within about 15 launches after idle or after a change of
+    # load (the first launches run 5-25 % slow); 20 untimed steps let the timed ones start
+    # in its steady state
+    ap.add_argument("--warmup", type=int, default=20)
     ap.add_argument("--config", type=int, default=1, choices=(1, 2, 3, 4),
                     help="1: one layer at 32K; 2: one layer at 128K; 3: full 32-layer "
                          "Llama-3-8B prefill of 65536 tokens (tokens/s, attention share); "
@@ -57,10 +60,12 @@ def parse_args():
     ap.add_argument("--select-arith", choices=("native", "fp32"), default="native",
                     help="Euclidean distance of the anchor selection: the keys' own 16-bit "
                          "arithmetic as the reference computes it (tritonModules.py:55-58), or fp32")
-    ap.add_argument("--only", choices=("delta", "hybrid", "dense", "compress", "copy", "convert"), default=None,
+    ap.add_argument("--only", choices=("delta", "hybrid", "dense", "compress", "copy", "convert", "peaks"),
+                    default=None,
                     help="run one part for K steps (copy: a 1 GiB device copy; convert: 1 GiB of fp32 "
                          "read and written as bf16 by a vectorized elementwise kernel -- the "
-                         "references for calibrating the WRITE_SIZE / FETCH_SIZE counters)")
+                         "references for calibrating the WRITE_SIZE / FETCH_SIZE counters; peaks: "
+                         "the on-box MFMA and copy ceilings, printed as JSON)")
     ap.add_argument("--decode", action="store_true",
                     help="per-token decode latency over the compressed cache left by a "
                          "config-1 prefill (update + attention), against the same decode "
@@ -473,42 +478,66 @@ def run_config4(args):
 
 
 def measure_peaks():
-    """On-box ceilings for the roofline fractions: the bf16 MFMA rate of an issue loop
-    with no memory traffic (libdeltaattn_diag.so: 1024 workgroups x 8 waves x 32 MFMAs per
-    round), and the HBM bandwidth of a 4 GiB device-to-device copy (bytes read + written),
-    each the best of 5 timed launches after a warm-up."""
+    """On-box ceilings for the roofline fractions, each the best of 5 timed launches after a
+    warm-up:
+
+    * the bf16 MFMA rate of an issue loop with no memory traffic (libdeltaattn_diag.so:
+      1024 workgroups x 8 waves x 32 MFMAs per round), once with constant operands and once
+      with random N(0, 1) operands, with the shader clock each holds (s_memtime cycles over
+      s_memrealtime's 100 MHz).  The chip's power limit lowers the clock as the multiplier
+      arrays switch: only the constant-operand loop comes near the published peak, and the
+      random-operand loop is the ceiling that data-bearing MFMA work (attention) can reach;
+    * the HBM bandwidth of a 4 GiB device-to-device copy (bytes read + written)."""
     import torch
     here = os.path.dirname(os.path.abspath(__file__))
     lib = ctypes.CDLL(os.path.join(here, "deltaattention_amd", "libdeltaattn_diag.so"))
     lib.diag_mfma_loop.restype = ctypes.c_int
-    lib.diag_mfma_loop.argtypes = [ctypes.c_void_p, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
-    grid, iters = 1024, 2000
+    lib.diag_mfma_loop.argtypes = [ctypes.c_void_p, ctypes.c_void_p, ctypes.c_void_p, ctypes.c_int, ctypes.c_int,
+                                   ctypes.c_void_p]
+    lib.diag_mfma_operand_count.restype = ctypes.c_int64
+    grid, iters = 1024, 4000
     sink = torch.empty(grid * 512, dtype=torch.float32, device="cuda")
+    clocks = torch.zeros(grid * 4, dtype=torch.int64, device="cuda")
+    gen = torch.Generator(device="cuda").manual_seed(1)
+    operands = torch.randn(lib.diag_mfma_operand_count() * 8, dtype=torch.float32, device="cuda",
+                           generator=gen).to(torch.bfloat16)
     stream = ctypes.c_void_p(torch.cuda.current_stream().cuda_stream)
-
-    def mfma():
-        rc = lib.diag_mfma_loop(ctypes.c_void_p(sink.data_ptr()), iters, grid, stream)
-        if rc != 0:
-            raise RuntimeError(f"diag_mfma_loop failed ({rc})")
-
-    mfma()
-    best = min(time_loop(mfma, 1) for _ in range(5))
     flops = grid * 8 * iters * 32 * 32768.0
+
+    def loop(ops):
+        def run():
+            rc = lib.diag_mfma_loop(ctypes.c_void_p(sink.data_ptr()), ops, ctypes.c_void_p(clocks.data_ptr()),
+                                    iters, grid, stream)
+            if rc != 0:
+                raise RuntimeError(f"diag_mfma_loop failed ({rc})")
+        run()
+        best = min(time_loop(run, 1) for _ in range(5))
+        c = clocks.view(grid, 4).cpu().double()
+        ghz = ((c[:, 1] - c[:, 0]) / ((c[:, 3] - c[:, 2]) * 10.0)).median().item()
+        return flops / (best * 1e-3) / 1e12, ghz
+
+    const_tf, const_ghz = loop(None)
+    live_tf, live_ghz = loop(ctypes.c_void_p(operands.data_ptr()))
     n = 1 << 31  # 2^31 bf16 elements: 4 GiB
     src = torch.empty(n, dtype=torch.bfloat16, device="cuda").fill_(1.0)
     dst = torch.empty_like(src)
     copy = lambda: dst.copy_(src)
     copy()
     best_copy = min(time_loop(copy, 1) for _ in range(5))
-    del src, dst, sink
+    del src, dst, sink, operands, clocks
     torch.cuda.empty_cache()
-    mfma_tf = flops / (best * 1e-3) / 1e12
     copy_gbs = 2.0 * n * 2 / (best_copy * 1e-3) / 1e9
-    log(f"peaks: MFMA loop {mfma_tf:.0f} TFLOP/s, copy {copy_gbs:.0f} GB/s")
-    return {"mfma_bf16_tflops": round(mfma_tf, 1), "mfma_frac_of_published": round(mfma_tf / BF16_PEAK_TFLOPS, 4),
+    log(f"peaks: MFMA loop {const_tf:.0f} TFLOP/s at {const_ghz:.2f} GHz (constant operands), "
+        f"{live_tf:.0f} TFLOP/s at {live_ghz:.2f} GHz (random operands), copy {copy_gbs:.0f} GB/s")
+    return {"mfma_bf16_tflops": round(const_tf, 1), "mfma_frac_of_published": round(const_tf / BF16_PEAK_TFLOPS, 4),
+            "mfma_clock_ghz": round(const_ghz, 3),
+            "mfma_live_bf16_tflops": round(live_tf, 1),
+            "mfma_live_frac_of_published": round(live_tf / BF16_PEAK_TFLOPS, 4),
+            "mfma_live_clock_ghz": round(live_ghz, 3),
             "copy_gbs": round(copy_gbs, 1), "copy_frac_of_published": round(copy_gbs / HBM_PEAK_GBS, 4),
-            "note": "MFMA: v_mfma_f32_32x32x16_bf16 issue loop, no memory traffic; copy: 4 GiB "
-                    "device-to-device, read + write bytes"}
+            "note": "MFMA: v_mfma_f32_32x32x16_bf16 issue loop, no memory traffic, constant operands "
+                    "(mfma_*) and random N(0,1) operands (mfma_live_*: the power limit lowers the "
+                    "shader clock); copy: 4 GiB device-to-device, read + write bytes"}
 
 
 def main():
@@ -531,6 +560,9 @@ def main():
         return
     if args.decode:
         run_decode(args)
+        return
+    if args.only == "peaks":
+        print(json.dumps(measure_peaks()), flush=True)
         return
     if args.only:
         run_only(args)
@@ -572,6 +604,7 @@ def main():
         rec["peaks_measured"] = measure_peaks()
         pk = rec["peaks_measured"]
         rec["roofline"]["frac_of_measured_peak"] = round(rec["roofline"]["achieved"] / pk["mfma_bf16_tflops"], 4)
+        rec["roofline"]["frac_of_live_mfma_peak"] = round(rec["roofline"]["achieved"] / pk["mfma_live_bf16_tflops"], 4)
         rec["compress_frac_of_measured_copy"] = round(rec["compress_gbs"] / pk["copy_gbs"], 4)
     if not args.no_cpu_baseline:
         log("cpu baseline (config 1 and config 0 in full) ...")
