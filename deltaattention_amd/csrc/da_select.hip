@@ -37,10 +37,18 @@ namespace da {
 constexpr int kSelBatch = 32;
 constexpr int64_t kSelPairMinChunks = 2048;
 
-// x rounded to the 16-bit type DT (nearest even) and widened back to fp32.
+// x rounded to the 16-bit type DT (nearest even) and widened back to fp32.  For bf16
+// one v_cvt_pk_bf16_f32 with x in the high half and 0 in the low half leaves exactly
+// that fp32 value in the register (the widening is free); fp16 converts there and back.
 template <int DT>
 __device__ __forceinline__ float round16(float x) {
-  return E16<DT>::one(E16<DT>::bits(x));
+  if constexpr (DT == DA_BF16) {
+    // as asm: written in C the compiler swaps the halves back and adds a v_perm_b32
+    float r;
+    asm("v_cvt_pk_bf16_f32 %0, 0, %1" : "=v"(r) : "v"(x));
+    return r;
+  } else
+    return E16<DT>::one(E16<DT>::bits(x));
 }
 
 // wave_tree_sum_all with every addition rounded to DT: the same pairing (DPP lane^1,
