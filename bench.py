@@ -9,7 +9,8 @@ reference times as time_get_row_delta + time_delta_mm_pattern,
 modeling_llama.py:612-754).
 
 The default run measures config 1 (N = 32768, r = 4) as the headline and adds to the same
-JSON line: config 2 (N = 131072) at r = 2, 4 and 8, the config-4 ragged batch, the
+JSON line: config 2 (N = 131072) at r = 2, 4 and 8, the same layer at N = 262144 and r = 4
+(the reference's longest point, key ``n262144_r4``), the config-4 ragged batch, the
 config-3 end-to-end 32-layer prefill, the selection in both arithmetic definitions, the
 on-box MFMA and copy ceilings, and the CPU baseline (config 1 and config 0 in full).
 ``--config 2`` runs N = 131072 alone with ``--ratio`` in {2, 4, 8}.  The threshold tau is
@@ -72,6 +73,8 @@ def parse_args():
                          "attention over the uncompressed cache")
     ap.add_argument("--decode-tokens", type=int, default=200)
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-262k", action="store_true",
+                    help="leave the N = 262144, r = 4 point out of the default run")
     ap.add_argument("--no-128k", action="store_true",
                     help="config 1 only: skip the config-2 (N=131072, r=2/4/8) measurements")
     ap.add_argument("--no-e2e", action="store_true",
@@ -585,6 +588,14 @@ def main():
             extra = measure_layer(args, 131072, r, headline=False, inputs=(q, k, v), shared=shared)
             rec[f"config2_r{int(r)}"] = extra
         del q, k, v, shared
+        torch.cuda.empty_cache()
+    if full and not args.no_262k:
+        # the reference's longest point (eval_speedup.py:28): the config-2 layer at 262144
+        # tokens, r = 4, with its own dense and SDPA controls
+        log("N=262144, r=4 ...")
+        q, k, v = layer_inputs(args, 262144)
+        rec["n262144_r4"] = measure_layer(args, 262144, 4.0, headline=False, inputs=(q, k, v), shared={})
+        del q, k, v
         torch.cuda.empty_cache()
     if full and not args.no_e2e:
         c4 = config4_record(args, warmup=3, steps=10)

@@ -7,7 +7,8 @@ Every configuration runs the HIP path at its real shape and sizes:
 * config 1: the benchmarked layer (B = 1, Hq = 32, Hkv = 8, D = 128, N = 32768, r = 4,
   the bench's own seeded inputs) -- selection and packing bit-exact at full size, the
   hybrid and dense outputs on query blocks spread from the first to the last;
-* config 2: the same layer at N = 131072 for r in {2, 4, 8};
+* config 2: the same layer at N = 131072 for r in {2, 4, 8}, and at N = 262144 for r = 4
+  (the reference's longest point);
 * config 3: a Llama-3-8B-shaped model (2 layers) prefilling 65536 tokens through the
   transformers swap with periodic anchors (r = 4); layer 0's attention is compared;
 * config 4: a ragged batch of 8 sequences of 4096..32768 tokens with rho ~ U[0.6, 0.95]
@@ -187,6 +188,19 @@ def test_config2_layer(gpu, config2_inputs, ratio):
     q, k, v = config2_inputs
     tau, r_real = synth.calibrate_threshold(k, ratio)
     _layer_parity(q, k, v, tau, 6, f"config2 r={ratio:g} (realised {r_real:.3f})")
+
+
+# --------------------------------------------------------------------------------------
+# the reference's longest point (eval_speedup.py:28, the paper's 262K): the config-2 layer
+# at N = 262144, r = 4 -- selection and packing bit-exact at full size, attention on query
+# blocks from the first to the last
+# --------------------------------------------------------------------------------------
+def test_layer_262k(gpu):
+    from deltaattention_amd import synth
+    announce("262K inputs N=262144")
+    q, k, v = _layer(262144, 0, gpu)
+    tau, r_real = synth.calibrate_threshold(k, 4.0)
+    _layer_parity(q, k, v, tau, 4, f"N=262144 r=4 (realised {r_real:.3f})")
 
 
 # --------------------------------------------------------------------------------------
