@@ -119,6 +119,9 @@ int da_pack(const int32_t* keep, const void* k, const void* v, int dtype, int64_
  * timestamp is >= start_m - W; Phase 2 starts at ((last+1)/128)*128).
  * D: a multiple of 8 in [8, 128] (the kernels zero-fill dims D..127, as the reference's
  * BLOCK_D = next_pow2(D) masked loads do, deltaFlashAttention.py:39-42); Hq % Hkv == 0.
+ * workspace: da_hybrid_workspace_size() bytes (the schedule, the key biases and the
+ *   attention grid's work-queue counters, all written by the call on its stream): calls
+ *   in stream order may share one workspace, concurrent calls may not.
  */
 int64_t da_hybrid_workspace_size(int64_t B, int64_t Hkv, int64_t num_packed);
 int da_hybrid_prefill(const void* q, const void* k, const void* v, const void* k_packed,
