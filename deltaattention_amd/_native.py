@@ -127,12 +127,13 @@ def strides_array(values) -> ctypes.Array:
 
 
 def dtype_code(*ts) -> int:
-    """DA_BF16 or DA_F16 for tensors that all share one of those dtypes."""
+    """DA_BF16, DA_F16 or DA_F32 for tensors that all share one of those dtypes (the entry
+    points that do not take fp32, the decode ones, refuse DA_F32 with DA_ERR_UNSUPPORTED)."""
     import torch
-    codes = {torch.bfloat16: DA_BF16, torch.float16: DA_F16}
+    codes = {torch.bfloat16: DA_BF16, torch.float16: DA_F16, torch.float32: DA_F32}
     dt = ts[0].dtype
     if dt not in codes:
-        raise TypeError(f"expected bfloat16 or float16 tensors, got {dt}")
+        raise TypeError(f"expected bfloat16, float16 or float32 tensors, got {dt}")
     for t in ts[1:]:
         if t is not None and t.dtype != dt:
             raise TypeError(f"all tensors must share one dtype ({dt}), got {t.dtype}")

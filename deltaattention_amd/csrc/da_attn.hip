@@ -1341,6 +1341,223 @@ __global__ __launch_bounds__(kSchedThreads) void hybrid_schedule_kernel(const in
   }
 }
 
+// ====================================================================================
+// fp32 tensors.  The reference's kernels take fp32 Q, K, V as they take 16-bit ones
+// (dtype-agnostic loads, deltaFlashAttention.py:41-42, 80; flashAttention.py:94-130), and
+// p.to(v.dtype) then leaves p in fp32 (:98, :137).  attn_f32_kernel computes the same
+// attention in fp32 throughout: one workgroup of 256 threads per (batch, query head,
+// 64 query rows), LDS tiles of 64 keys, fp32 FMAs on the VALU (the MFMA path is 16-bit),
+// an exact running maximum (rescaled at every new maximum) and P.V on the fp32 p.  The
+// logical 128-row schedule, the key biases log2(w)/c and the variants come from the same
+// schedule pre-pass as the 16-bit kernels.  Thread (ti, tj) holds scores of rows
+// 4 ti .. 4 ti + 3 and keys tj + 16 jj, and output dims 4 tj + 64 gg of the same rows.
+// ====================================================================================
+constexpr int kFRows = 64, kFKeys = 64;
+constexpr int kFStride = kD + 4;        // row stride (floats) of the Q, K and V tiles
+constexpr int kFPStride = kFKeys + 4;   // row stride of the P tile
+constexpr int kFLds = (kFRows * kFStride + 2 * kFKeys * kFStride + kFRows * kFPStride + 2 * kFKeys) * 4;
+
+template <int VARIANT>
+__global__ __launch_bounds__(256) void attn_f32_kernel(AttnArgs a) {
+  extern __shared__ __attribute__((aligned(16))) float fsm[];
+  float* const sQ = fsm;
+  float* const sK = sQ + kFRows * kFStride;
+  float* const sV = sK + kFKeys * kFStride;
+  float* const sP = sV + kFKeys * kFStride;
+  float* const sB = sP + kFRows * kFPStride;  // the tile's key biases (units of the score)
+  int* const sT = (int*)(sB + kFKeys);        // the tile's timestamps (pure Phase 1)
+  const int tid = threadIdx.x;
+  const int ti = tid >> 4, tj = tid & 15;
+  const int nrb = (a.Nq + kFRows - 1) / kFRows;
+  const int rb = (int)(blockIdx.x % (unsigned)nrb);
+  const int bh = (int)(blockIdx.x / (unsigned)nrb);
+  const int h = bh % a.Hq, b = bh / a.Hq;
+  const int g = h / a.G;
+  const int bg = b * a.Hkv + g;
+  const int Nq = a.seq.cu ? a.seq.len(b) : a.Nq;
+  const int Nk = a.seq.cu ? a.seq.len(b) : a.Nk;
+  const int R0 = rb * kFRows;
+  if (R0 >= Nq) return;  // a row block past the end of a shorter sequence (whole workgroup)
+  const int D = a.D;
+  const float c = a.scale_log2;
+
+  // ---- schedule of the logical 128-row block holding these rows (every wave computes
+  // the same values).  Phase 1: packed keys [0, n1); Phase 2: keys [ds, kend), causal.
+  // Keys past the block's own last row are all masked, so Phase 2 ends there. ----
+  const int start_m = (R0 / kBlock) * kBlock;
+  int P = a.P_host;
+  if (a.P_dev) P = min(a.seq.cu ? a.P_dev[b] : *a.P_dev, a.P_host);
+  if (a.seq.cu) P = min(P, Nk);
+  int n1 = 0, ds = 0;
+  int kend = a.causal ? min(Nk, R0 + kFRows) : Nk;
+  if (VARIANT == kHybrid || VARIANT == kSanity) {
+    const int nblk = (P + kBlock - 1) / kBlock;
+    const int32_t* bmax = a.sched + (int64_t)bg * 2 * a.nblk_cap;
+    int n_safe, last;
+    safe_prefix(bmax, bmax + a.nblk_cap, nblk, start_m - a.window, n_safe, last, tid & 63);
+    ds = max(0, ((last + 1) / kBlock) * kBlock);
+    if (VARIANT == kHybrid) n1 = min(n_safe * kBlock, a.wcap);
+  } else if (VARIANT == kPure) {
+    n1 = P;
+    kend = 0;
+  }
+  const int t1 = (n1 + kFKeys - 1) / kFKeys;
+  const int t2 = kend > ds ? (kend - ds + kFKeys - 1) / kFKeys : 0;
+
+  const float* qg = (const float*)a.q + a.seq.base(b, a.sq_b, a.sq_n) + (int64_t)h * a.sq_h;
+  const float* kg = (const float*)a.k + a.seq.base(b, a.sk_b, a.sk_n) + (int64_t)g * a.sk_h;
+  const float* vg = (const float*)a.v + a.seq.base(b, a.sv_b, a.sv_n) + (int64_t)g * a.sv_h;
+  const float* kpg = (const float*)a.kp + a.seq.base(b, a.skp_b, a.skp_n) + (int64_t)g * a.skp_h;
+  const float* vpg = (const float*)a.vp + a.seq.base(b, a.svp_b, a.svp_n) + (int64_t)g * a.svp_h;
+  const float* wrow = a.wts ? a.wts + (int64_t)bg * a.wcap : nullptr;
+  const int32_t* tsrow = a.tsw ? a.tsw + (int64_t)bg * a.wcap : nullptr;
+
+  // ---- Q of the 64 rows (rows past Nq and dims past D are zero) ----
+  for (int i = tid; i < kFRows * (kD / 4); i += 256) {
+    const int r = i / (kD / 4), d = 4 * (i % (kD / 4));
+    float4 x = {0.0f, 0.0f, 0.0f, 0.0f};
+    if (R0 + r < Nq && d < D) x = *(const float4*)(qg + (int64_t)(R0 + r) * a.sq_n + d);
+    *(float4*)(sQ + r * kFStride + d) = x;
+  }
+
+  float o[4][2][4];
+  float m[4], l[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    m[i] = -INFINITY;
+    l[i] = 0.0f;
+#pragma unroll
+    for (int gg = 0; gg < 2; ++gg)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[i][gg][e] = 0.0f;
+  }
+
+  for (int t = 0; t < t1 + t2; ++t) {
+    const bool ph1 = t < t1;
+    const int key0 = ph1 ? t * kFKeys : ds + (t - t1) * kFKeys;
+    if (!ph1 && a.causal && key0 > R0 + kFRows - 1) break;  // every later tile is masked
+    const int kvalid = ph1 ? n1 : kend;  // keys [key0, kvalid) of this tile are real
+    const int klimit = ph1 ? P : Nk;     // rows of the source tensor that exist
+    const float* ksrc = ph1 ? kpg : kg;
+    const float* vsrc = ph1 ? vpg : vg;
+    const int64_t skn = ph1 ? a.skp_n : a.sk_n, svn = ph1 ? a.svp_n : a.sv_n;
+    __syncthreads();  // the previous tile's K, V, P and biases are read
+    for (int i = tid; i < kFKeys * (kD / 4); i += 256) {
+      const int r = i / (kD / 4), d = 4 * (i % (kD / 4));
+      const int key = key0 + r;
+      float4 kx = {0.0f, 0.0f, 0.0f, 0.0f}, vx = kx;
+      if (key < kvalid && key < klimit && d < D) {
+        kx = *(const float4*)(ksrc + (int64_t)key * skn + d);
+        vx = *(const float4*)(vsrc + (int64_t)key * svn + d);
+      }
+      *(float4*)(sK + r * kFStride + d) = kx;
+      *(float4*)(sV + r * kFStride + d) = vx;
+    }
+    if (tid < kFKeys) {
+      const int key = key0 + tid;
+      float bias = key < kvalid ? 0.0f : -INFINITY;
+      int ts = 0;
+      if (ph1 && (VARIANT == kHybrid || VARIANT == kPure) && key < kvalid) bias = wrow[key];
+      if (ph1 && VARIANT == kPure && key < kvalid) ts = tsrow[key];
+      sB[tid] = bias;
+      sT[tid] = ts;
+    }
+    __syncthreads();
+
+    // ---- scores of rows 4 ti + i and keys tj + 16 jj ----
+    float sc[4][4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) sc[i][jj] = 0.0f;
+    for (int d = 0; d < D; d += 4) {
+      float4 qv[4], kv[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) qv[i] = *(const float4*)(sQ + (4 * ti + i) * kFStride + d);
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) kv[jj] = *(const float4*)(sK + (tj + 16 * jj) * kFStride + d);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int jj = 0; jj < 4; ++jj) {
+          sc[i][jj] = __builtin_fmaf(qv[i].x, kv[jj].x, sc[i][jj]);
+          sc[i][jj] = __builtin_fmaf(qv[i].y, kv[jj].y, sc[i][jj]);
+          sc[i][jj] = __builtin_fmaf(qv[i].z, kv[jj].z, sc[i][jj]);
+          sc[i][jj] = __builtin_fmaf(qv[i].w, kv[jj].w, sc[i][jj]);
+        }
+    }
+    // ---- masks, online softmax (exact maximum), p to LDS ----
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = R0 + 4 * ti + i;
+      float mt = -INFINITY;
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        const int kl = tj + 16 * jj;
+        bool ok = sB[kl] != -INFINITY;
+        if (!ph1 && a.causal) ok = ok && key0 + kl <= row;                 // deltaFlashAttention.py:126-130
+        if (VARIANT == kPure) ok = ok && sT[kl] <= row;                    // :338-341
+        sc[i][jj] = ok ? (sc[i][jj] + sB[kl]) * c : -INFINITY;
+        mt = __builtin_fmaxf(mt, sc[i][jj]);
+      }
+#pragma unroll
+      for (int x = 1; x < 16; x <<= 1) mt = __builtin_fmaxf(mt, __shfl_xor(mt, x, 64));
+      const float mn = __builtin_fmaxf(m[i], mt);
+      const float alpha = mn == -INFINITY ? 1.0f : exp2f(m[i] - mn);
+      float ps = 0.0f;
+#pragma unroll
+      for (int jj = 0; jj < 4; ++jj) {
+        const float pv = mn == -INFINITY ? 0.0f : exp2f(sc[i][jj] - mn);
+        ps += pv;
+        sP[(4 * ti + i) * kFPStride + tj + 16 * jj] = pv;
+      }
+#pragma unroll
+      for (int x = 1; x < 16; x <<= 1) ps += __shfl_xor(ps, x, 64);
+      l[i] = l[i] * alpha + ps;
+      m[i] = mn;
+#pragma unroll
+      for (int gg = 0; gg < 2; ++gg)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[i][gg][e] *= alpha;
+    }
+    __syncthreads();
+    // ---- O += P V on dims 4 tj + 64 gg ----
+    for (int j = 0; j < kFKeys; ++j) {
+      float pj[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) pj[i] = sP[(4 * ti + i) * kFPStride + j];
+#pragma unroll
+      for (int gg = 0; gg < 2; ++gg) {
+        const float4 vv = *(const float4*)(sV + j * kFStride + 4 * tj + 64 * gg);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          o[i][gg][0] = __builtin_fmaf(pj[i], vv.x, o[i][gg][0]);
+          o[i][gg][1] = __builtin_fmaf(pj[i], vv.y, o[i][gg][1]);
+          o[i][gg][2] = __builtin_fmaf(pj[i], vv.z, o[i][gg][2]);
+          o[i][gg][3] = __builtin_fmaf(pj[i], vv.w, o[i][gg][3]);
+        }
+      }
+    }
+  }
+
+  // ---- normalise and store rows < Nq, dims < D ----
+  float* og = (float*)a.out + a.seq.base(b, a.so_b, a.so_n) + (int64_t)h * a.so_h;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int row = R0 + 4 * ti + i;
+    if (row >= Nq) continue;
+    // a row without any key (pure Phase 1) stays zero, deltaFlashAttention.py:353-354
+    const float inv = l[i] > 0.0f ? 1.0f / l[i] : 0.0f;
+#pragma unroll
+    for (int gg = 0; gg < 2; ++gg) {
+      const int d = 4 * tj + 64 * gg;
+      if (d < D)
+        *(float4*)(og + (int64_t)row * a.so_n + d) =
+            float4{o[i][gg][0] * inv, o[i][gg][1] * inv, o[i][gg][2] * inv, o[i][gg][3] * inv};
+    }
+  }
+}
+
 template <int V, int DT>
 static const void* attn_kernel_fn() {
   if constexpr (V == kPure) return reinterpret_cast<const void*>(&attn_kernel_pure<DT>);
@@ -1418,7 +1635,30 @@ static int launch_attn_dt(int variant, AttnArgs& a, hipStream_t st) {
   }
 }
 
+template <int V>
+static int launch_attn_f32_t(const AttnArgs& a, hipStream_t st) {
+  static int done = 0;
+  if (!done) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&attn_f32_kernel<V>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, kFLds);
+    if (e != hipSuccess) return set_error(DA_ERR_HIP, "hipFuncSetAttribute: %s", hipGetErrorString(e));
+    done = 1;
+  }
+  const int64_t grid = (int64_t)a.B * a.Hq * ((a.Nq + kFRows - 1) / kFRows);
+  if (grid >= (1ll << 31)) return set_error(DA_ERR_INVALID, "attention (fp32): grid too large");
+  hipLaunchKernelGGL((attn_f32_kernel<V>), dim3((unsigned)grid), dim3(256), kFLds, st, a);
+  return check_launch("attention kernel (fp32)");
+}
+
 static int launch_attn(int variant, int dtype, AttnArgs& a, hipStream_t st) {
+  if (dtype == DA_F32) {
+    switch (variant) {
+      case kHybrid: return launch_attn_f32_t<kHybrid>(a, st);
+      case kSanity: return launch_attn_f32_t<kSanity>(a, st);
+      case kPure: return launch_attn_f32_t<kPure>(a, st);
+      default: return launch_attn_f32_t<kDense>(a, st);
+    }
+  }
   return dtype == DA_F16 ? launch_attn_dt<DA_F16>(variant, a, st) : launch_attn_dt<DA_BF16>(variant, a, st);
 }
 
@@ -1549,7 +1789,7 @@ static int hybrid_impl(const char* who, AttnArgs& a, const void* k_packed, const
   }
   const unsigned prep_chunks = prep.wts ? (unsigned)((wl.wcap + kSchedThreads - 1) / kSchedThreads) : 0u;
   // the grouped kernel's persistent grid takes its items from 8 counters in the workspace
-  a.queue = a.hpw == 4 ? (int*)(ws + wl.queue_off) : nullptr;
+  a.queue = a.hpw == 4 && dtype != DA_F32 ? (int*)(ws + wl.queue_off) : nullptr;
   hipLaunchKernelGGL(hybrid_schedule_kernel, dim3((unsigned)(B * Hkv), 1 + prep_chunks), dim3(kSchedThreads), 0, st,
                      timestamps, a.sts_b, a.sts_h, (int)Hkv, (int)P_bound, num_packed_dev, (int)Nk, a.seq,
                      a.nblk_cap, (int32_t*)ws, prep, a.queue);
@@ -1567,8 +1807,8 @@ extern "C" int da_hybrid_prefill(const void* q, const void* k, const void* v, co
                                  int variant, int no_count, void* workspace,
                                  int64_t workspace_bytes, void* stream) {
   const char* who = "da_hybrid_prefill";
-  if (dtype != DA_BF16 && dtype != DA_F16)
-    return set_error(DA_ERR_UNSUPPORTED, "%s: tensors must be bf16 or fp16", who);
+  if (dtype != DA_BF16 && dtype != DA_F16 && dtype != DA_F32)
+    return set_error(DA_ERR_UNSUPPORTED, "%s: tensors must be bf16, fp16 or fp32", who);
   AttnArgs a = {};
   if (int rc = fill_common(a, q, k, v, out, B, Hq, Hkv, Nq, Nk, D, strides, scale, who)) return rc;
   a.seq = SeqMap{nullptr, 0, (int)Nq};
@@ -1581,8 +1821,8 @@ extern "C" int da_dense_prefill(const void* q, const void* k, const void* v, voi
                                 int64_t B, int64_t Hq, int64_t Hkv, int64_t Nq, int64_t Nk,
                                 int64_t D, const int64_t* strides, int causal, float scale,
                                 void* stream) {
-  if (dtype != DA_BF16 && dtype != DA_F16)
-    return set_error(DA_ERR_UNSUPPORTED, "da_dense_prefill: tensors must be bf16 or fp16");
+  if (dtype != DA_BF16 && dtype != DA_F16 && dtype != DA_F32)
+    return set_error(DA_ERR_UNSUPPORTED, "da_dense_prefill: tensors must be bf16, fp16 or fp32");
   AttnArgs a = {};
   int rc = fill_common(a, q, k, v, out, B, Hq, Hkv, Nq, Nk, D, strides, scale, "da_dense_prefill");
   if (rc) return rc;
@@ -1598,8 +1838,8 @@ extern "C" int da_dense_prefill(const void* q, const void* k, const void* v, voi
 static int varlen_common(const char* who, AttnArgs& a, const void* q, const void* k, const void* v, void* out,
                          int dtype, int64_t B, int64_t Hq, int64_t Hkv, int64_t T, int64_t D,
                          const int64_t* strides, const int32_t* cu_seqlens, int64_t max_seqlen, float scale) {
-  if (dtype != DA_BF16 && dtype != DA_F16)
-    return set_error(DA_ERR_UNSUPPORTED, "%s: tensors must be bf16 or fp16", who);
+  if (dtype != DA_BF16 && dtype != DA_F16 && dtype != DA_F32)
+    return set_error(DA_ERR_UNSUPPORTED, "%s: tensors must be bf16, fp16 or fp32", who);
   DA_REQUIRE(cu_seqlens, "%s: null cu_seqlens", who);
   DA_REQUIRE(T > 0 && max_seqlen > 0 && max_seqlen <= T, "%s: need 0 < max_seqlen <= total tokens", who);
   DA_REQUIRE(T < (1ll << 31), "%s: too many tokens", who);

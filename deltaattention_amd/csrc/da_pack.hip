@@ -164,7 +164,9 @@ struct PackOut {
 };
 
 // VEC: K, V and the packed rows are 16-byte aligned with D a multiple of 8, and each
-// anchor row moves as 16-byte chunks, four rows per load instruction.
+// anchor row moves as 16-byte chunks, four rows per load instruction.  D counts 16-bit
+// words (rows of fp32 elements are moved as twice as many words): up to 256, a row in
+// one or two passes of 16 chunks (VEC) or 64 words.
 template <bool VEC>
 __global__ __launch_bounds__(256) void pack_scatter_kernel(
     const int32_t* __restrict__ keep, const uint16_t* __restrict__ k,
@@ -223,11 +225,13 @@ __global__ __launch_bounds__(256) void pack_scatter_kernel(
       __builtin_amdgcn_wave_barrier();
       __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront", "local");
       const int na = __popcll(bits);
-      const int sub = lane >> 4, cq = lane & 15;
-      const bool actq = cq < (D >> 3);
-      const uint16_t* kbase = k + seq.base((int)b, sk_b, sk_n) + h * sk_h + 8 * cq;
-      const uint16_t* vbase = v + seq.base((int)b, sv_b, sv_n) + h * sv_h + 8 * cq;
+      const int sub = lane >> 4;
+      for (int c0 = 0; c0 < (D >> 3); c0 += 16)
       for (int j0 = 0; j0 < na; j0 += 16) {
+        const int cq = c0 + (lane & 15);
+        const bool actq = cq < (D >> 3);
+        const uint16_t* kbase = k + seq.base((int)b, sk_b, sk_n) + h * sk_h + 8 * cq;
+        const uint16_t* vbase = v + seq.base((int)b, sv_b, sv_n) + h * sv_h + 8 * cq;
         uint4 kw[4], vw[4];
         int64_t dj[4];
 #pragma unroll
@@ -251,10 +255,12 @@ __global__ __launch_bounds__(256) void pack_scatter_kernel(
     // Copy the anchor rows, sixteen rows per step so that their loads are in flight
     // together (a 64-row group holds about 64 / r anchors).
     constexpr int kRows = 16;
-    const uint16_t* kbase = k + seq.base((int)b, sk_b, sk_n) + h * sk_h + 2 * lane;
-    const uint16_t* vbase = v + seq.base((int)b, sv_b, sv_n) + h * sv_h + 2 * lane;
-    const bool act = lane < nw;
-    uint64_t rem = VEC ? 0ull : bits;
+    for (int w0 = 0; w0 < (VEC ? 0 : nw); w0 += 64) {
+    const int wl = w0 + lane;
+    const uint16_t* kbase = k + seq.base((int)b, sk_b, sk_n) + h * sk_h + 2 * wl;
+    const uint16_t* vbase = v + seq.base((int)b, sv_b, sv_n) + h * sv_h + 2 * wl;
+    const bool act = wl < nw;
+    uint64_t rem = bits;
     int64_t dst = off;
     while (rem) {
       int rows[kRows];
@@ -278,11 +284,12 @@ __global__ __launch_bounds__(256) void pack_scatter_kernel(
       for (int j = 0; j < kRows; ++j) {
         const int64_t d = dst + j;
         if (act && j < nr && d < capacity) {
-          *(uint32_t*)(po.kp + kp_row0 + d * po.sp_n + 2 * lane) = kw[j];
-          *(uint32_t*)(po.vp + kp_row0 + d * po.sp_n + 2 * lane) = vw[j];
+          *(uint32_t*)(po.kp + kp_row0 + d * po.sp_n + 2 * wl) = kw[j];
+          *(uint32_t*)(po.vp + kp_row0 + d * po.sp_n + 2 * wl) = vw[j];
         }
       }
       dst += nr;
+    }
     }
   }
 
@@ -348,10 +355,14 @@ extern "C" int da_pack(const int32_t* keep, const void* k, const void* v, int dt
   DA_REQUIRE(keep && k && v && k_packed && v_packed && timestamps && counts && anchor_counts &&
                  num_packed,
              "da_pack: null pointer");
-  if (dtype != DA_BF16 && dtype != DA_F16)
-    return set_error(DA_ERR_UNSUPPORTED, "da_pack: K and V must be bf16 or fp16");
+  if (dtype != DA_BF16 && dtype != DA_F16 && dtype != DA_F32)
+    return set_error(DA_ERR_UNSUPPORTED, "da_pack: K and V must be bf16, fp16 or fp32");
   DA_REQUIRE(B > 0 && Hkv > 0 && N > 0 && D > 0 && capacity > 0, "da_pack: empty shape");
   if (D > 128 || (D & 1)) return set_error(DA_ERR_UNSUPPORTED, "da_pack: head_dim must be even and <= 128");
+  if (dtype == DA_F32) {  // the rows move as 16-bit words: twice as many, at twice the strides
+    D *= 2;
+    sk_b *= 2, sk_h *= 2, sk_n *= 2, sv_b *= 2, sv_h *= 2, sv_n *= 2;
+  }
   const int64_t ngroups = (N + 63) / 64;
   if (ngroups > kMaxGroups) return set_error(DA_ERR_UNSUPPORTED, "da_pack: sequence longer than %d", kMaxGroups * 64);
   DA_REQUIRE(B * Hkv < 65536, "da_pack: too many heads");
@@ -381,10 +392,14 @@ extern "C" int da_pack_varlen(const int32_t* keep, const void* k, const void* v,
   DA_REQUIRE(keep && k && v && k_packed && v_packed && timestamps && counts && anchor_counts && num_packed &&
                  cu_seqlens,
              "%s: null pointer", who);
-  if (dtype != DA_BF16 && dtype != DA_F16)
-    return set_error(DA_ERR_UNSUPPORTED, "%s: K and V must be bf16 or fp16", who);
+  if (dtype != DA_BF16 && dtype != DA_F16 && dtype != DA_F32)
+    return set_error(DA_ERR_UNSUPPORTED, "%s: K and V must be bf16, fp16 or fp32", who);
   DA_REQUIRE(B > 0 && Hkv > 0 && T > 0 && D > 0, "%s: empty shape", who);
   if (D > 128 || (D & 1)) return set_error(DA_ERR_UNSUPPORTED, "%s: head_dim must be even and <= 128", who);
+  if (dtype == DA_F32) {  // the rows move as 16-bit words: twice as many, at twice the strides
+    D *= 2;
+    sk_t *= 2, sk_h *= 2, sv_t *= 2, sv_h *= 2;
+  }
   DA_REQUIRE(T < (1ll << 31) && max_seqlen > 0 && max_seqlen <= T, "%s: need 0 < max_seqlen <= total tokens < 2^31", who);
   const int64_t ngroups = (max_seqlen + 63) / 64;
   if (ngroups > kMaxGroups) return set_error(DA_ERR_UNSUPPORTED, "%s: sequence longer than %d", who, kMaxGroups * 64);

@@ -66,22 +66,39 @@ __device__ __forceinline__ float wave_tree_sum_all_r16(float t) {
   return round16<DT>(__uint_as_float(q[0]) + __uint_as_float(q[1]));
 }
 
+// A lane's two key elements (2l, 2l + 1) of one row: one 4-byte word of a 16-bit type,
+// or two fp32 values (8 bytes; fp32 keys are compared in fp32, the reference's
+// arithmetic on fp32 tensors).
+template <int DT>
+struct SelKey {
+  using Elem = uint16_t;
+  using Row = uint32_t;
+  static __device__ __forceinline__ float lo(Row w) { return E16<DT>::lo(w); }
+  static __device__ __forceinline__ float hi(Row w) { return E16<DT>::hi(w); }
+};
+template <>
+struct SelKey<DA_F32> {
+  using Elem = float;
+  using Row = u32x2;
+  static __device__ __forceinline__ float lo(Row w) { return __uint_as_float(w[0]); }
+  static __device__ __forceinline__ float hi(Row w) { return __uint_as_float(w[1]); }
+};
+
 // One key of the walk: the decision and the anchor update without a branch (the
 // decision is the same in every lane).
 template <bool COS, bool A16, int DT>
-__device__ __forceinline__ bool select_step(uint32_t xb, float& a0, float& a1, float& a_norm,
+__device__ __forceinline__ bool select_step(float x0, float x1, float& a0, float& a1, float& a_norm,
                                             float thr) {
 #pragma clang fp contract(off)
-  const float x0 = E16<DT>::lo(xb), x1 = E16<DT>::hi(xb);
   const float eps = 1e-8f;
   bool kp;
   float x_norm = 0.0f;
-  if (COS) {  // tritonModules.py:48-54
+  if constexpr (COS) {  // tritonModules.py:48-54
     const float dot = wave_tree_sum_all(pair_dot(x0, x1, a0, a1));
     x_norm = sqrt_rn(wave_tree_sum_all(pair_dot(x0, x1, x0, x1)) + eps);
     const float sim = __fdiv_rn(dot, x_norm * a_norm);
     kp = sim < thr;
-  } else if (A16) {  // tritonModules.py:55-58 in the keys' 16-bit arithmetic
+  } else if constexpr (A16) {  // tritonModules.py:55-58 in the keys' 16-bit arithmetic
     const float d0 = round16<DT>(x0 - a0), d1 = round16<DT>(x1 - a1);
     const float p0 = round16<DT>(d0 * d0), p1 = round16<DT>(d1 * d1);
     kp = wave_tree_sum_all_r16<DT>(round16<DT>(p0 + p1)) > thr;
@@ -122,15 +139,18 @@ __global__ __launch_bounds__(256) void select_kernel(
   // rows are 32-bit from here on (N < 2^31)
   const int s = (int)(c * csb);
   const int e = (int)((c * csb + csb < Nb) ? c * csb + csb : Nb);
-  const uint16_t* base = k + seq.base((int)b, sk_b, sk_n) + h * sk_h + 2 * lane;
+  using KT = SelKey<DT>;
+  using Row = typename KT::Row;
+  const typename KT::Elem* base =
+      (const typename KT::Elem*)(const void*)k + seq.base((int)b, sk_b, sk_n) + h * sk_h + 2 * lane;
   const bool active = 2 * lane < D;
   int32_t* keep_row = keep + (seq.cu ? h * keep_sh + seq.start((int)b) : bh * N);
-  auto row_bits = [&](int r) -> uint32_t {
-    return (active && r < e) ? *(const uint32_t*)(base + (int64_t)r * sk_n) : 0u;
+  auto row_bits = [&](int r) -> Row {
+    return (active && r < e) ? *(const Row*)(base + (int64_t)r * sk_n) : Row{};
   };
 
-  const uint32_t a_bits = row_bits(s);
-  float a0 = E16<DT>::lo(a_bits), a1 = E16<DT>::hi(a_bits);
+  const Row a_bits = row_bits(s);
+  float a0 = KT::lo(a_bits), a1 = KT::hi(a_bits);
   float a_norm = 0.0f;
   if (COS) a_norm = sqrt_rn(wave_tree_sum_all(pair_dot(a0, a1, a0, a1)) + 1e-8f);
   if (lane == 0) keep_row[s] = 1;  // row s is an anchor (tritonModules.py:41)
@@ -138,7 +158,7 @@ __global__ __launch_bounds__(256) void select_kernel(
 
   // Rows s + 1 .. e - 1 in batches of 32, each loaded one batch ahead (the loads never
   // depend on the decisions); a batch's 32 decisions are stored by lanes 0..31.
-  uint32_t cur[kSelBatch], nxt[kSelBatch];
+  Row cur[kSelBatch], nxt[kSelBatch];
 #pragma unroll
   for (int j = 0; j < kSelBatch; ++j) cur[j] = row_bits(s + 1 + j);
   for (int i0 = s + 1; i0 < e; i0 += kSelBatch) {
@@ -148,11 +168,12 @@ __global__ __launch_bounds__(256) void select_kernel(
     if (i0 + kSelBatch <= e) {
 #pragma unroll
       for (int j = 0; j < kSelBatch; ++j)
-        bb |= (uint32_t)select_step<COS, A16, DT>(cur[j], a0, a1, a_norm, thr) << j;
+        bb |= (uint32_t)select_step<COS, A16, DT>(KT::lo(cur[j]), KT::hi(cur[j]), a0, a1, a_norm, thr) << j;
     } else {
 #pragma unroll
       for (int j = 0; j < kSelBatch; ++j)
-        if (i0 + j < e) bb |= (uint32_t)select_step<COS, A16, DT>(cur[j], a0, a1, a_norm, thr) << j;
+        if (i0 + j < e)
+          bb |= (uint32_t)select_step<COS, A16, DT>(KT::lo(cur[j]), KT::hi(cur[j]), a0, a1, a_norm, thr) << j;
     }
     count += __builtin_popcount(bb);  // tritonModules.py:68
     if (lane < kSelBatch && i0 + lane < e) keep_row[i0 + lane] = (int32_t)((bb >> lane) & 1u);
@@ -285,11 +306,24 @@ static int launch_select(const void* k, int dtype, int64_t B, int64_t Hkv, int64
                          int64_t sk_h, int64_t sk_n, float threshold, bool use_cosine, bool a16, int64_t chunk_size,
                          int64_t num_chunks, int32_t* keep, int32_t* chunk_counts, SeqMap seq, int64_t keep_sh,
                          int divide_to, hipStream_t st, const char* who) {
-  DA_REQUIRE(((sk_b | sk_h | sk_n) & 1) == 0 && ((uintptr_t)k & 3) == 0,
-             "%s: key rows must be 4-byte aligned (even strides)", who);
+  DA_REQUIRE(((sk_b | sk_h | sk_n) & 1) == 0 && ((uintptr_t)k & (dtype == DA_F32 ? 7 : 3)) == 0,
+             "%s: key rows must be %d-byte aligned (even strides)", who, dtype == DA_F32 ? 8 : 4);
   const int64_t total = B * Hkv * num_chunks;
   const int64_t blocks = (total + 3) / 4;
   DA_REQUIRE(blocks < (1ll << 31), "%s: too many chunks", who);
+  if (dtype == DA_F32) {
+    // fp32 keys: one wave per chunk, each lane two fp32 elements; the 16-bit definition
+    // does not apply (the keys' own arithmetic is fp32)
+    if (use_cosine)
+      hipLaunchKernelGGL((select_kernel<true, false, DA_F32>), dim3((unsigned)blocks), dim3(256), 0, st,
+                         (const uint16_t*)k, sk_b, sk_h, sk_n, (int)Hkv, N, (int)D, chunk_size, num_chunks, total,
+                         threshold, keep, chunk_counts, seq, keep_sh, divide_to);
+    else
+      hipLaunchKernelGGL((select_kernel<false, false, DA_F32>), dim3((unsigned)blocks), dim3(256), 0, st,
+                         (const uint16_t*)k, sk_b, sk_h, sk_n, (int)Hkv, N, (int)D, chunk_size, num_chunks, total,
+                         threshold, keep, chunk_counts, seq, keep_sh, divide_to);
+    return check_launch(who);
+  }
   // From two chunks per SIMD on (256 CUs x 4 SIMDs), one wave per pair of chunks walks
   // both in one instruction stream and leaves the SIMDs one wave each: 79 against 85 us
   // at 131072 keys x 8 heads.  Fewer chunks keep one wave per chunk (the pair layout
@@ -341,14 +375,12 @@ extern "C" int da_select(const void* k, int dtype, int64_t B, int64_t Hkv, int64
   DA_REQUIRE((flags & ~(DA_SELECT_COSINE | DA_SELECT_ARITH16)) == 0, "da_select: unknown flags 0x%x", flags);
   const bool use_cosine = flags & DA_SELECT_COSINE;
   const bool a16 = !use_cosine && (flags & DA_SELECT_ARITH16);
-  if (dtype != DA_BF16 && dtype != DA_F16)
-    return set_error(DA_ERR_UNSUPPORTED, "da_select: keys must be bf16 or fp16");
+  if (dtype != DA_BF16 && dtype != DA_F16 && dtype != DA_F32)
+    return set_error(DA_ERR_UNSUPPORTED, "da_select: keys must be bf16, fp16 or fp32");
   DA_REQUIRE(B > 0 && Hkv > 0 && N > 0 && D > 0, "da_select: empty shape");
   if (D > 128 || (D & 1)) return set_error(DA_ERR_UNSUPPORTED, "da_select: head_dim must be even and <= 128 (got %lld)", (long long)D);
   DA_REQUIRE(chunk_size > 0 && num_chunks > 0, "da_select: chunk_size and num_chunks must be positive");
   DA_REQUIRE(N < (1ll << 31), "da_select: sequence too long");
-  DA_REQUIRE(((sk_b | sk_h | sk_n) & 1) == 0 && ((uintptr_t)k & 3) == 0,
-             "da_select: key rows must be 4-byte aligned (even strides)");
   return launch_select(k, dtype, B, Hkv, N, D, sk_b, sk_h, sk_n, threshold, use_cosine, a16, chunk_size,
                        num_chunks, keep, chunk_counts, SeqMap{nullptr, 0, (int)N}, N, 0, (hipStream_t)stream,
                        "da_select");
@@ -363,8 +395,8 @@ extern "C" int da_select_varlen(const void* k, int dtype, int64_t B, int64_t Hkv
   DA_REQUIRE((flags & ~(DA_SELECT_COSINE | DA_SELECT_ARITH16)) == 0, "%s: unknown flags 0x%x", who, flags);
   const bool use_cosine = flags & DA_SELECT_COSINE;
   const bool a16 = !use_cosine && (flags & DA_SELECT_ARITH16);
-  if (dtype != DA_BF16 && dtype != DA_F16)
-    return set_error(DA_ERR_UNSUPPORTED, "%s: keys must be bf16 or fp16", who);
+  if (dtype != DA_BF16 && dtype != DA_F16 && dtype != DA_F32)
+    return set_error(DA_ERR_UNSUPPORTED, "%s: keys must be bf16, fp16 or fp32", who);
   DA_REQUIRE(B > 0 && Hkv > 0 && T > 0 && D > 0, "%s: empty shape", who);
   if (D > 128 || (D & 1)) return set_error(DA_ERR_UNSUPPORTED, "%s: head_dim must be even and <= 128 (got %lld)", who, (long long)D);
   DA_REQUIRE(T < (1ll << 31) && max_seqlen > 0 && max_seqlen <= T, "%s: need 0 < max_seqlen <= total tokens < 2^31", who);

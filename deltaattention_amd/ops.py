@@ -39,8 +39,8 @@ def _require_device(*ts: torch.Tensor) -> None:
                              f"(got a tensor on {t.device}); there is no CPU path")
 
 
-def _require_half(*ts: torch.Tensor) -> int:
-    """The library's code of the one 16-bit dtype (bf16 or fp16) the tensors share."""
+def _data_dtype(*ts: torch.Tensor) -> int:
+    """The library's code of the one data dtype (bf16, fp16 or fp32) the tensors share."""
     return dtype_code(*ts)
 
 
@@ -86,7 +86,7 @@ def select(k: torch.Tensor, threshold: float, chunk_size: int = 512, divide_to: 
     Returns keep [B, Hkv, N] int32 and chunk counts [B, Hkv, num_chunks] int32.
     """
     _require_device(k)
-    dt = _require_half(k)
+    dt = _data_dtype(k)
     k = _last_dim_contig(k)
     B, H, N, D = k.shape
     cs, nc = chunking(N, chunk_size, divide_to)
@@ -139,7 +139,7 @@ def pack(keep: torch.Tensor, k: torch.Tensor, v: torch.Tensor, capacity: Optiona
     anchor, so nothing waits for P on the host.
     """
     _require_device(keep, k, v)
-    dt = _require_half(k, v)
+    dt = _data_dtype(k, v)
     k, v = _last_dim_contig(k), _last_dim_contig(v)
     keep = keep.contiguous()
     if keep.dtype != torch.int32:
@@ -195,7 +195,7 @@ def hybrid_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, k_packed: 
     if variant not in DA_VARIANT:
         raise ValueError(f"variant must be one of {sorted(DA_VARIANT)}")
     _require_device(q, k, v, k_packed, v_packed, timestamps, counts)
-    dt = _require_half(q, k, v, k_packed, v_packed)
+    dt = _data_dtype(q, k, v, k_packed, v_packed)
     q, k, v = _last_dim_contig(q), _last_dim_contig(k), _last_dim_contig(v)
     k_packed, v_packed = _last_dim_contig(k_packed), _last_dim_contig(v_packed)
     timestamps = _last_dim_contig(timestamps)
@@ -229,7 +229,7 @@ def dense_prefill(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, causal: boo
                   scale: Optional[float] = None, out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Dense flash prefill (flashAttention.py:5-130) with GQA indexing."""
     _require_device(q, k, v)
-    dt = _require_half(q, k, v)
+    dt = _data_dtype(q, k, v)
     q, k, v = _last_dim_contig(q), _last_dim_contig(k), _last_dim_contig(v)
     B, Hq, Nq, D = q.shape
     Hkv, Nk = k.shape[1], k.shape[2]
@@ -318,7 +318,7 @@ def select_varlen(k: torch.Tensor, cu_seqlens, threshold: float, chunk_size: int
     -> keep [Hkv, T] int32, chunk counts [B, Hkv, max_chunks] int32.  Each sequence is
     chunked by the reference's rule on its own length (modeling_llama.py:602-610)."""
     _require_device(k)
-    dt = _require_half(k)
+    dt = _data_dtype(k)
     k = _last_dim_contig(k)
     T, H, D = k.shape
     vb = varlen_batch(cu_seqlens, T, k.device, max_seqlen)
@@ -353,7 +353,7 @@ def pack_varlen(keep: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_seqlens
     """Index + pack + counts of every sequence of a ragged batch in one pass
     (modeling_llama.py:655-685 per sequence)."""
     _require_device(keep, k, v)
-    dt = _require_half(k, v)
+    dt = _data_dtype(k, v)
     k, v = _last_dim_contig(k), _last_dim_contig(v)
     T, H, D = k.shape
     vb = varlen_batch(cu_seqlens, T, k.device, max_seqlen)
@@ -403,7 +403,7 @@ def hybrid_prefill_varlen(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, pac
         raise ValueError(f"variant must be one of {sorted(DA_VARIANT)}")
     _check_varlen(q, k, v)
     _require_device(q, k, v, packed.k_packed)
-    dt = _require_half(q, k, v, packed.k_packed, packed.v_packed)
+    dt = _data_dtype(q, k, v, packed.k_packed, packed.v_packed)
     q, k, v = _last_dim_contig(q), _last_dim_contig(k), _last_dim_contig(v)
     T, Hq, D = q.shape
     Hkv = k.shape[1]
@@ -457,7 +457,7 @@ def dense_prefill_varlen(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, cu_s
     delta_prefill_varlen)."""
     _check_varlen(q, k, v)
     _require_device(q, k, v)
-    dt = _require_half(q, k, v)
+    dt = _data_dtype(q, k, v)
     q, k, v = _last_dim_contig(q), _last_dim_contig(k), _last_dim_contig(v)
     T, Hq, D = q.shape
     Hkv = k.shape[1]

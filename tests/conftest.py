@@ -30,7 +30,7 @@ def announce(msg: str) -> None:
 
 def oracle_arith(keys) -> str:
     """The oracle's name for the product's default selection arithmetic on these keys:
-    "native" evaluates the Euclidean distance in the keys' own 16-bit type
-    (tritonModules.py:55-58), which the oracle calls "bf16" or "fp16"."""
+    "native" evaluates the Euclidean distance in the keys' own type (tritonModules.py:
+    55-58), which the oracle calls "bf16", "fp16" or (fp32 keys) "fp32"."""
     import torch
-    return "fp16" if keys.dtype == torch.float16 else "bf16"
+    return {torch.float16: "fp16", torch.float32: "fp32"}.get(keys.dtype, "bf16")

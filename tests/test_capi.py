@@ -46,7 +46,11 @@ def test_select_rejects_null_and_dtype():
     assert lib.da_select(None, 1, 1, 1, 8, 128, 0, 0, 0, f, 0, 8, 1, None, None, None) == -1
     assert "null" in _err()
     fake = ctypes.c_void_p(1 << 20)
-    assert lib.da_select(fake, 4, 1, 1, 8, 128, 0, 0, 128, f, 0, 8, 1, fake, fake, None) == -2
+    # keys are bf16, fp16 or fp32: int32 (DA_I32 = 3) is refused
+    assert lib.da_select(fake, 3, 1, 1, 8, 128, 0, 0, 128, f, 0, 8, 1, fake, fake, None) == -2
+    assert "bf16, fp16 or fp32" in _err()
+    # fp32 rows are read 8 bytes per lane: odd strides are refused
+    assert lib.da_select(fake, 4, 1, 1, 8, 128, 0, 0, 129, f, 0, 8, 1, fake, fake, None) == -1
     assert lib.da_select(fake, 1, 1, 1, 8, 130, 0, 0, 130, f, 0, 8, 1, fake, fake, None) == -2
     assert "head_dim" in _err()
     assert lib.da_select(fake, 1, 1, 1, 8, 128, 0, 0, 129, f, 0, 8, 1, fake, fake, None) == -1
@@ -133,10 +137,13 @@ def test_decode_shape_limits():
     f = ctypes.c_float(0.1)
     cap, W = 64, 16
 
-    def call(Hq, Hkv, D, ws=None, ws_bytes=0):
+    def call(Hq, Hkv, D, ws=None, ws_bytes=0, dtype=1):
         st_p, st_x = (Hkv * cap * D, cap * D, D), (Hkv * W * D, W * D, D)
-        return lib.da_decode_attention(a, 1, 1, Hq, Hkv, D, Hq * D, D, a, a, *st_p, a, Hkv * cap, cap, a, cap,
-                                       a, a, *st_x, W, 0, f, a, Hq * D, D, ws, ws_bytes, None)
+        return lib.da_decode_attention(a, dtype, 1, Hq, Hkv, D, Hq * D, D, a, a, *st_p, a, Hkv * cap, cap, a,
+                                       cap, a, a, *st_x, W, 0, f, a, Hq * D, D, ws, ws_bytes, None)
+
+    # the decode cache is 16-bit: fp32 (DA_F32 = 4) is refused as unsupported
+    assert call(8, 8, 64, dtype=4) == -2 and "bf16 or fp16" in _err()
 
     for D in (4, 100, 136):
         assert call(8, 8, D) == -2 and "head_dim" in _err(), D

@@ -142,6 +142,82 @@ def test_config0_dense_head_dim_64(gpu):
     _close(out.float().cpu().numpy(), want, "config0 dense D=64")
 
 
+# fp32 tensors: the oracle's fp32 arithmetic without 16-bit rounding of p; the two
+# differ only by fp32 summation order and the key-bias formulation of the weights
+FP32_MAX_ABS = 1e-4
+FP32_MEAN_ABS = 1e-5
+
+
+def _close32(got, want, what):
+    got = np.asarray(got, dtype=np.float32)
+    err = np.abs(got - np.asarray(want, dtype=np.float32))
+    mx, mean = float(err.max()), float(err.mean())
+    print(f"{what}: max-abs {mx:.3e} mean-abs {mean:.3e}", flush=True)
+    assert np.isfinite(got).all(), f"{what}: non-finite output"
+    assert mx <= FP32_MAX_ABS and mean <= FP32_MEAN_ABS, f"{what}: max-abs {mx:.3e}, mean-abs {mean:.3e}"
+
+
+@pytest.mark.parametrize("variant", ["hybrid", "sanity", "pure_phase1", "dense"])
+def test_config0_fp32(gpu, variant):
+    """Config 0 as BASELINE.json states it, fp32 end to end: fp32 Q, K, V (no 16-bit
+    rounding of the inputs), the selection in fp32 (the keys' own arithmetic) bit-exact,
+    packing bit-exact, and attention within 1e-4 of the fp32 oracle."""
+    from deltaattention_amd import ops, synth
+    N, D = 2048, 64
+    q, k, v = synth.make_layer_inputs(1, 8, 8, N, D, rope_base=10000.0, seed=0, dtype=torch.float32,
+                                      device=gpu, qv_on_device=True)
+    qf, kf, vf = q.cpu().numpy(), k.cpu().numpy(), v.cpu().numpy()
+    if variant == "dense":
+        announce("config0 fp32 dense")
+        _close32(ops.dense_prefill(q, k, v).cpu().numpy(), O.dense_attention(qf, kf, vf, True), "config0 fp32 dense")
+        return
+    tau, r_real = synth.calibrate_threshold(k, 4.0)
+    announce(f"config0 fp32 {variant} tau={tau:.4f} r={r_real:.3f}")
+    out, packed = ops.delta_prefill(q, k, v, tau, 512, window=128, variant=variant, return_packed=True)
+    keep, _ = ops.select(k, tau, 512)
+    _, _, ref = _check_select_pack(k, v, tau, keep, packed, "config0 fp32")
+    want = O.hybrid_attention(qf, kf, vf, ref["k_packed"], ref["v_packed"], ref["timestamps"], ref["counts"], 128,
+                              variant=variant)
+    _close32(out.cpu().numpy(), want, f"config0 fp32 {variant}")
+
+
+def test_fp32_ragged_batch_and_dims(gpu):
+    """fp32 through the varlen entry points (each sequence equal to its own B = 1 run),
+    and at head dims 96 and 128 with GQA, against the fp32 oracle."""
+    from deltaattention_amd import ops, synth
+    for D, Hq, Hkv in ((96, 8, 2), (128, 8, 4)):
+        q, k, v = synth.make_layer_inputs(1, Hq, Hkv, 1500, D, rope_base=10000.0, seed=D, dtype=torch.float32,
+                                          device=gpu, qv_on_device=True)
+        tau = 8.0 * (D / 128) ** 0.5
+        announce(f"fp32 D={D} Hq={Hq} Hkv={Hkv}")
+        out, packed = ops.delta_prefill(q, k, v, tau, 512, window=128, return_packed=True)
+        kf, vf = k.cpu().numpy(), v.cpu().numpy()
+        keep, _ = OC.select_delta(kf, tau, 512, arith="fp32")
+        p = O.pack(kf, vf, keep)
+        P = int(packed.num_packed.item())
+        assert P == p["P"] and np.array_equal(packed.k_packed[:, :, :P].cpu().numpy(), p["k_packed"])
+        want = O.hybrid_attention(q.cpu().numpy(), kf, vf, p["k_packed"], p["v_packed"], p["timestamps"],
+                                  p["counts"], 128)
+        _close32(out.cpu().numpy(), want, f"fp32 D={D} hybrid")
+    # a ragged batch: [T, H, D] tensors, every sequence bitwise equal to its B = 1 run
+    lens = [700, 1300, 64]
+    cu = [0]
+    for n in lens:
+        cu.append(cu[-1] + n)
+    qs, ks, vs = [], [], []
+    for i, n in enumerate(lens):
+        q, k, v = synth.make_layer_inputs(1, 8, 2, n, 64, rope_base=10000.0, seed=50 + i, dtype=torch.float32,
+                                          device=gpu, qv_on_device=True)
+        qs.append(q); ks.append(k); vs.append(v)
+    tok = lambda ts: torch.cat([t[0].transpose(0, 1) for t in ts]).contiguous()  # [T, H, D]
+    announce(f"fp32 varlen lens {lens}")
+    out = ops.delta_prefill_varlen(tok(qs), tok(ks), tok(vs), torch.tensor(cu, dtype=torch.int32, device=gpu),
+                                   6.0, 512)
+    for i, n in enumerate(lens):
+        one = ops.delta_prefill(qs[i], ks[i], vs[i], 6.0, 512)
+        assert torch.equal(out[cu[i]:cu[i + 1]].transpose(0, 1), one[0]), f"sequence {i}"
+
+
 @pytest.mark.parametrize("D", [32, 80, 96])
 def test_other_head_dims(gpu, D):
     """Head dims below 128 (multiples of 8) on the GQA-4 grouped kernel and the per-head

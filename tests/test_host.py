@@ -81,14 +81,18 @@ def test_llama_swap_routes_attention_to_this_build():
                 model(torch.zeros(1, 8, dtype=torch.long), use_cache=False)
 
 
-def test_dtype_code_accepts_one_16bit_type():
+def test_dtype_code_accepts_one_data_type():
     import torch
-    from deltaattention_amd._native import DA_BF16, DA_F16, dtype_code
+    from deltaattention_amd._native import DA_BF16, DA_F16, DA_F32, dtype_code
     a = torch.zeros(2, dtype=torch.bfloat16)
     h = torch.zeros(2, dtype=torch.float16)
+    f = torch.zeros(2, dtype=torch.float32)
     assert dtype_code(a, a, None) == DA_BF16
     assert dtype_code(h, h) == DA_F16
+    assert dtype_code(f, f) == DA_F32
     with pytest.raises(TypeError):
         dtype_code(a, h)
     with pytest.raises(TypeError):
-        dtype_code(torch.zeros(2, dtype=torch.float32))
+        dtype_code(f, a)
+    with pytest.raises(TypeError):
+        dtype_code(torch.zeros(2, dtype=torch.float64))
