@@ -52,14 +52,14 @@ int da_version(void);
  * Delta-mode anchor selection.  Replaces chunked_eval_kernel
  * (tritonModules.py:7-69) and its launch (modeling_llama.py:634-653).
  *
- * k: [B, Hkv, N, D] bf16 or fp16 (dtype DA_BF16 / DA_F16), strides (sk_b, sk_h, sk_n),
- * D even and <= 128.
+ * k: [B, Hkv, N, D] bf16, fp16 or fp32 (dtype DA_BF16 / DA_F16 / DA_F32), strides
+ * (sk_b, sk_h, sk_n), D even and <= 128; fp32 rows 8-byte aligned.
  * threshold: tau^2 for Euclidean, tau for cosine (modeling_llama.py:641-642).
  * flags: DA_SELECT_COSINE selects the cosine test (keep iff cos < tau, else Euclidean
  *   keep iff dist^2 > tau^2); DA_SELECT_ARITH16 evaluates the Euclidean distance in the
  *   keys' 16-bit arithmetic (every difference, square and tree addition rounded to
  *   bf16 / fp16, as the reference's Triton code does on 16-bit keys,
- *   tritonModules.py:55-58); without it the distance is fp32.
+ *   tritonModules.py:55-58); without it, and always for fp32 keys, the distance is fp32.
  * chunk_size / num_chunks: from the chunking rule of modeling_llama.py:602-610.
  * keep: [B, Hkv, N] int32 contiguous, 1 for anchors and 0 otherwise (rows of
  *   chunks that start at or beyond N are not written).
@@ -82,7 +82,8 @@ int da_select(const void* k, int dtype, int64_t B, int64_t Hkv, int64_t N, int64
  *
  * keep: [B, Hkv, N] int32 contiguous; keep[..., 0] must be 1 (every mode of the
  *   reference guarantees it, modeling_llama.py:623/630 and tritonModules.py:41).
- * k, v: [B, Hkv, N, D] bf16 or fp16 (dtype) with strides (s*_b, s*_h, s*_n).
+ * k, v: [B, Hkv, N, D] bf16, fp16 or fp32 (dtype) with strides (s*_b, s*_h, s*_n); the
+ *   packed rows are copies of theirs, in the same type.
  * capacity: rows allocated per head in the packed outputs; must be >= P
  *   (N always suffices).
  * k_packed, v_packed: [B, Hkv, capacity, D] contiguous; rows [0, c) receive the
@@ -107,8 +108,9 @@ int da_pack(const int32_t* keep, const void* k, const void* v, int dtype, int64_
  * h / (Hq / Hkv) directly.
  *
  * q, out: [B, Hq, Nq, D]; k, v: [B, Hkv, Nk, D]; k_packed, v_packed: [B, Hkv, >=P, D], all
- * of one 16-bit type (dtype DA_BF16 or DA_F16; P is rounded to it before P.V, as
- * deltaFlashAttention.py:98, 137 round p to V's type); timestamps: [B, Hkv, >=P] int32;
+ * of one type (dtype DA_BF16, DA_F16 or DA_F32; P is rounded to it before P.V, as
+ * deltaFlashAttention.py:98, 137 round p to V's type: fp32 tensors run an fp32 kernel
+ * with p in fp32); timestamps: [B, Hkv, >=P] int32;
  * counts: [B, Hkv, >=P] int32 or fp32 (counts_dtype DA_I32 / DA_F32).
  * num_packed: P (rows of the packed tensors that are read); if num_packed_dev
  *   is non-null the device value is used instead (it must be <= num_packed).
