@@ -10,9 +10,10 @@ modeling_llama.py:612-754).
 
 The default run measures config 1 (N = 32768, r = 4) as the headline and adds to the same
 JSON line: config 2 (N = 131072) at r = 2, 4 and 8, the same layer at N = 262144 and r = 4
-(the reference's longest point, key ``n262144_r4``), the config-4 ragged batch, the
-config-3 end-to-end 32-layer prefill, the selection in both arithmetic definitions, the
-on-box MFMA and copy ceilings, and the CPU baseline (config 1 and config 0 in full).
+(the reference's longest point, key ``n262144_r4``), config 0 in fp32 (``config0_fp32``),
+the config-4 ragged batch, the config-3 end-to-end 32-layer prefill, the selection in both
+arithmetic definitions, the on-box MFMA and copy ceilings, and the CPU baseline (config 1
+and config 0 in full).
 ``--config 2`` runs N = 131072 alone with ``--ratio`` in {2, 4, 8}.  The threshold tau is
 calibrated on the seeded keys so that the realised compression is r (smallest tau with
 keep rate <= 1/r), in the selection arithmetic that is timed.
@@ -480,6 +481,30 @@ def run_config4(args):
     print(json.dumps(config4_record(args, args.warmup, args.steps)), flush=True)
 
 
+def config0_record(args):
+    """Config 0 as BASELINE.json states it, on the GPU: B=1, 8 query and 8 KV heads,
+    head_dim 64, N=2048, fp32 tensors (fp32 selection, packing and attention), RoPE base
+    1e4, tau calibrated to r = 4 by the GPU selection; the same inputs as the CPU
+    baseline's config-0 leg.  HIP-event time of the whole delta step and of the dense
+    prefill, 20 warm-up and 50 timed calls each."""
+    import torch
+    from deltaattention_amd import ops, synth
+    dev = torch.device("cuda:0")
+    q, k, v = (t.to(dev) for t in synth.make_layer_inputs(1, 8, 8, 2048, 64, rope_base=10000.0, seed=0,
+                                                           dtype=torch.float32))
+    tau, r_real = synth.calibrate_threshold(k, 4.0)
+    step = lambda: ops.delta_prefill(q, k, v, tau, 512, window=args.window)
+    dense = lambda: ops.dense_prefill(q, k, v)
+    for _ in range(20):
+        step(), dense()
+    ms_step, ms_dense = time_loop(step, 50), time_loop(dense, 50)
+    log(f"config 0 (fp32): delta {ms_step:.3f} ms, dense {ms_dense:.3f} ms")
+    return {"delta_ms": round(ms_step, 4), "dense_ms": round(ms_dense, 4),
+            "speedup_vs_dense": round(ms_dense / ms_step, 3), "tau": round(tau, 4),
+            "realised_ratio": round(r_real, 3),
+            "workload": "config0: B=1 Hq=Hkv=8 D=64 N=2048 fp32 r=4, RoPE 1e4 (fp32 selection and attention)"}
+
+
 def measure_peaks():
     """On-box ceilings for the roofline fractions, each the best of 5 timed launches after a
     warm-up:
@@ -610,6 +635,8 @@ def main():
             "attention_ms_delta", "attention_share_delta", "attention_ms_dense", "attention_share_dense",
             "attention_speedup_vs_dense", "steps", "warmup")}
         rec["config3"]["workload"] = c3["config"]["workload"] + f", anchors {args.e2e_mode} r={args.ratio:g}"
+        torch.cuda.empty_cache()
+        rec["config0_fp32"] = config0_record(args)
         torch.cuda.empty_cache()
     if full:
         rec["peaks_measured"] = measure_peaks()
