@@ -148,10 +148,12 @@ __device__ __forceinline__ float wave_sum_all(float v) {
 // scores are done and arrive during the softmax.  Lane t scores key j0 + t for every
 // query head of the sub-group (q broadcast from LDS); the slice max and sum are wave
 // reductions; for P.V lane l owns dims 2l and 2l + 1.  Outputs past the head dimension
-// are not stored.
+// are not stored.  FULL (D = 128) loads each key row at immediate offsets from one base;
+// the clamped chunk addresses of the general form cost 12% of the attention's time at
+// D = 128 (22.5 against 20.0 us per call after the config-1 prefill).
 // Small slices keep many waves in flight per CU: the kernel is latency-bound at decode
 // sizes, and holding K and V rows at once would halve the waves per SIMD.
-template <int G, int DT>
+template <int G, int DT, bool FULL>
 __global__ __launch_bounds__(64) void decode_attn_kernel(DecodeAttnArgs a) {
   __shared__ float s_q[G][kDecD];
   __shared__ float s_p[G][kDecSlice];
@@ -159,12 +161,12 @@ __global__ __launch_bounds__(64) void decode_attn_kernel(DecodeAttnArgs a) {
   const int bg = blockIdx.x, slice = blockIdx.y;
   const int hh0 = blockIdx.z * G;  // first query head of the sub-group
   auto head = [&](int hh) { return min(hh0 + hh, a.G - 1); };
-  const int D = a.D;
+  const int D = FULL ? kDecD : a.D;
   // Loads stay unconditional: key chunks past the head dimension repeat its last chunk
   // and meet zero query elements, value lanes past it read its last pair and their
   // partials are never stored
   const int dlast8 = D / 8 - 1;
-  const int vdim = min(2 * lane, D - 2);
+  const int vdim = FULL ? 2 * lane : min(2 * lane, D - 2);
   const int b = bg / a.Hkv, g = bg - (bg / a.Hkv) * a.Hkv;
   int plen = a.lengths[bg];
   plen = plen < 0 ? 0 : (plen > a.capacity ? (int)a.capacity : plen);
@@ -182,7 +184,7 @@ __global__ __launch_bounds__(64) void decode_attn_kernel(DecodeAttnArgs a) {
     const uint16_t* krow = j < plen ? a.kp + b * a.sp_b + g * a.sp_h + (int64_t)j * a.sp_s
                                     : a.kx + b * a.sx_b + g * a.sx_h + (int64_t)(j - plen) * a.sx_s;
 #pragma unroll
-    for (int c8 = 0; c8 < kDecD / 8; ++c8) kw[c8] = *(const u32x4*)(krow + 8 * min(c8, dlast8));
+    for (int c8 = 0; c8 < kDecD / 8; ++c8) kw[c8] = *(const u32x4*)(krow + 8 * (FULL ? c8 : min(c8, dlast8)));
     if (j < plen) cnt = a.counts[b * a.sc_b + g * a.sc_h + j];
   }
   constexpr int kQPerLane = G * kDecD / 64;
@@ -190,7 +192,7 @@ __global__ __launch_bounds__(64) void decode_attn_kernel(DecodeAttnArgs a) {
 #pragma unroll
   for (int it = 0; it < kQPerLane; ++it) {
     const int i = lane + 64 * it, hh = i / kDecD, d = i - hh * kDecD;
-    qh[it] = d < D ? a.q[b * a.sq_b + (int64_t)(g * a.G + head(hh)) * a.sq_h + d] : (uint16_t)0;
+    qh[it] = FULL || d < D ? a.q[b * a.sq_b + (int64_t)(g * a.G + head(hh)) * a.sq_h + d] : (uint16_t)0;
   }
 #pragma unroll
   for (int it = 0; it < kQPerLane; ++it) {
@@ -425,26 +427,30 @@ extern "C" int da_decode_update(const void* new_k, const void* new_v, int dtype,
                             "da_decode_update");
 }
 
-template <int DT>
-static int launch_decode(DecodeAttnArgs& a, int64_t n_heads, hipStream_t st) {
+template <int DT, bool FULL>
+static int launch_decode_g(DecodeAttnArgs& a, int64_t n_heads, hipStream_t st) {
   // a group above kDecMaxG query heads is split into ceil(G / kDecMaxG) sub-groups of
   // equal size (the last one smaller when G does not divide), one wave each
   const int nsub = (a.G + kDecMaxG - 1) / kDecMaxG;
   const int gw = (a.G + nsub - 1) / nsub;
   const dim3 agrid((unsigned)(a.B * a.Hkv), (unsigned)a.nslice, (unsigned)nsub);
   switch (gw) {
-    case 1: hipLaunchKernelGGL((decode_attn_kernel<1, DT>), agrid, dim3(64), 0, st, a); break;
-    case 2: hipLaunchKernelGGL((decode_attn_kernel<2, DT>), agrid, dim3(64), 0, st, a); break;
-    case 3: hipLaunchKernelGGL((decode_attn_kernel<3, DT>), agrid, dim3(64), 0, st, a); break;
-    case 4: hipLaunchKernelGGL((decode_attn_kernel<4, DT>), agrid, dim3(64), 0, st, a); break;
-    case 5: hipLaunchKernelGGL((decode_attn_kernel<5, DT>), agrid, dim3(64), 0, st, a); break;
-    case 6: hipLaunchKernelGGL((decode_attn_kernel<6, DT>), agrid, dim3(64), 0, st, a); break;
-    case 7: hipLaunchKernelGGL((decode_attn_kernel<7, DT>), agrid, dim3(64), 0, st, a); break;
-    default: hipLaunchKernelGGL((decode_attn_kernel<8, DT>), agrid, dim3(64), 0, st, a); break;
+    case 1: hipLaunchKernelGGL((decode_attn_kernel<1, DT, FULL>), agrid, dim3(64), 0, st, a); break;
+    case 2: hipLaunchKernelGGL((decode_attn_kernel<2, DT, FULL>), agrid, dim3(64), 0, st, a); break;
+    case 3: hipLaunchKernelGGL((decode_attn_kernel<3, DT, FULL>), agrid, dim3(64), 0, st, a); break;
+    case 4: hipLaunchKernelGGL((decode_attn_kernel<4, DT, FULL>), agrid, dim3(64), 0, st, a); break;
+    case 5: hipLaunchKernelGGL((decode_attn_kernel<5, DT, FULL>), agrid, dim3(64), 0, st, a); break;
+    case 6: hipLaunchKernelGGL((decode_attn_kernel<6, DT, FULL>), agrid, dim3(64), 0, st, a); break;
+    case 7: hipLaunchKernelGGL((decode_attn_kernel<7, DT, FULL>), agrid, dim3(64), 0, st, a); break;
+    default: hipLaunchKernelGGL((decode_attn_kernel<8, DT, FULL>), agrid, dim3(64), 0, st, a); break;
   }
   if (int rc = check_launch("da_decode_attention")) return rc;
   hipLaunchKernelGGL((decode_combine_kernel<DT>), dim3((unsigned)n_heads, kCombParts), dim3(256), 0, st, a);
   return check_launch("da_decode_attention(combine)");
+}
+template <int DT>
+static int launch_decode(DecodeAttnArgs& a, int64_t n_heads, hipStream_t st) {
+  return a.D == kDecD ? launch_decode_g<DT, true>(a, n_heads, st) : launch_decode_g<DT, false>(a, n_heads, st);
 }
 
 extern "C" int64_t da_decode_workspace_size(int64_t B, int64_t Hq, int64_t capacity, int64_t window) {
@@ -560,10 +566,20 @@ static std::mutex g_scratch_mu;
 static void* g_scratch_ptr[kMaxScratchDevices] = {};
 
 // Device address of `scratch` on the current device (looked up once per device).
-static int scratch_for_current_device(void** ptr, const char* who) {
+static int scratch_for_current_device(void** ptr, hipStream_t stream, const char* who) {
   int dev = -1;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return set_error(DA_ERR_HIP, "%s: hipGetDevice: %s", who, hipGetErrorString(e));
+  if (stream) {
+    // the scratch array is per device: a stream of another device would get this
+    // device's copy, so the stream's device must be the current one
+    hipDevice_t sdev = -1;
+    e = hipStreamGetDevice(stream, &sdev);
+    if (e != hipSuccess) return set_error(DA_ERR_HIP, "%s: hipStreamGetDevice: %s", who, hipGetErrorString(e));
+    if ((int)sdev != dev)
+      return set_error(DA_ERR_INVALID, "%s: the stream belongs to device %d but device %d is current", who,
+                       (int)sdev, dev);
+  }
   if (dev < 0 || dev >= kMaxScratchDevices)
     return set_error(DA_ERR_UNSUPPORTED, "%s: device index %d above %d", who, dev, kMaxScratchDevices - 1);
   std::lock_guard<std::mutex> lock(g_scratch_mu);
@@ -599,7 +615,7 @@ extern "C" int da_decode_attention_noalloc(const void* q, int dtype, int64_t B, 
                      "(B * Hq * ceil((capacity + window) / 64) * 520 bytes); use da_decode_attention",
                      who, (long long)need, (long long)DA_DECODE_SCRATCH_BYTES);
   void* part = nullptr;
-  if (int rc = scratch_for_current_device(&part, who)) return rc;
+  if (int rc = scratch_for_current_device(&part, (hipStream_t)stream, who)) return rc;
   return decode_attention_impl(q, dtype, B, Hq, Hkv, D, sq_b, sq_h, k_packed, v_packed, sp_b, sp_h, sp_s, counts,
                                sc_b, sc_h, lengths, capacity, k_exact, v_exact, sx_b, sx_h, sx_s, window,
                                exact_len, scale, out, so_b, so_h, (float*)part, (hipStream_t)stream);

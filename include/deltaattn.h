@@ -298,7 +298,8 @@ int da_decode_step(const DaDecodeStep* step, void* stream);
  * live in a static device array of DA_DECODE_SCRATCH_BYTES per GPU (held until the
  * process ends), so da_decode_workspace_size(B, Hq, capacity, window) must not exceed
  * DA_DECODE_SCRATCH_BYTES (DA_ERR_UNSUPPORTED otherwise; e.g. B = 1, Hq = 32 allows
- * capacity + window up to 129024 keys).  The stream must belong to the current device.
+ * capacity + window up to 129024 keys).  The stream must belong to the current device
+ * (checked: DA_ERR_INVALID otherwise; the null stream is the current device's).
  * Every call on one GPU shares that GPU's array: calls that overlap on one GPU (on
  * streams not ordered with each other) race.
  */

@@ -9,8 +9,8 @@ Every configuration runs the HIP path at its real shape and sizes:
   hybrid and dense outputs on query blocks spread from the first to the last;
 * config 2: the same layer at N = 131072 for r in {2, 4, 8}, and at N = 262144 for r = 4
   (the reference's longest point);
-* config 3: a Llama-3-8B-shaped model (2 layers) prefilling 65536 tokens through the
-  transformers swap with periodic anchors (r = 4); layer 0's attention is compared;
+* config 3: a Llama-3-8B-shaped model (4 layers) prefilling 65536 tokens through the
+  transformers swap with periodic anchors (r = 4); every layer's attention is compared;
 * config 4: a ragged batch of 8 sequences of 4096..32768 tokens with rho ~ U[0.6, 0.95]
   per (sequence, KV head), each sequence compared as a B = 1 prefill.
 
@@ -282,44 +282,50 @@ def test_layer_262k(gpu):
 # --------------------------------------------------------------------------------------
 # config 3: Llama-3-8B-shaped prefill of 65536 tokens through the transformers swap
 # --------------------------------------------------------------------------------------
-def test_config3_model_layer(gpu, monkeypatch):
+def test_config3_model_layers(gpu, monkeypatch):
+    """A 4-layer Llama-3-8B-shaped model prefills 65536 tokens through the swap (periodic
+    anchors, r = 4); every layer's attention output is compared with the oracle on its own
+    inputs (the layer's post-RoPE q, k, v as the swap passed them)."""
     pytest.importorskip("transformers")
     from deltaattention_amd import attention, globVR, llama_swap
-    N = 65536
+    N, L = 65536, 4
     captured = {}
     real = attention.delta_prefill_attention
 
     def spy(query_states, key_states, value_states, layer_idx=0, **kw):
         out = real(query_states, key_states, value_states, layer_idx=layer_idx, **kw)
-        if layer_idx == 0 and "q" not in captured:
-            captured.update(q=query_states.detach().clone(), k=key_states.detach().clone(),
-                            v=value_states.detach().clone(), out=out.detach().clone())
+        if layer_idx not in captured:
+            captured[layer_idx] = (query_states.detach().clone(), key_states.detach().clone(),
+                                   value_states.detach().clone(), out.detach().clone())
         return out
 
     monkeypatch.setattr(attention, "delta_prefill_attention", spy)
     monkeypatch.setattr(globVR, "packing_mode", "periodic", raising=False)
     monkeypatch.setattr(globVR, "target_keep_rate", 0.25, raising=False)
     monkeypatch.setattr(globVR, "dense_window_size", 128, raising=False)
-    cfg = llama_swap.llama3_8b_config(llama_swap.DELTA, num_layers=2)
+    cfg = llama_swap.llama3_8b_config(llama_swap.DELTA, num_layers=L)
     model = llama_swap.random_llama(cfg, gpu, seed=0)
     ids = torch.randint(0, cfg.vocab_size, (1, N), generator=torch.Generator().manual_seed(0)).to(gpu)
-    announce(f"config3 2-layer Llama-3-8B shape, N={N}, periodic r=4")
+    announce(f"config3 {L}-layer Llama-3-8B shape, N={N}, periodic r=4")
     with torch.no_grad():
         hidden = model.model(input_ids=ids).last_hidden_state
     torch.cuda.synchronize()
     assert torch.isfinite(hidden).all()
-    q, k, v, out = captured["q"], captured["k"], captured["v"], captured["out"]
-    assert q.shape == (1, 32, N, 128) and k.shape == (1, 8, N, 128)
     del model, hidden
     torch.cuda.empty_cache()
-    kf, vf = k.float().cpu().numpy(), v.float().cpu().numpy()
+    assert sorted(captured) == list(range(L))
     keep = O.select_periodic(1, 8, N, 0.25)
-    ref = O.pack(kf, vf, keep)
     blocks = _spread(N // 128, 6)
     rows = _rows(blocks, N)
-    want = O.hybrid_attention(q.float().cpu().numpy(), kf, vf, ref["k_packed"], ref["v_packed"],
-                              ref["timestamps"], ref["counts"], 128, q_blocks=blocks)
-    _close(out[:, :, rows].float().cpu().numpy(), want[:, :, rows], f"config3 layer0 blocks {blocks}")
+    for layer in range(L):
+        q, k, v, out = captured.pop(layer)
+        assert q.shape == (1, 32, N, 128) and k.shape == (1, 8, N, 128)
+        kf, vf = k.float().cpu().numpy(), v.float().cpu().numpy()
+        ref = O.pack(kf, vf, keep)
+        want = O.hybrid_attention(q.float().cpu().numpy(), kf, vf, ref["k_packed"], ref["v_packed"],
+                                  ref["timestamps"], ref["counts"], 128, q_blocks=blocks)
+        _close(out[:, :, rows].float().cpu().numpy(), want[:, :, rows], f"config3 layer {layer} blocks {blocks}")
+        del q, k, v, out, kf, vf, ref, want
 
 
 # --------------------------------------------------------------------------------------
