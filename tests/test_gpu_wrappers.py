@@ -62,3 +62,34 @@ def test_reference_wrappers(gpu, layer, monkeypatch, variant, expanded, no_count
     print(f"{variant} expanded={expanded} no_count={no_count}: max-abs {err.max():.3e} "
           f"mean-abs {err.mean():.3e}", flush=True)
     assert err.max() <= MAX_ABS and err.mean() <= MEAN_ABS
+
+
+@pytest.mark.parametrize("variant", ["hybrid", "sanity", "pure_phase1", "dense"])
+def test_reference_wrappers_fp32(gpu, variant):
+    """The same wrappers and the dense drop-in (flashAttention.triton_flash_attention,
+    flashAttention.py:94-130) on fp32 tensors, which the reference's kernels take as they
+    take 16-bit ones: the selection runs in fp32, the output is fp32, within 1e-5 of the
+    fp32 oracle."""
+    from deltaattention_amd import attention, flashAttention, ops, synth
+    q, k, v = synth.make_layer_inputs(1, 8, 2, 1536, 128, seed=37, rope_base=10000.0, dtype=torch.float32)
+    qg, kg, vg = q.to(gpu), k.to(gpu), v.to(gpu)
+    qf, kf, vf = q.numpy(), k.numpy(), v.numpy()
+    announce(f"fp32 wrapper {variant}")
+    if variant == "dense":
+        out = flashAttention.triton_flash_attention(qg, _repeat_kv(kg, 4), _repeat_kv(vg, 4))
+        want = O.dense_attention(qf, kf, vf, True)
+    else:
+        keep, _ = ops.select(kg, 10.0, 512)
+        p = ops.pack(keep, kg, vg).trimmed()
+        okeep, _ = OC.select_delta(kf, 10.0, 512, arith="fp32")
+        ref = O.pack(kf, vf, okeep)
+        assert np.array_equal(keep.cpu().numpy(), okeep) and p.k_packed.shape[2] == ref["P"]
+        fn = {"hybrid": attention.forward_hybrid_flash, "sanity": attention.forward_hybrid_flash_sanity,
+              "pure_phase1": attention.forward_pure_phase1}[variant]
+        out = fn(qg, kg, vg, p.k_packed, p.v_packed, p.timestamps, p.counts, 128)
+        want = O.hybrid_attention(qf, kf, vf, ref["k_packed"], ref["v_packed"], ref["timestamps"], ref["counts"],
+                                  128, variant=variant)
+    assert out.dtype == torch.float32 and out.shape == qg.shape
+    err = np.abs(out.cpu().numpy() - want)
+    print(f"fp32 {variant}: max-abs {err.max():.3e} mean-abs {err.mean():.3e}", flush=True)
+    assert err.max() <= 1e-5 and err.mean() <= 1e-6
