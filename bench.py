@@ -623,7 +623,7 @@ def main():
         del q, k, v
         torch.cuda.empty_cache()
     if full and not args.no_e2e:
-        c4 = config4_record(args, warmup=3, steps=10)
+        c4 = config4_record(args, warmup=20, steps=10)
         rec["config4"] = {key: c4[key] for key in (
             "delta_ms_per_batch", "dense_ms_per_batch", "speedup_vs_dense", "value", "unit",
             "dense_tokens_per_s", "realised_ratio", "steps", "warmup")}
