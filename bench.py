@@ -348,11 +348,16 @@ def run_decode(args):
 
     ms_two = timed(step, T)
     ms_delta = timed(fused_step, T)
-    # the one-call step leaves the same cache and the same last output as the two calls
-    if not (torch.equal(last["one"], last["two"])
+    # the one-call step leaves the same cache as the two calls, and the same last output up
+    # to rounding (its key list holds the evicted token after the ring, not before it)
+    step_err = float((last["one"].float() - last["two"].float()).abs().max())
+    if not (step_err <= 1e-2
             and torch.equal(fused.packed_lengths, cache.packed_lengths)
-            and torch.equal(fused.k_packed, cache.k_packed)):
-        raise RuntimeError("decode_step differs from update + decode_attention")
+            and torch.equal(fused.packed_counts, cache.packed_counts)
+            and torch.equal(fused.k_packed, cache.k_packed)
+            and torch.equal(fused.v_packed, cache.v_packed)
+            and torch.equal(fused.k_exact, cache.k_exact)):
+        raise RuntimeError(f"decode_step differs from update + decode_attention (max-abs {step_err:.3e})")
     ms_attn = timed(lambda i: dd.decode_attention(q_tok[i], cache, 0), T)
     ms_dense = timed(lambda i: dd.decode_attention(q_tok[i], dense, 0), T)
 

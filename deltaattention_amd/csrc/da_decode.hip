@@ -44,6 +44,25 @@ struct DecodeUpdateArgs {
   float thr;
 };
 
+// The update's test (deltaDecoding.py:61-77): does the evicted token (this lane's 4-byte
+// word ek, dims 2l and 2l + 1) merge into the last packed anchor (word lk)?  Euclidean
+// dist^2 <= thr or cosine >= thr, with the selection's fixed fp32 tree; the same result
+// in every lane.
+template <bool COS, int DT>
+__device__ __forceinline__ bool evict_merges(uint32_t ek, uint32_t lk, float thr) {
+#pragma clang fp contract(off)
+  const float e0 = E16<DT>::lo(ek), e1 = E16<DT>::hi(ek), l0 = E16<DT>::lo(lk), l1 = E16<DT>::hi(lk);
+  if (COS) {
+    const float eps = 1e-8f;
+    const float dot = wave_tree_sum(pair_dot(e0, e1, l0, l1));
+    const float ne = sqrt_rn(wave_tree_sum(pair_dot(e0, e1, e0, e1)) + eps);
+    const float nl = sqrt_rn(wave_tree_sum(pair_dot(l0, l1, l0, l1)) + eps);
+    return __fdiv_rn(dot, ne * nl) >= thr;
+  }
+  const float d0 = e0 - l0, d1 = e1 - l1;
+  return wave_tree_sum(pair_dot(d0, d1, d0, d1)) <= thr;
+}
+
 template <bool COS, int DT>
 __global__ __launch_bounds__(256) void decode_update_kernel(DecodeUpdateArgs a) {
 #pragma clang fp contract(off)
@@ -66,17 +85,7 @@ __global__ __launch_bounds__(256) void decode_update_kernel(DecodeUpdateArgs a) 
     bool merge = false;
     if (plen > 0) {                                                  // :61-77
       const uint32_t lk = act ? *(const uint32_t*)(pk + (int64_t)(plen - 1) * a.sp_s) : 0u;
-      const float e0 = E16<DT>::lo(ek), e1 = E16<DT>::hi(ek), l0 = E16<DT>::lo(lk), l1 = E16<DT>::hi(lk);
-      if (COS) {
-        const float eps = 1e-8f;
-        const float dot = wave_tree_sum(pair_dot(e0, e1, l0, l1));
-        const float ne = sqrt_rn(wave_tree_sum(pair_dot(e0, e1, e0, e1)) + eps);
-        const float nl = sqrt_rn(wave_tree_sum(pair_dot(l0, l1, l0, l1)) + eps);
-        merge = __fdiv_rn(dot, ne * nl) >= a.thr;
-      } else {
-        const float d0 = e0 - l0, d1 = e1 - l1;
-        merge = wave_tree_sum(pair_dot(d0, d1, d0, d1)) <= a.thr;
-      }
+      merge = evict_merges<COS, DT>(ek, lk, a.thr);
     }
     if (merge) {                                                     // :78-82
       if (lane == 0) cnt[plen - 1] += 1;
@@ -127,6 +136,18 @@ struct DecodeAttnArgs {
   int nslice;
   int B, Hq, Hkv, G;
   int D;            // head dimension: a multiple of 8, at most kDecD
+  // da_decode_step's fused update only: the new token, its ring slot widx, whether the
+  // ring was full (evict: the token in slot widx leaves it), the update's test, the
+  // timestamp base, the writable cache arrays, and per (batch, kv head) two ints in the
+  // workspace: the update's decision (0 drop, 1 merge, 2 append) and the key list length
+  const uint16_t* new_k;
+  const uint16_t* new_v;
+  int64_t sn_b, sn_h;
+  int widx, evict, cosine;
+  float thr;
+  int64_t total_len, window;
+  int32_t* ts;
+  int32_t* fused;
 };
 
 __device__ __forceinline__ float wave_max_all(float v) {
@@ -153,7 +174,21 @@ __device__ __forceinline__ float wave_sum_all(float v) {
 // D = 128 (22.5 against 20.0 us per call after the config-1 prefill).
 // Small slices keep many waves in flight per CU: the kernel is latency-bound at decode
 // sizes, and holding K and V rows at once would halve the waves per SIMD.
-template <int G, int DT, bool FULL>
+//
+// FUSED (da_decode_step): the token's cache update enters this launch instead of running
+// before it.  The list is the packed anchors [0, plen) (as before the update), the ring
+// slots [0, exact_len) with slot widx holding the new token (read from new_k / new_v),
+// and, when the ring was full, one extra key jx = plen + exact_len: the evicted token,
+// still in slot widx.  Its row never depends on the update's decision; the weights do.
+// A merge gives the last anchor count + 1, as the update would, and the extra key weight
+// zero; an append gives the extra key count 1, which is the update's new anchor at
+// another place in the list; a drop (no room) gives it zero.  So merges and drops score
+// exactly the list the update leaves, and an append adds the same terms in another
+// order.  The waves whose slice holds key plen - 1 or key jx evaluate the update's test
+// (its two rows loaded with the key rows, the test after the scores), and the wave
+// holding jx records the decision.  The cache itself is written by the combine kernel,
+// after every read of this launch.
+template <int G, int DT, bool FULL, bool FUSED>
 __global__ __launch_bounds__(64) void decode_attn_kernel(DecodeAttnArgs a) {
   __shared__ float s_q[G][kDecD];
   __shared__ float s_p[G][kDecSlice];
@@ -170,9 +205,33 @@ __global__ __launch_bounds__(64) void decode_attn_kernel(DecodeAttnArgs a) {
   const int b = bg / a.Hkv, g = bg - (bg / a.Hkv) * a.Hkv;
   int plen = a.lengths[bg];
   plen = plen < 0 ? 0 : (plen > a.capacity ? (int)a.capacity : plen);
-  const int total = plen + a.exact_len;
+  const int jx = plen + a.exact_len;                   // the extra key's index (FUSED)
+  const int total = jx + (FUSED && a.evict ? 1 : 0);
   const int j0 = slice * kDecSlice;
+  if (FUSED && slice == 0 && blockIdx.z == 0 && lane == 0) a.fused[2 * bg + 1] = total;
   if (j0 >= total) return;  // the combine kernel skips slices past the end
+  const uint16_t* const pk_row0 = a.kp + b * a.sp_b + g * a.sp_h;
+  const uint16_t* const pv_row0 = a.vp + b * a.sp_b + g * a.sp_h;
+  const uint16_t* const xk_row0 = a.kx + b * a.sx_b + g * a.sx_h;
+  const uint16_t* const xv_row0 = a.vx + b * a.sx_b + g * a.sx_h;
+  // FUSED: the waves whose slice holds the last anchor or the extra key need the update's
+  // decision; the two rows it compares are loaded first, the test waits for the scores
+  const bool holds_last = FUSED && plen > 0 && plen - 1 >= j0 && plen - 1 < j0 + kDecSlice;
+  const bool holds_extra = FUSED && jx < j0 + kDecSlice;  // jx >= j0: slice j0 is not past the end
+  const bool need_dec = FUSED && a.evict && (holds_last || holds_extra);
+  uint32_t ek = 0u, lk = 0u;
+  if (need_dec && 2 * lane < D) {
+    ek = *(const uint32_t*)(xk_row0 + (int64_t)a.widx * a.sx_s + 2 * lane);
+    if (plen > 0) lk = *(const uint32_t*)(pk_row0 + (int64_t)(plen - 1) * a.sp_s + 2 * lane);
+  }
+  // the key / value row of list index jj (FUSED: the new token in ring slot widx, and the
+  // extra key jx, the evicted token, still in that slot)
+  auto key_row = [&](int jj, const uint16_t* p0, const uint16_t* x0, const uint16_t* nw) -> const uint16_t* {
+    if (jj < plen) return p0 + (int64_t)jj * a.sp_s;
+    const int r = FUSED && jj >= jx ? a.widx : jj - plen;
+    if (FUSED && r == a.widx && jj < jx) return nw + b * a.sn_b + g * a.sn_h;
+    return x0 + (int64_t)r * a.sx_s;
+  };
 
   // This lane's key row and count and the group's query rows (G * D / 64 elements per
   // lane) go out together, before the first wait.
@@ -181,8 +240,7 @@ __global__ __launch_bounds__(64) void decode_attn_kernel(DecodeAttnArgs a) {
   u32x4 kw[kDecD / 8];
   int cnt = 1;
   if (valid) {
-    const uint16_t* krow = j < plen ? a.kp + b * a.sp_b + g * a.sp_h + (int64_t)j * a.sp_s
-                                    : a.kx + b * a.sx_b + g * a.sx_h + (int64_t)(j - plen) * a.sx_s;
+    const uint16_t* krow = key_row(j, pk_row0, xk_row0, a.new_k);
 #pragma unroll
     for (int c8 = 0; c8 < kDecD / 8; ++c8) kw[c8] = *(const u32x4*)(krow + 8 * (FULL ? c8 : min(c8, dlast8)));
     if (j < plen) cnt = a.counts[b * a.sc_b + g * a.sc_h + j];
@@ -205,10 +263,8 @@ __global__ __launch_bounds__(64) void decode_attn_kernel(DecodeAttnArgs a) {
   float sc[G];
 #pragma unroll
   for (int hh = 0; hh < G; ++hh) sc[hh] = -INFINITY;
-  if (valid) {
-    // log(count) bias; log(0) = -inf: padding anchors get no weight (:309-311)
-    const float bias = j >= plen ? 0.0f : (cnt <= 0 ? -INFINITY : __logf((float)cnt));
-    float acc[G];
+  // q . k for the group's heads (this lane's key row)
+  auto dot_group = [&](float (&acc)[G]) {
 #pragma unroll
     for (int hh = 0; hh < G; ++hh) acc[hh] = 0.0f;
 #pragma unroll
@@ -224,20 +280,65 @@ __global__ __launch_bounds__(64) void decode_attn_kernel(DecodeAttnArgs a) {
         }
       }
     }
+  };
+  // log(count) bias; log(0) = -inf: padding anchors get no weight (:309-311); ring keys
+  // weigh one
+  auto bias_of = [&](int c) {
+    return j >= plen && (!FUSED || j < jx) ? 0.0f : (c <= 0 ? -INFINITY : __logf((float)c));
+  };
+  if constexpr (!FUSED) {
+    if (valid) {
+      const float bias = bias_of(cnt);
+      float acc[G];
+      dot_group(acc);
 #pragma unroll
-    for (int hh = 0; hh < G; ++hh)
-      if (hh < G) sc[hh] = acc[hh] * a.scale + bias;
+      for (int hh = 0; hh < G; ++hh) sc[hh] = acc[hh] * a.scale + bias;
+    }
+  } else {
+    float acc[G];
+    if (valid) dot_group(acc);
+    // the update's decision (deltaDecoding.py:61-96): a merge weighs the last anchor with
+    // count + 1, an append gives the evicted token (key jx) weight one, a drop (no room)
+    // weight zero; the extra key of a merge or drop carries no weight.  Every lane runs
+    // the test (wave reductions).
+    if (need_dec) {
+      const bool merge = plen > 0 && (a.cosine ? evict_merges<true, DT>(ek, lk, a.thr)
+                                               : evict_merges<false, DT>(ek, lk, a.thr));
+      const int dec = merge ? 1 : (plen < a.capacity ? 2 : 0);
+      if (holds_extra && blockIdx.z == 0 && lane == 0) a.fused[2 * bg] = dec;
+      if (j == plen - 1 && dec == 1) cnt += 1;
+      if (j == jx) cnt = dec == 2 ? 1 : 0;
+    }
+    if (valid) {
+      const float bias = bias_of(cnt);
+#pragma unroll
+      for (int hh = 0; hh < G; ++hh) sc[hh] = acc[hh] * a.scale + bias;
+    }
   }
 
   // ---- the slice's 64 value rows (rows past the end load nothing and carry p = 0),
   // in flight during the softmax ----
+  // A slice of packed anchors only (most of them) reads its rows at one stride from one
+  // base.  In the others, lane t finds the source of row j0 + t (clamped to the list's
+  // last key: every pointer is a real row) and row u's loads take lane u's pointer; rows
+  // past the end carry p = 0.
   uint32_t vw[kDecSlice];
+  if (j0 + kDecSlice <= plen) {
+    const uint16_t* vrow = pv_row0 + (int64_t)j0 * a.sp_s + vdim;
 #pragma unroll
-  for (int u = 0; u < kDecSlice; ++u) {
-    const int jk = j0 + u;
-    const uint16_t* vrow = jk < plen ? a.vp + b * a.sp_b + g * a.sp_h + (int64_t)jk * a.sp_s
-                                     : a.vx + b * a.sx_b + g * a.sx_h + (int64_t)(jk - plen) * a.sx_s;
-    vw[u] = jk < total ? *(const uint32_t*)(vrow + vdim) : 0u;
+    for (int u = 0; u < kDecSlice; ++u) vw[u] = *(const uint32_t*)(vrow + (int64_t)u * a.sp_s);
+  } else {
+    const uint64_t mine = (uint64_t)key_row(min(j, total - 1), pv_row0, xv_row0, a.new_v);
+    const uint32_t lo = (uint32_t)mine, hi = (uint32_t)(mine >> 32);
+    const uint32_t voff = 2u * (uint32_t)vdim;  // bytes; unsigned, for scalar base + vector offset
+#pragma unroll
+    for (int u = 0; u < kDecSlice; ++u) {
+      const uint64_t row = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane(hi, u) << 32) |
+                           (uint32_t)__builtin_amdgcn_readlane(lo, u);
+      vw[u] = *(const __attribute__((address_space(1))) uint32_t*)(row + voff);  // a global load
+      // in groups of 16 rows: the addresses are not all formed ahead of the loads
+      if ((u & 15) == 15) __builtin_amdgcn_sched_barrier(0);
+    }
   }
 
   // ---- per-head slice max and sum; weights rounded to the cache's type, to LDS ----
@@ -287,7 +388,15 @@ __global__ __launch_bounds__(64) void decode_attn_kernel(DecodeAttnArgs a) {
 constexpr int kDecMaxSlices = 16384;
 constexpr int kCombParts = 4, kCombDims = kDecD / kCombParts, kCombPhases = 256 / kCombDims;
 constexpr int kCombUnroll = 32;
-template <int DT>
+//
+// FUSED (da_decode_step): the list length comes from the attention launch (the update
+// below may change the packed length), and after the merge the workgroup of the
+// group's first query head and first dim part writes the token's cache update
+// (deltaDecoding.py:54-104) with the attention's decision: a merge adds one to the last
+// anchor's count, an append copies the evicted token out of its ring slot into packed
+// row plen (count 1, timestamp total - W, length plen + 1), and then the new token takes
+// the ring slot.  Every read of the attention launch is done by then (stream order).
+template <int DT, bool FUSED>
 __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeAttnArgs a) {
   __shared__ float s_f[kDecMaxSlices];
   __shared__ float s_red[8];
@@ -299,7 +408,8 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeAttnArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
   int plen = a.lengths[bg];
   plen = plen < 0 ? 0 : (plen > a.capacity ? (int)a.capacity : plen);
-  const int total = plen + a.exact_len;
+  int total = FUSED ? a.fused[2 * bg + 1] : plen + a.exact_len;
+  total = total < 0 ? 0 : (total > a.nslice * kDecSlice ? a.nslice * kDecSlice : total);
   const int ns = (total + kDecSlice - 1) / kDecSlice;
   const float* base = a.part + (int64_t)bg * a.nslice * a.G * (kDecD + 2) + hh * (kDecD + 2);
   // 32-bit offsets within one (batch, KV head): nslice * G * (kDecD + 2) stays below
@@ -371,6 +481,37 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeAttnArgs a) {
     for (int p = 1; p < kCombPhases; ++p) o += s_acc[p][dl];
     a.out[b * a.so_b + hq * a.so_h + d] = E16<DT>::bits(o / L);
   }
+  if constexpr (FUSED) {
+    if (hh == 0 && blockIdx.y == 0 && tid < 64) {
+      const bool act = 2 * tid < a.D;
+      uint16_t* const ring_k = const_cast<uint16_t*>(a.kx) + b * a.sx_b + g * a.sx_h + (int64_t)a.widx * a.sx_s + 2 * tid;
+      uint16_t* const ring_v = const_cast<uint16_t*>(a.vx) + b * a.sx_b + g * a.sx_h + (int64_t)a.widx * a.sx_s + 2 * tid;
+      int32_t* const cnt = const_cast<int32_t*>(a.counts) + b * a.sc_b + g * a.sc_h;
+      if (a.evict) {
+        const int dec = a.fused[2 * bg];
+        if (dec == 1) {  // :78-82
+          if (tid == 0) cnt[plen - 1] += 1;
+        } else if (dec == 2) {  // :83-96
+          if (act) {
+            uint16_t* const pk = const_cast<uint16_t*>(a.kp) + b * a.sp_b + g * a.sp_h + (int64_t)plen * a.sp_s + 2 * tid;
+            uint16_t* const pv = const_cast<uint16_t*>(a.vp) + b * a.sp_b + g * a.sp_h + (int64_t)plen * a.sp_s + 2 * tid;
+            *(uint32_t*)pk = *(const uint32_t*)ring_k;
+            *(uint32_t*)pv = *(const uint32_t*)ring_v;
+          }
+          if (tid == 0) {
+            cnt[plen] = 1;
+            a.ts[b * a.sc_b + g * a.sc_h + plen] = (int32_t)(a.total_len - a.window);
+            const_cast<int32_t*>(a.lengths)[bg] = plen + 1;
+          }
+        }
+      }
+      // the new token into the ring (:101-104), after this thread's read of the evicted one
+      if (act) {
+        *(uint32_t*)ring_k = *(const uint32_t*)(a.new_k + b * a.sn_b + g * a.sn_h + 2 * tid);
+        *(uint32_t*)ring_v = *(const uint32_t*)(a.new_v + b * a.sn_b + g * a.sn_h + 2 * tid);
+      }
+    }
+  }
 }
 
 }  // namespace da
@@ -427,7 +568,7 @@ extern "C" int da_decode_update(const void* new_k, const void* new_v, int dtype,
                             "da_decode_update");
 }
 
-template <int DT, bool FULL>
+template <int DT, bool FULL, bool FUSED>
 static int launch_decode_g(DecodeAttnArgs& a, int64_t n_heads, hipStream_t st) {
   // a group above kDecMaxG query heads is split into ceil(G / kDecMaxG) sub-groups of
   // equal size (the last one smaller when G does not divide), one wave each
@@ -435,27 +576,35 @@ static int launch_decode_g(DecodeAttnArgs& a, int64_t n_heads, hipStream_t st) {
   const int gw = (a.G + nsub - 1) / nsub;
   const dim3 agrid((unsigned)(a.B * a.Hkv), (unsigned)a.nslice, (unsigned)nsub);
   switch (gw) {
-    case 1: hipLaunchKernelGGL((decode_attn_kernel<1, DT, FULL>), agrid, dim3(64), 0, st, a); break;
-    case 2: hipLaunchKernelGGL((decode_attn_kernel<2, DT, FULL>), agrid, dim3(64), 0, st, a); break;
-    case 3: hipLaunchKernelGGL((decode_attn_kernel<3, DT, FULL>), agrid, dim3(64), 0, st, a); break;
-    case 4: hipLaunchKernelGGL((decode_attn_kernel<4, DT, FULL>), agrid, dim3(64), 0, st, a); break;
-    case 5: hipLaunchKernelGGL((decode_attn_kernel<5, DT, FULL>), agrid, dim3(64), 0, st, a); break;
-    case 6: hipLaunchKernelGGL((decode_attn_kernel<6, DT, FULL>), agrid, dim3(64), 0, st, a); break;
-    case 7: hipLaunchKernelGGL((decode_attn_kernel<7, DT, FULL>), agrid, dim3(64), 0, st, a); break;
-    default: hipLaunchKernelGGL((decode_attn_kernel<8, DT, FULL>), agrid, dim3(64), 0, st, a); break;
+    case 1: hipLaunchKernelGGL((decode_attn_kernel<1, DT, FULL, FUSED>), agrid, dim3(64), 0, st, a); break;
+    case 2: hipLaunchKernelGGL((decode_attn_kernel<2, DT, FULL, FUSED>), agrid, dim3(64), 0, st, a); break;
+    case 3: hipLaunchKernelGGL((decode_attn_kernel<3, DT, FULL, FUSED>), agrid, dim3(64), 0, st, a); break;
+    case 4: hipLaunchKernelGGL((decode_attn_kernel<4, DT, FULL, FUSED>), agrid, dim3(64), 0, st, a); break;
+    case 5: hipLaunchKernelGGL((decode_attn_kernel<5, DT, FULL, FUSED>), agrid, dim3(64), 0, st, a); break;
+    case 6: hipLaunchKernelGGL((decode_attn_kernel<6, DT, FULL, FUSED>), agrid, dim3(64), 0, st, a); break;
+    case 7: hipLaunchKernelGGL((decode_attn_kernel<7, DT, FULL, FUSED>), agrid, dim3(64), 0, st, a); break;
+    default: hipLaunchKernelGGL((decode_attn_kernel<8, DT, FULL, FUSED>), agrid, dim3(64), 0, st, a); break;
   }
   if (int rc = check_launch("da_decode_attention")) return rc;
-  hipLaunchKernelGGL((decode_combine_kernel<DT>), dim3((unsigned)n_heads, kCombParts), dim3(256), 0, st, a);
+  hipLaunchKernelGGL((decode_combine_kernel<DT, FUSED>), dim3((unsigned)n_heads, kCombParts), dim3(256), 0, st, a);
   return check_launch("da_decode_attention(combine)");
 }
-template <int DT>
+template <int DT, bool FUSED>
 static int launch_decode(DecodeAttnArgs& a, int64_t n_heads, hipStream_t st) {
-  return a.D == kDecD ? launch_decode_g<DT, true>(a, n_heads, st) : launch_decode_g<DT, false>(a, n_heads, st);
+  return a.D == kDecD ? launch_decode_g<DT, true, FUSED>(a, n_heads, st)
+                      : launch_decode_g<DT, false, FUSED>(a, n_heads, st);
 }
 
+// Slices of a key list of up to capacity + window keys, plus the extra key of
+// da_decode_step's fused update.
+static int64_t decode_slices(int64_t capacity, int64_t window) {
+  return (capacity + window + 1 + kDecSlice - 1) / kDecSlice;
+}
+
+// The slice partials, then (da_decode_step) two ints per (batch, query head).
 extern "C" int64_t da_decode_workspace_size(int64_t B, int64_t Hq, int64_t capacity, int64_t window) {
-  const int64_t nslice = (capacity + window + kDecSlice - 1) / kDecSlice;
-  return B * Hq * nslice * (kDecD + 2) * (int64_t)sizeof(float);
+  return B * Hq * decode_slices(capacity, window) * (kDecD + 2) * (int64_t)sizeof(float) +
+         2 * B * Hq * (int64_t)sizeof(int32_t);
 }
 
 // Validation and launch shared by da_decode_attention and da_decode_attention_noalloc:
@@ -476,7 +625,7 @@ static int decode_attention_impl(const void* q, int dtype, int64_t B, int64_t Hq
   a.part = part;
   a.nslice = (int)((capacity + window + kDecSlice - 1) / kDecSlice);
   a.B = (int)B; a.Hq = (int)Hq; a.Hkv = (int)Hkv; a.G = (int)(Hq / Hkv); a.D = (int)D;
-  return dtype == DA_F16 ? launch_decode<DA_F16>(a, B * Hq, st) : launch_decode<DA_BF16>(a, B * Hq, st);
+  return dtype == DA_F16 ? launch_decode<DA_F16, false>(a, B * Hq, st) : launch_decode<DA_BF16, false>(a, B * Hq, st);
 }
 
 // Argument checks common to both decode attention entry points.
@@ -499,8 +648,8 @@ static int decode_attention_check(const void* q, int dtype, int64_t B, int64_t H
   DA_REQUIRE(((sp_b | sp_h | sp_s | sx_b | sx_h | sx_s) & 7) == 0 && (((uintptr_t)k_packed | (uintptr_t)k_exact) & 15) == 0,
              "%s: key rows must be 16-byte aligned", who);
   DA_REQUIRE((((uintptr_t)v_packed | (uintptr_t)v_exact) & 3) == 0, "%s: value rows must be 4-byte aligned", who);
-  if ((capacity + window + kDecSlice - 1) / kDecSlice > kDecMaxSlices)
-    return set_error(DA_ERR_UNSUPPORTED, "%s: cache longer than %d keys", who, kDecMaxSlices * kDecSlice);
+  if (decode_slices(capacity, window) > kDecMaxSlices)
+    return set_error(DA_ERR_UNSUPPORTED, "%s: cache longer than %d keys", who, kDecMaxSlices * kDecSlice - 1);
   return DA_OK;
 }
 
@@ -526,6 +675,34 @@ extern "C" int da_decode_attention(const void* q, int dtype, int64_t B, int64_t 
                                exact_len, scale, out, so_b, so_h, (float*)workspace, (hipStream_t)stream);
 }
 
+// One token of da_decode_step as two launches: the attention with the update folded into
+// its key list, and the combine that then writes the cache (decode_attn_kernel and
+// decode_combine_kernel, FUSED).  Needs the new token's rows 16-byte aligned, as the
+// attention reads key rows; the caller falls back to update + attention otherwise.
+static int decode_step_fused(const DaDecodeStep* s, int64_t exact_len, hipStream_t st) {
+  DecodeAttnArgs a = {};
+  a.q = (const uint16_t*)s->q; a.sq_b = s->sq_b; a.sq_h = s->sq_h;
+  a.kp = (const uint16_t*)s->k_packed; a.vp = (const uint16_t*)s->v_packed;
+  a.sp_b = s->sp_b; a.sp_h = s->sp_h; a.sp_s = s->sp_s;
+  a.counts = s->counts; a.sc_b = s->sc_b; a.sc_h = s->sc_h; a.lengths = s->lengths; a.capacity = s->capacity;
+  a.kx = (const uint16_t*)s->k_exact; a.vx = (const uint16_t*)s->v_exact;
+  a.sx_b = s->sx_b; a.sx_h = s->sx_h; a.sx_s = s->sx_s;
+  a.exact_len = (int)exact_len; a.scale = s->scale; a.out = (uint16_t*)s->out; a.so_b = s->so_b; a.so_h = s->so_h;
+  a.part = (float*)s->workspace;
+  a.nslice = (int)decode_slices(s->capacity, s->window);
+  a.B = (int)s->B; a.Hq = (int)s->Hq; a.Hkv = (int)s->Hkv; a.G = (int)(s->Hq / s->Hkv); a.D = (int)s->D;
+  a.new_k = (const uint16_t*)s->new_k; a.new_v = (const uint16_t*)s->new_v; a.sn_b = s->sn_b; a.sn_h = s->sn_h;
+  a.widx = (int)(s->exact_seq_len % s->window);
+  a.evict = s->exact_seq_len >= s->window ? 1 : 0;
+  a.cosine = s->use_cosine ? 1 : 0;
+  a.thr = s->threshold;
+  a.total_len = s->total_seq_len; a.window = s->window;
+  a.ts = s->timestamps;
+  a.fused = (int32_t*)((float*)s->workspace + s->B * s->Hq * a.nslice * (int64_t)(kDecD + 2));
+  return s->dtype == DA_F16 ? launch_decode<DA_F16, true>(a, s->B * s->Hq, st)
+                            : launch_decode<DA_BF16, true>(a, s->B * s->Hq, st);
+}
+
 // One decode token in one call: the cache update, then the attention over the updated
 // cache (its ring holds min(exact_seq_len + 1, window) tokens).
 extern "C" int da_decode_step(const DaDecodeStep* s, void* stream) {
@@ -539,6 +716,11 @@ extern "C" int da_decode_step(const DaDecodeStep* s, void* stream) {
   const int64_t need = da_decode_workspace_size(s->B, s->Hq, s->capacity, s->window);
   if (!s->workspace || s->workspace_bytes < need)
     return set_error(DA_ERR_WORKSPACE, "%s: workspace of %lld bytes required", who, (long long)need);
+  DA_REQUIRE(s->new_k && s->new_v && s->timestamps, "%s: null pointer", who);
+  DA_REQUIRE(s->exact_seq_len >= 0 && s->total_seq_len >= 0, "%s: negative lengths", who);
+  // the fused path reads the new token's key row like the cache's: 16-byte aligned rows
+  if (((s->sn_b | s->sn_h) & 7) == 0 && (((uintptr_t)s->new_k | (uintptr_t)s->new_v) & 15) == 0)
+    return decode_step_fused(s, exact_len, (hipStream_t)stream);
   if (int rc = decode_update_impl(s->new_k, s->new_v, s->dtype, s->B, s->Hkv, s->D, s->sn_b, s->sn_h, s->k_exact,
                                   s->v_exact, s->sx_b, s->sx_h, s->sx_s, s->k_packed, s->v_packed, s->sp_b,
                                   s->sp_h, s->sp_s, s->counts, s->timestamps, s->sc_b, s->sc_h, s->lengths,
@@ -612,7 +794,7 @@ extern "C" int da_decode_attention_noalloc(const void* q, int dtype, int64_t B, 
   if (need > (int64_t)DA_DECODE_SCRATCH_BYTES)
     return set_error(DA_ERR_UNSUPPORTED,
                      "%s: needs %lld bytes of scratch, above the static maximum of %lld "
-                     "(B * Hq * ceil((capacity + window) / 64) * 520 bytes); use da_decode_attention",
+                     "(B * Hq * (ceil((capacity + window + 1) / 64) * 520 + 8) bytes); use da_decode_attention",
                      who, (long long)need, (long long)DA_DECODE_SCRATCH_BYTES);
   void* part = nullptr;
   if (int rc = scratch_for_current_device(&part, (hipStream_t)stream, who)) return rc;

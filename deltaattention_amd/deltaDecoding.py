@@ -290,8 +290,10 @@ class HybridCompressedCache(_CacheBase):
         """One decode token of one layer in one library call: ``update`` and
         ``decode_attention`` (modeling_llama.py:565-567 then :453-518) fused into
         ``da_decode_step``, with the layer's argument block built once.  q [B, Hq, 1, D],
-        key/value [B, Hkv, 1, D] -> [B, Hq, 1, D]; results and cache state are those of
-        the two calls in sequence."""
+        key/value [B, Hkv, 1, D] -> [B, Hq, 1, D].  The cache state is that of the two calls
+        in sequence, bit for bit; so is the output of every KV head whose evicted token
+        merged or was dropped, while one that appended gets the same terms summed in
+        another order (the new anchor is scored at the end of its key list)."""
         if self.max_packed_len[layer_idx] + 1 >= self.capacity:
             self._expand_capacity(self.capacity + 1024)
         B, Hq, _, D = query_states.shape

@@ -255,8 +255,19 @@ int da_decode_attention(const void* q, int dtype, int64_t B, int64_t Hq, int64_t
  * path per token matters (token-by-token decode, one call per layer instead of two,
  * with every argument in one block the caller fills once per layer and updates per
  * token).  Fields mean what the same-named arguments of the two entries above mean;
- * the checks are theirs (D = 128 for the attention).  Results are bit-identical to the
- * two calls in sequence.
+ * the checks are theirs.
+ *
+ * Two launches instead of three: the attention scores the cache as it was plus the new
+ * token in its ring slot and, when the ring was full, the evicted token as one more key
+ * whose weight follows the update's decision (a merge gives the last anchor count + 1,
+ * an append gives the evicted token count 1, a drop gives it 0); the launch that merges
+ * the slices then writes the update into the cache.  The cache afterwards is
+ * bit-identical to the two calls'.  The output is bit-identical for every KV head whose
+ * token merged, was dropped or evicted nothing; where it appended, the new anchor is
+ * scored at the end of the key list instead of after the packed anchors, so the output
+ * equals the two calls' up to fp32 summation order.  New-token rows that are not 16-byte
+ * aligned (sn_b, sn_h multiples of 8 elements, new_k / new_v 16-byte aligned) run the
+ * update and attention kernels in sequence instead, bit-identical to the two calls.
  */
 typedef struct DaDecodeStep {
   /* this token */
@@ -298,7 +309,7 @@ int da_decode_step(const DaDecodeStep* step, void* stream);
  * live in a static device array of DA_DECODE_SCRATCH_BYTES per GPU (held until the
  * process ends), so da_decode_workspace_size(B, Hq, capacity, window) must not exceed
  * DA_DECODE_SCRATCH_BYTES (DA_ERR_UNSUPPORTED otherwise; e.g. B = 1, Hq = 32 allows
- * capacity + window up to 129024 keys).  The stream must belong to the current device
+ * capacity + window up to 129023 keys).  The stream must belong to the current device
  * (checked: DA_ERR_INVALID otherwise; the null stream is the current device's).
  * Every call on one GPU shares that GPU's array: calls that overlap on one GPU (on
  * streams not ordered with each other) race.

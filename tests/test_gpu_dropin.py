@@ -220,6 +220,67 @@ def test_decode_cache_matches_oracle(gpu, metric, tau, dtype):
             setattr(globVR, name, val)
 
 
+def _misaligned(t):
+    """A copy of t whose data starts 8 bytes past a 16-byte boundary: da_decode_step then
+    takes its unfused path (update kernel, then attention)."""
+    buf = torch.empty(t.numel() + 4, dtype=t.dtype, device=t.device)
+    out = buf[4:].view(t.shape)
+    out.copy_(t)
+    assert out.data_ptr() % 16 == 8
+    return out
+
+
+def _decode_twins(gpu, dtype, Hq, Hkv, steps, cap0, grow, seed=11):
+    """Two caches fed the same tokens: cache a by cache.update + decode_attention, cache b
+    by cache.decode_step.  Even steps hand decode_step 16-byte aligned key/value rows (the
+    fused launch pair: the update folded into the attention); odd steps misaligned ones (the
+    unfused path, which must equal the two calls bit for bit).  The fused path's output
+    is bit-identical for every KV head whose step merged, dropped or evicted nothing, and
+    differs only in rounding where it appended: the evicted token then sits at the end of
+    its key list instead of after the packed anchors, so the slice sums add the same terms
+    in another order (bar: max-abs 1e-2 bf16, 2e-3 fp16).  The cache state must be
+    bit-identical.  grow=False holds the capacity (the host
+    tracker is kept below it), so a full cache drops evicted tokens that do not merge
+    (deltaDecoding.py:83-96)."""
+    from types import SimpleNamespace
+    from deltaattention_amd.deltaDecoding import HybridCompressedCache, decode_attention
+    B, W = 2, 16
+    q, k, v = (t.to(dtype) for t in _inputs(B, Hq, Hkv, steps, seed))
+    cfg = SimpleNamespace(hidden_size=Hq * 128, num_attention_heads=Hq, num_key_value_heads=Hkv,
+                          num_hidden_layers=2, head_dim=128)
+    a = HybridCompressedCache(cfg, B, dtype=dtype, exact_window_size=W, initial_capacity=cap0)
+    b = HybridCompressedCache(cfg, B, dtype=dtype, exact_window_size=W, initial_capacity=cap0)
+    qg, kg, vg = q.to(gpu), k.to(gpu), v.to(gpu)
+    bar = 1e-2 if dtype == torch.bfloat16 else 2e-3
+    worst, exact_heads = 0.0, 0
+    for t in range(steps):
+        if not grow:
+            a.max_packed_len[1] = b.max_packed_len[1] = -steps
+        qt, kt, vt = qg[:, :, t:t + 1], kg[:, :, t:t + 1], vg[:, :, t:t + 1]
+        a.update(kt, vt, 1)
+        want = decode_attention(qt, a, 1, scaling=0.07)
+        if t % 2:
+            got = b.decode_step(qt, _misaligned(kt), _misaligned(vt), 1, scaling=0.07)
+            assert torch.equal(got, want), t
+        else:
+            before = b.packed_lengths[1].clone()
+            got = b.decode_step(qt, kt, vt, 1, scaling=0.07)
+            err = float((got.float() - want.float()).abs().max())
+            worst = max(worst, err)
+            assert err <= bar, (t, err)
+            appended = (b.packed_lengths[1] != before).reshape(B, Hkv)
+            same = ~appended.repeat_interleave(Hq // Hkv, dim=1)   # [B, Hq]
+            assert torch.equal(got[same], want[same]), t
+            exact_heads += int(same.sum())
+        assert got.shape == want.shape == (B, Hq, 1, 128)
+    assert (b.exact_seq_lens, b.total_seq_lens) == (a.exact_seq_lens, a.total_seq_lens)
+    for name in ("packed_lengths", "packed_counts", "packed_timestamps", "k_packed",
+                 "v_packed", "k_exact", "v_exact"):
+        assert torch.equal(getattr(a, name), getattr(b, name)), name
+    assert 0 < exact_heads < B * Hq * ((steps + 1) // 2)
+    return a, b, worst
+
+
 @pytest.mark.parametrize("metric,tau,dtype,Hq,Hkv", [
     ("euclidean", 9.5, torch.bfloat16, 8, 2),
     ("cosine", 0.9, torch.bfloat16, 8, 2),
@@ -227,40 +288,48 @@ def test_decode_cache_matches_oracle(gpu, metric, tau, dtype):
 ], ids=["euclidean-bf16-G4", "cosine-bf16-G4", "euclidean-fp16-G8"])
 def test_decode_step_equals_update_then_attention(gpu, metric, tau, dtype, Hq, Hkv):
     """HybridCompressedCache.decode_step (one da_decode_step call per token) against
-    cache.update + decode_attention on a twin cache: every step's output and the final
-    cache state bit-identical, through ring fill, eviction into the packed cache and a
-    capacity growth (initial capacity 8) that rebuilds the cached argument block."""
-    from types import SimpleNamespace
+    cache.update + decode_attention on a twin cache, through ring fill, eviction into the
+    packed cache and a capacity growth (initial capacity 8) that rebuilds the cached
+    argument block: the cache state bit-identical after 96 tokens, the unfused path's
+    outputs bit-identical and the fused path's within rounding."""
     from deltaattention_amd import globVR
-    from deltaattention_amd.deltaDecoding import HybridCompressedCache, decode_attention
     B, W, steps = 2, 16, 96
-    q, k, v = (t.to(dtype) for t in _inputs(B, Hq, Hkv, steps, 11))
-    cfg = SimpleNamespace(hidden_size=Hq * 128, num_attention_heads=Hq, num_key_value_heads=Hkv,
-                          num_hidden_layers=2, head_dim=128)
     saved = dict(vars(globVR))
     try:
         globVR.row_delta_threshold, globVR.row_similarity_metric = tau, metric
-        a = HybridCompressedCache(cfg, B, dtype=dtype, exact_window_size=W, initial_capacity=8)
-        b = HybridCompressedCache(cfg, B, dtype=dtype, exact_window_size=W, initial_capacity=8)
-        qg, kg, vg = q.to(gpu), k.to(gpu), v.to(gpu)
-        announce(f"decode_step {metric}: {steps} steps on layer 1, B={B} Hq={Hq} Hkv={Hkv} W={W}")
-        for t in range(steps):
-            qt, kt, vt = qg[:, :, t:t + 1], kg[:, :, t:t + 1], vg[:, :, t:t + 1]
-            a.update(kt, vt, 1)
-            want = decode_attention(qt, a, 1, scaling=0.07)
-            got = b.decode_step(qt, kt, vt, 1, scaling=0.07)
-            assert got.shape == want.shape == (B, Hq, 1, 128)
-            assert torch.equal(got, want), t
+        announce(f"decode_step {metric}: {steps} steps on layer 1, Hq={Hq} Hkv={Hkv} W={W}")
+        a, b, worst = _decode_twins(gpu, dtype, Hq, Hkv, steps, 8, True)
         assert b.capacity == a.capacity > 8
-        assert (b.exact_seq_lens, b.total_seq_lens) == (a.exact_seq_lens, a.total_seq_lens)
         n = int(a.packed_lengths[1].max().item())
         assert 0 < n < B * Hkv * (steps - W)
-        for name in ("packed_lengths", "packed_counts", "packed_timestamps", "k_packed",
-                     "v_packed", "k_exact", "v_exact"):
-            assert torch.equal(getattr(a, name), getattr(b, name)), name
-        with pytest.raises(ValueError):
-            b.decode_step(qg[:, :, :1], kg[:, :1, :1], vg[:, :1, :1], 1)
-        print(f"decode_step {metric}: packed length {n} after {steps} tokens", flush=True)
+        merged = int(a.packed_counts[1].sum().item()) - int(a.packed_lengths[1].sum().item())
+        assert merged > 0   # both decisions occur
+        x = torch.zeros((B, Hq, 1, 128), dtype=dtype, device=gpu)
+        with pytest.raises(ValueError):   # one KV head where the cache has Hkv
+            b.decode_step(x, x[:, :1], x[:, :1], 1)
+        print(f"decode_step {metric}: packed length {n}, merged {merged}, fused max-abs {worst:.3e}",
+              flush=True)
+    finally:
+        for name, val in saved.items():
+            setattr(globVR, name, val)
+
+
+def test_decode_step_full_cache_drops_like_update(gpu):
+    """A packed cache held at capacity 8: evicted tokens that do not merge are dropped
+    (deltaDecoding.py:83-96), in the fused step as in the update kernel; the dropped
+    token gets no weight in the fused attention (count 0)."""
+    from deltaattention_amd import globVR
+    saved = dict(vars(globVR))
+    try:
+        globVR.row_delta_threshold, globVR.row_similarity_metric = 9.5, "euclidean"
+        announce("decode_step at capacity 8: drops")
+        a, b, worst = _decode_twins(gpu, torch.bfloat16, 8, 2, 64, 8, False)
+        assert a.capacity == 8
+        assert (a.packed_lengths[1] == 8).all()
+        kept = int(a.packed_counts[1].sum().item())
+        assert kept < 2 * 2 * (64 - 16)     # some evicted tokens were dropped
+        print(f"decode_step full cache: {kept} of {2 * 2 * (64 - 16)} evicted tokens kept, "
+              f"fused max-abs {worst:.3e}", flush=True)
     finally:
         for name, val in saved.items():
             setattr(globVR, name, val)
