@@ -406,8 +406,25 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeAttnArgs a) {
   const int g = hq / a.G, hh = hq - g * a.G;
   const int bg = b * a.Hkv + g;
   const int tid = threadIdx.x, lane = tid & 63, wid = tid >> 6;
+  // FUSED: the writer's reads (the update's decision, the evicted token, the new token,
+  // the last anchor's count) go out with the first loads; its writes come at the end
+  const bool writer = FUSED && hh == 0 && blockIdx.y == 0 && tid < 64;
+  const bool wact = writer && 2 * tid < a.D;
+  uint16_t* const ring_k = const_cast<uint16_t*>(a.kx) + b * a.sx_b + g * a.sx_h + (int64_t)a.widx * a.sx_s + 2 * tid;
+  uint16_t* const ring_v = const_cast<uint16_t*>(a.vx) + b * a.sx_b + g * a.sx_h + (int64_t)a.widx * a.sx_s + 2 * tid;
+  int32_t* const cnt = const_cast<int32_t*>(a.counts) + b * a.sc_b + g * a.sc_h;
+  uint32_t ek = 0u, ev = 0u, nk = 0u, nv = 0u;
+  int dec = 0;
+  if (wact) {
+    ek = *(const uint32_t*)ring_k;
+    ev = *(const uint32_t*)ring_v;
+    nk = *(const uint32_t*)(a.new_k + b * a.sn_b + g * a.sn_h + 2 * tid);
+    nv = *(const uint32_t*)(a.new_v + b * a.sn_b + g * a.sn_h + 2 * tid);
+  }
+  if (writer && a.evict) dec = a.fused[2 * bg];
   int plen = a.lengths[bg];
   plen = plen < 0 ? 0 : (plen > a.capacity ? (int)a.capacity : plen);
+  const int c_last = writer && tid == 0 && a.evict && plen > 0 ? cnt[plen - 1] : 0;
   int total = FUSED ? a.fused[2 * bg + 1] : plen + a.exact_len;
   total = total < 0 ? 0 : (total > a.nslice * kDecSlice ? a.nslice * kDecSlice : total);
   const int ns = (total + kDecSlice - 1) / kDecSlice;
@@ -482,21 +499,16 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeAttnArgs a) {
     a.out[b * a.so_b + hq * a.so_h + d] = E16<DT>::bits(o / L);
   }
   if constexpr (FUSED) {
-    if (hh == 0 && blockIdx.y == 0 && tid < 64) {
-      const bool act = 2 * tid < a.D;
-      uint16_t* const ring_k = const_cast<uint16_t*>(a.kx) + b * a.sx_b + g * a.sx_h + (int64_t)a.widx * a.sx_s + 2 * tid;
-      uint16_t* const ring_v = const_cast<uint16_t*>(a.vx) + b * a.sx_b + g * a.sx_h + (int64_t)a.widx * a.sx_s + 2 * tid;
-      int32_t* const cnt = const_cast<int32_t*>(a.counts) + b * a.sc_b + g * a.sc_h;
+    if (writer) {
       if (a.evict) {
-        const int dec = a.fused[2 * bg];
         if (dec == 1) {  // :78-82
-          if (tid == 0) cnt[plen - 1] += 1;
+          if (tid == 0) cnt[plen - 1] = c_last + 1;
         } else if (dec == 2) {  // :83-96
-          if (act) {
+          if (wact) {
             uint16_t* const pk = const_cast<uint16_t*>(a.kp) + b * a.sp_b + g * a.sp_h + (int64_t)plen * a.sp_s + 2 * tid;
             uint16_t* const pv = const_cast<uint16_t*>(a.vp) + b * a.sp_b + g * a.sp_h + (int64_t)plen * a.sp_s + 2 * tid;
-            *(uint32_t*)pk = *(const uint32_t*)ring_k;
-            *(uint32_t*)pv = *(const uint32_t*)ring_v;
+            *(uint32_t*)pk = ek;
+            *(uint32_t*)pv = ev;
           }
           if (tid == 0) {
             cnt[plen] = 1;
@@ -505,10 +517,10 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeAttnArgs a) {
           }
         }
       }
-      // the new token into the ring (:101-104), after this thread's read of the evicted one
-      if (act) {
-        *(uint32_t*)ring_k = *(const uint32_t*)(a.new_k + b * a.sn_b + g * a.sn_h + 2 * tid);
-        *(uint32_t*)ring_v = *(const uint32_t*)(a.new_v + b * a.sn_b + g * a.sn_h + 2 * tid);
+      // the new token into the ring (:101-104), in place of the evicted one
+      if (wact) {
+        *(uint32_t*)ring_k = nk;
+        *(uint32_t*)ring_v = nv;
       }
     }
   }
