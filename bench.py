@@ -11,9 +11,10 @@ modeling_llama.py:612-754).
 The default run measures config 1 (N = 32768, r = 4) as the headline and adds to the same
 JSON line: config 2 (N = 131072) at r = 2, 4 and 8, the same layer at N = 262144 and r = 4
 (the reference's longest point, key ``n262144_r4``), config 0 in fp32 (``config0_fp32``),
-the config-4 ragged batch, the config-3 end-to-end 32-layer prefill, the selection in both
-arithmetic definitions, the on-box MFMA and copy ceilings, and the CPU baseline (config 1
-and config 0 in full).
+the config-4 ragged batch, the config-3 end-to-end 32-layer prefill, the per-token decode
+after the config-1 prefill (``decode``: the one-call step, and the decode attention against
+the same kernels over the dense cache), the selection in both arithmetic definitions, the
+on-box MFMA and copy ceilings, and the CPU baseline (config 1 and config 0 in full).
 ``--config 2`` runs N = 131072 alone with ``--ratio`` in {2, 4, 8}.  The threshold tau is
 calibrated on the seeded keys so that the realised compression is r (smallest tau with
 keep rate <= 1/r), in the selection arithmetic that is timed.
@@ -79,7 +80,8 @@ def parse_args():
     ap.add_argument("--no-128k", action="store_true",
                     help="config 1 only: skip the config-2 (N=131072, r=2/4/8) measurements")
     ap.add_argument("--no-e2e", action="store_true",
-                    help="config 1 only: skip the config-3 end-to-end and config-4 ragged-batch parts")
+                    help="config 1 only: skip the config-3 end-to-end, config-4 ragged-batch, config-0 "
+                         "fp32 and decode parts")
     ap.add_argument("--no-sdpa", action="store_true",
                     help="skip timing torch's scaled_dot_product_attention as a second dense control")
     return ap.parse_args()
@@ -272,12 +274,16 @@ def run_config3(args):
 
 
 def run_decode(args):
+    print(json.dumps(decode_record(args)), flush=True)
+
+
+def decode_record(args):
     """Per-token decode (deltaDecoding.py:181-362 as modeling_llama.py:453-518 drives it)
     after a config-1 prefill: the compressed cache holds the P packed anchors of the
     delta selection plus the last W keys in the ring; each token runs the cache update
     and the decode attention for one layer.  The control is the same decode attention
-    over an uncompressed cache (all N keys packed with count 1, empty ring).  Prints one
-    JSON line."""
+    over an uncompressed cache (all N keys packed with count 1, empty ring).  Returns the
+    record (bench.py --decode prints it as its JSON line)."""
     import types
     import torch
     from deltaattention_amd import deltaDecoding as dd
@@ -410,7 +416,7 @@ def run_decode(args):
                  "in one graph, per call"),
         "keys_delta": P + W, "keys_dense": N,
     }
-    print(json.dumps(rec), flush=True)
+    return rec
 
 
 def config4_record(args, warmup, steps):
@@ -642,6 +648,14 @@ def main():
         rec["config3"]["workload"] = c3["config"]["workload"] + f", anchors {args.e2e_mode} r={args.ratio:g}"
         torch.cuda.empty_cache()
         rec["config0_fp32"] = config0_record(args)
+        torch.cuda.empty_cache()
+        log("decode after the config-1 prefill ...")
+        d = decode_record(args)
+        rec["decode"] = {key: d[key] for key in (
+            "value", "unit", "two_call_us_delta", "attention_us_delta", "attention_gpu_us_delta",
+            "attention_gpu_us_dense", "attention_gpu_speedup_vs_dense", "keys_delta", "keys_dense", "steps")}
+        rec["decode"]["metric"] = d["metric"]
+        rec["decode"]["workload"] = d["config"]["workload"]
         torch.cuda.empty_cache()
     if full:
         rec["peaks_measured"] = measure_peaks()
