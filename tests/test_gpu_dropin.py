@@ -230,7 +230,7 @@ def _misaligned(t):
     return out
 
 
-def _decode_twins(gpu, dtype, Hq, Hkv, steps, cap0, grow, seed=11):
+def _decode_twins(gpu, dtype, Hq, Hkv, steps, cap0, grow, seed=11, W=16):
     """Two caches fed the same tokens: cache a by cache.update + decode_attention, cache b
     by cache.decode_step.  Even steps hand decode_step 16-byte aligned key/value rows (the
     fused launch pair: the update folded into the attention); odd steps misaligned ones (the
@@ -244,7 +244,7 @@ def _decode_twins(gpu, dtype, Hq, Hkv, steps, cap0, grow, seed=11):
     (deltaDecoding.py:83-96)."""
     from types import SimpleNamespace
     from deltaattention_amd.deltaDecoding import HybridCompressedCache, decode_attention
-    B, W = 2, 16
+    B = 2
     q, k, v = (t.to(dtype) for t in _inputs(B, Hq, Hkv, steps, seed))
     cfg = SimpleNamespace(hidden_size=Hq * 128, num_attention_heads=Hq, num_key_value_heads=Hkv,
                           num_hidden_layers=2, head_dim=128)
@@ -308,6 +308,25 @@ def test_decode_step_equals_update_then_attention(gpu, metric, tau, dtype, Hq, H
         with pytest.raises(ValueError):   # one KV head where the cache has Hkv
             b.decode_step(x, x[:, :1], x[:, :1], 1)
         print(f"decode_step {metric}: packed length {n}, merged {merged}, fused max-abs {worst:.3e}",
+              flush=True)
+    finally:
+        for name, val in saved.items():
+            setattr(globVR, name, val)
+
+
+@pytest.mark.parametrize("W", [1, 3])
+def test_decode_step_small_rings(gpu, W):
+    """Rings of one and three slots: from the second token (W = 1) or the fourth on, every
+    step evicts, and the new token's slot rotates through the ring while the packed list
+    grows past capacity 8 (a rebuilt argument block)."""
+    from deltaattention_amd import globVR
+    saved = dict(vars(globVR))
+    try:
+        globVR.row_delta_threshold, globVR.row_similarity_metric = 9.5, "euclidean"
+        announce(f"decode_step with a ring of {W}")
+        a, b, worst = _decode_twins(gpu, torch.bfloat16, 8, 2, 40, 8, True, W=W)
+        assert a.capacity > 8
+        print(f"decode_step W={W}: packed length {int(a.packed_lengths[1].max())}, fused max-abs {worst:.3e}",
               flush=True)
     finally:
         for name, val in saved.items():
