@@ -17,7 +17,8 @@
 // are read once per group), keeps the slice's max / sum / P.V partials, and the
 // combine kernel merges the slices exactly (rescaling by exp(m_s - M)).  As in the
 // reference, P is rounded to the cache's 16-bit type before the P.V product while the
-// row sum stays fp32.  The cache is bf16 or fp16 (the E16 element type).
+// row sum stays fp32.  The cache is bf16 or fp16 (the E16 element type), or fp32
+// (decode_attn_f32_kernel: p stays fp32, as the reference's p.to(v.dtype) leaves it).
 #include <mutex>
 
 #include "da_common.hpp"
@@ -44,14 +45,33 @@ struct DecodeUpdateArgs {
   float thr;
 };
 
-// The update's test (deltaDecoding.py:61-77): does the evicted token (this lane's 4-byte
-// word ek, dims 2l and 2l + 1) merge into the last packed anchor (word lk)?  Euclidean
+// A lane's two elements (dims 2l and 2l + 1) of a cache row: one 32-bit word of a 16-bit
+// type, or two fp32 values (8 bytes).
+template <int DT>
+struct DecPair {
+  using Elem = uint16_t;
+  using Word = uint32_t;
+  static __device__ __forceinline__ float lo(Word w) { return E16<DT>::lo(w); }
+  static __device__ __forceinline__ float hi(Word w) { return E16<DT>::hi(w); }
+};
+template <>
+struct DecPair<DA_F32> {
+  using Elem = float;
+  using Word = u32x2;
+  static __device__ __forceinline__ float lo(Word w) { return __uint_as_float(w[0]); }
+  static __device__ __forceinline__ float hi(Word w) { return __uint_as_float(w[1]); }
+};
+
+// The update's test (deltaDecoding.py:61-77): does the evicted token (this lane's pair
+// ek, dims 2l and 2l + 1) merge into the last packed anchor (pair lk)?  Euclidean
 // dist^2 <= thr or cosine >= thr, with the selection's fixed fp32 tree; the same result
 // in every lane.
 template <bool COS, int DT>
-__device__ __forceinline__ bool evict_merges(uint32_t ek, uint32_t lk, float thr) {
+__device__ __forceinline__ bool evict_merges(typename DecPair<DT>::Word ek, typename DecPair<DT>::Word lk,
+                                             float thr) {
 #pragma clang fp contract(off)
-  const float e0 = E16<DT>::lo(ek), e1 = E16<DT>::hi(ek), l0 = E16<DT>::lo(lk), l1 = E16<DT>::hi(lk);
+  using PT = DecPair<DT>;
+  const float e0 = PT::lo(ek), e1 = PT::hi(ek), l0 = PT::lo(lk), l1 = PT::hi(lk);
   if (COS) {
     const float eps = 1e-8f;
     const float dot = wave_tree_sum(pair_dot(e0, e1, l0, l1));
@@ -70,29 +90,31 @@ __global__ __launch_bounds__(256) void decode_update_kernel(DecodeUpdateArgs a) 
   const int w = blockIdx.x * 4 + (threadIdx.x >> 6);
   if (w >= a.B * a.H) return;
   const int b = w / a.H, h = w - (w / a.H) * a.H;
+  using E = typename DecPair<DT>::Elem;
+  using Word = typename DecPair<DT>::Word;
   const bool act = 2 * lane < a.D;
   const int64_t widx = a.exact_len % a.window;                       // :35
-  uint16_t* ring_k = a.kx + b * a.sx_b + h * a.sx_h + 2 * lane;
-  uint16_t* ring_v = a.vx + b * a.sx_b + h * a.sx_h + 2 * lane;
-  uint16_t* pk = a.kp + b * a.sp_b + h * a.sp_h + 2 * lane;
-  uint16_t* pv = a.vp + b * a.sp_b + h * a.sp_h + 2 * lane;
+  E* ring_k = (E*)(void*)a.kx + b * a.sx_b + h * a.sx_h + 2 * lane;
+  E* ring_v = (E*)(void*)a.vx + b * a.sx_b + h * a.sx_h + 2 * lane;
+  E* pk = (E*)(void*)a.kp + b * a.sp_b + h * a.sp_h + 2 * lane;
+  E* pv = (E*)(void*)a.vp + b * a.sp_b + h * a.sp_h + 2 * lane;
   int32_t* cnt = a.counts + b * a.sc_b + h * a.sc_h;
   int32_t* tsr = a.ts + b * a.sc_b + h * a.sc_h;
   if (a.exact_len >= a.window) {                                     // :54
-    const uint32_t ek = act ? *(const uint32_t*)(ring_k + widx * a.sx_s) : 0u;
-    const uint32_t ev = act ? *(const uint32_t*)(ring_v + widx * a.sx_s) : 0u;
+    const Word ek = act ? *(const Word*)(ring_k + widx * a.sx_s) : Word{};
+    const Word ev = act ? *(const Word*)(ring_v + widx * a.sx_s) : Word{};
     const int plen = a.lengths[w];
     bool merge = false;
     if (plen > 0) {                                                  // :61-77
-      const uint32_t lk = act ? *(const uint32_t*)(pk + (int64_t)(plen - 1) * a.sp_s) : 0u;
+      const Word lk = act ? *(const Word*)(pk + (int64_t)(plen - 1) * a.sp_s) : Word{};
       merge = evict_merges<COS, DT>(ek, lk, a.thr);
     }
     if (merge) {                                                     // :78-82
       if (lane == 0) cnt[plen - 1] += 1;
     } else if (plen < a.capacity) {                                  // :83-96
       if (act) {
-        *(uint32_t*)(pk + (int64_t)plen * a.sp_s) = ek;
-        *(uint32_t*)(pv + (int64_t)plen * a.sp_s) = ev;
+        *(Word*)(pk + (int64_t)plen * a.sp_s) = ek;
+        *(Word*)(pv + (int64_t)plen * a.sp_s) = ev;
       }
       if (lane == 0) {
         cnt[plen] = 1;
@@ -103,10 +125,10 @@ __global__ __launch_bounds__(256) void decode_update_kernel(DecodeUpdateArgs a) 
   }
   // insert the new token into the ring (:101-104)
   if (act) {
-    const uint32_t nk = *(const uint32_t*)(a.new_k + b * a.sn_b + h * a.sn_h + 2 * lane);
-    const uint32_t nv = *(const uint32_t*)(a.new_v + b * a.sn_b + h * a.sn_h + 2 * lane);
-    *(uint32_t*)(ring_k + widx * a.sx_s) = nk;
-    *(uint32_t*)(ring_v + widx * a.sx_s) = nv;
+    const Word nk = *(const Word*)((const E*)(const void*)a.new_k + b * a.sn_b + h * a.sn_h + 2 * lane);
+    const Word nv = *(const Word*)((const E*)(const void*)a.new_v + b * a.sn_b + h * a.sn_h + 2 * lane);
+    *(Word*)(ring_k + widx * a.sx_s) = nk;
+    *(Word*)(ring_v + widx * a.sx_s) = nv;
   }
 }
 
@@ -379,6 +401,128 @@ __global__ __launch_bounds__(64) void decode_attn_kernel(DecodeAttnArgs a) {
     }
 }
 
+// fp32 caches: the reference's kernels load the cache's own type and compute in fp32, and
+// P.V takes p in the cache's type (deltaDecoding.py:319), here fp32 itself, unrounded.
+// Slices, partials and the combine are decode_attn_kernel's.  A key row is D fp32 values
+// (twice the bytes of a 16-bit row), so lane t reads its row eight 16-byte chunks at a
+// time and the slice's value rows go in four batches of 16 (8 bytes per lane each), which
+// keeps the wave's registers near the 16-bit kernel's.  Value rows: lane t finds the
+// source of row j0 + t (clamped to the list's last key) and row u's loads take lane u's
+// pointer, as in the 16-bit kernel's mixed slices.
+template <int G>
+__global__ __launch_bounds__(64) void decode_attn_f32_kernel(DecodeAttnArgs a) {
+  __shared__ float s_q[G][kDecD];
+  __shared__ float s_p[G][kDecSlice];
+  const int lane = threadIdx.x;
+  const int bg = blockIdx.x, slice = blockIdx.y;
+  const int hh0 = blockIdx.z * G;
+  auto head = [&](int hh) { return min(hh0 + hh, a.G - 1); };
+  const int D = a.D;
+  const int b = bg / a.Hkv, g = bg - (bg / a.Hkv) * a.Hkv;
+  int plen = a.lengths[bg];
+  plen = plen < 0 ? 0 : (plen > a.capacity ? (int)a.capacity : plen);
+  const int total = plen + a.exact_len;
+  const int j0 = slice * kDecSlice;
+  if (j0 >= total) return;  // the combine kernel skips slices past the end
+  const float* const pk_row0 = (const float*)(const void*)a.kp + b * a.sp_b + g * a.sp_h;
+  const float* const pv_row0 = (const float*)(const void*)a.vp + b * a.sp_b + g * a.sp_h;
+  const float* const xk_row0 = (const float*)(const void*)a.kx + b * a.sx_b + g * a.sx_h;
+  const float* const xv_row0 = (const float*)(const void*)a.vx + b * a.sx_b + g * a.sx_h;
+  auto row_of = [&](int jj, const float* p0, const float* x0) -> const float* {
+    return jj < plen ? p0 + (int64_t)jj * a.sp_s : x0 + (int64_t)(jj - plen) * a.sx_s;
+  };
+
+  const float* const q = (const float*)(const void*)a.q;
+  constexpr int kQPerLane = G * kDecD / 64;
+#pragma unroll
+  for (int it = 0; it < kQPerLane; ++it) {
+    const int i = lane + 64 * it, hh = i / kDecD, d = i - hh * kDecD;
+    s_q[hh][d] = d < D ? q[b * a.sq_b + (int64_t)(g * a.G + head(hh)) * a.sq_h + d] : 0.0f;
+  }
+  __syncthreads();
+
+  // ---- scores: lane t scores key j0 + t for every query head of the sub-group ----
+  const int j = j0 + lane;
+  const bool valid = j < total;
+  float sc[G];
+#pragma unroll
+  for (int hh = 0; hh < G; ++hh) sc[hh] = -INFINITY;
+  if (valid) {
+    const float* krow = row_of(j, pk_row0, xk_row0);
+    const int cnt = j < plen ? a.counts[b * a.sc_b + g * a.sc_h + j] : 1;
+    float acc[G];
+#pragma unroll
+    for (int hh = 0; hh < G; ++hh) acc[hh] = 0.0f;
+#pragma unroll
+    for (int c0 = 0; c0 < kDecD / 4; c0 += 8) {
+      if (4 * c0 < D) {  // D is a multiple of 8: a chunk of four is all in or all out
+        f32x4 kk[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+          kk[u] = 4 * (c0 + u) < D ? *(const f32x4*)(krow + 4 * (c0 + u)) : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+#pragma unroll
+            for (int hh = 0; hh < G; ++hh) acc[hh] = __builtin_fmaf(s_q[hh][4 * (c0 + u) + e], kk[u][e], acc[hh]);
+      }
+    }
+    // log(count) bias; log(0) = -inf: padding anchors get no weight (:309-311)
+    const float bias = j >= plen ? 0.0f : (cnt <= 0 ? -INFINITY : __logf((float)cnt));
+#pragma unroll
+    for (int hh = 0; hh < G; ++hh) sc[hh] = acc[hh] * a.scale + bias;
+  }
+
+  // ---- per-head slice max and sum; p (fp32) to LDS ----
+  float* part = a.part + ((int64_t)bg * a.nslice + slice) * a.G * (kDecD + 2);
+#pragma unroll
+  for (int hh = 0; hh < G; ++hh) {
+    const float m = wave_max_all(sc[hh]);
+    const float p = (sc[hh] == -INFINITY) ? 0.0f : __expf(sc[hh] - m);
+    const float l = wave_sum_all(p);
+    s_p[hh][lane] = p;
+    if (lane == 0) {
+      part[head(hh) * (kDecD + 2)] = m;
+      part[head(hh) * (kDecD + 2) + 1] = l;
+    }
+  }
+  __syncthreads();
+
+  // ---- P.V: lane l owns dims 2l, 2l+1 (lanes past the head dimension read its last
+  // pair; their partials are never stored by the combine) ----
+  const int vdim = min(2 * lane, D - 2);
+  const uint64_t mine = (uint64_t)row_of(min(j, total - 1), pv_row0, xv_row0);
+  const uint32_t lo = (uint32_t)mine, hi = (uint32_t)(mine >> 32);
+  const uint32_t voff = 4u * (uint32_t)vdim;  // bytes
+  float av[G][2];
+#pragma unroll
+  for (int hh = 0; hh < G; ++hh) av[hh][0] = av[hh][1] = 0.0f;
+#pragma unroll
+  for (int u0 = 0; u0 < kDecSlice; u0 += 16) {
+    f32x2 vv[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) {
+      const uint64_t row = ((uint64_t)(uint32_t)__builtin_amdgcn_readlane(hi, u0 + u) << 32) |
+                           (uint32_t)__builtin_amdgcn_readlane(lo, u0 + u);
+      vv[u] = *(const __attribute__((address_space(1))) f32x2*)(row + voff);  // a global load
+    }
+#pragma unroll
+    for (int u = 0; u < 16; ++u)
+#pragma unroll
+      for (int hh = 0; hh < G; ++hh) {
+        av[hh][0] = __builtin_fmaf(s_p[hh][u0 + u], vv[u][0], av[hh][0]);
+        av[hh][1] = __builtin_fmaf(s_p[hh][u0 + u], vv[u][1], av[hh][1]);
+      }
+    __builtin_amdgcn_sched_barrier(0);  // one batch of rows in flight at a time
+  }
+#pragma unroll
+  for (int hh = 0; hh < G; ++hh) {
+    part[head(hh) * (kDecD + 2) + 2 + 2 * lane] = av[hh][0];
+    part[head(hh) * (kDecD + 2) + 3 + 2 * lane] = av[hh][1];
+  }
+}
+
 // Merge of the slices of one query head, split over kCombParts workgroups of
 // kCombDims dims each.  Thread (dim d, phase q) adds dim d of the P.V partials of the
 // slices s = q (mod kCombPhases), kCombUnroll slices at a time with all of their loads in
@@ -496,7 +640,10 @@ __global__ __launch_bounds__(256) void decode_combine_kernel(DecodeAttnArgs a) {
     float o = acc;
 #pragma unroll
     for (int p = 1; p < kCombPhases; ++p) o += s_acc[p][dl];
-    a.out[b * a.so_b + hq * a.so_h + d] = E16<DT>::bits(o / L);
+    if constexpr (DT == DA_F32)
+      ((float*)(void*)a.out)[b * a.so_b + hq * a.so_h + d] = o / L;
+    else
+      a.out[b * a.so_b + hq * a.so_h + d] = E16<DT>::bits(o / L);
   }
   if constexpr (FUSED) {
     if (writer) {
@@ -540,13 +687,17 @@ static int decode_update_impl(const void* new_k, const void* new_v, int dtype, i
                               void* stream, const char* who) {
   DA_REQUIRE(new_k && new_v && k_exact && v_exact && k_packed && v_packed && counts && timestamps && lengths,
              "%s: null pointer", who);
-  if (dtype != DA_BF16 && dtype != DA_F16)
-    return set_error(DA_ERR_UNSUPPORTED, "%s: the cache must be bf16 or fp16", who);
+  if (dtype != DA_BF16 && dtype != DA_F16 && dtype != DA_F32)
+    return set_error(DA_ERR_UNSUPPORTED, "%s: the cache must be bf16, fp16 or fp32", who);
   DA_REQUIRE(B > 0 && Hkv > 0 && window > 0 && capacity > 0, "%s: empty shape", who);
   if (D > 128 || (D & 1)) return set_error(DA_ERR_UNSUPPORTED, "%s: head_dim must be even and <= 128", who);
   DA_REQUIRE(exact_seq_len >= 0 && total_seq_len >= 0, "%s: negative lengths", who);
-  DA_REQUIRE(((sn_b | sn_h | sx_b | sx_h | sx_s | sp_b | sp_h | sp_s) & 1) == 0,
-             "%s: rows must be 4-byte aligned", who);
+  // a lane moves an element pair: 4 bytes (16-bit) or 8 bytes (fp32) at once
+  const uintptr_t pair_align = dtype == DA_F32 ? 7 : 3;
+  DA_REQUIRE(((sn_b | sn_h | sx_b | sx_h | sx_s | sp_b | sp_h | sp_s) & 1) == 0 &&
+                 (((uintptr_t)new_k | (uintptr_t)new_v | (uintptr_t)k_exact | (uintptr_t)v_exact |
+                   (uintptr_t)k_packed | (uintptr_t)v_packed) & pair_align) == 0,
+             "%s: rows must be %d-byte aligned (even strides)", who, dtype == DA_F32 ? 8 : 4);
   DecodeUpdateArgs a = {};
   a.new_k = (const uint16_t*)new_k; a.new_v = (const uint16_t*)new_v; a.sn_b = sn_b; a.sn_h = sn_h;
   a.kx = (uint16_t*)k_exact; a.vx = (uint16_t*)v_exact; a.sx_b = sx_b; a.sx_h = sx_h; a.sx_s = sx_s;
@@ -556,7 +707,10 @@ static int decode_update_impl(const void* new_k, const void* new_v, int dtype, i
   a.B = (int)B; a.H = (int)Hkv; a.D = (int)D; a.thr = threshold;
   const unsigned blocks = (unsigned)((B * Hkv + 3) / 4);
   hipStream_t st = (hipStream_t)stream;
-  if (dtype == DA_F16) {
+  if (dtype == DA_F32) {
+    if (use_cosine) hipLaunchKernelGGL((decode_update_kernel<true, DA_F32>), dim3(blocks), dim3(256), 0, st, a);
+    else hipLaunchKernelGGL((decode_update_kernel<false, DA_F32>), dim3(blocks), dim3(256), 0, st, a);
+  } else if (dtype == DA_F16) {
     if (use_cosine) hipLaunchKernelGGL((decode_update_kernel<true, DA_F16>), dim3(blocks), dim3(256), 0, st, a);
     else hipLaunchKernelGGL((decode_update_kernel<false, DA_F16>), dim3(blocks), dim3(256), 0, st, a);
   } else {
@@ -601,6 +755,25 @@ static int launch_decode_g(DecodeAttnArgs& a, int64_t n_heads, hipStream_t st) {
   hipLaunchKernelGGL((decode_combine_kernel<DT, FUSED>), dim3((unsigned)n_heads, kCombParts), dim3(256), 0, st, a);
   return check_launch("da_decode_attention(combine)");
 }
+static int launch_decode_f32(DecodeAttnArgs& a, int64_t n_heads, hipStream_t st) {
+  const int nsub = (a.G + kDecMaxG - 1) / kDecMaxG;
+  const int gw = (a.G + nsub - 1) / nsub;
+  const dim3 agrid((unsigned)(a.B * a.Hkv), (unsigned)a.nslice, (unsigned)nsub);
+  switch (gw) {
+    case 1: hipLaunchKernelGGL((decode_attn_f32_kernel<1>), agrid, dim3(64), 0, st, a); break;
+    case 2: hipLaunchKernelGGL((decode_attn_f32_kernel<2>), agrid, dim3(64), 0, st, a); break;
+    case 3: hipLaunchKernelGGL((decode_attn_f32_kernel<3>), agrid, dim3(64), 0, st, a); break;
+    case 4: hipLaunchKernelGGL((decode_attn_f32_kernel<4>), agrid, dim3(64), 0, st, a); break;
+    case 5: hipLaunchKernelGGL((decode_attn_f32_kernel<5>), agrid, dim3(64), 0, st, a); break;
+    case 6: hipLaunchKernelGGL((decode_attn_f32_kernel<6>), agrid, dim3(64), 0, st, a); break;
+    case 7: hipLaunchKernelGGL((decode_attn_f32_kernel<7>), agrid, dim3(64), 0, st, a); break;
+    default: hipLaunchKernelGGL((decode_attn_f32_kernel<8>), agrid, dim3(64), 0, st, a); break;
+  }
+  if (int rc = check_launch("da_decode_attention")) return rc;
+  hipLaunchKernelGGL((decode_combine_kernel<DA_F32, false>), dim3((unsigned)n_heads, kCombParts), dim3(256), 0, st,
+                     a);
+  return check_launch("da_decode_attention(combine)");
+}
 template <int DT, bool FUSED>
 static int launch_decode(DecodeAttnArgs& a, int64_t n_heads, hipStream_t st) {
   return a.D == kDecD ? launch_decode_g<DT, true, FUSED>(a, n_heads, st)
@@ -637,6 +810,7 @@ static int decode_attention_impl(const void* q, int dtype, int64_t B, int64_t Hq
   a.part = part;
   a.nslice = (int)((capacity + window + kDecSlice - 1) / kDecSlice);
   a.B = (int)B; a.Hq = (int)Hq; a.Hkv = (int)Hkv; a.G = (int)(Hq / Hkv); a.D = (int)D;
+  if (dtype == DA_F32) return launch_decode_f32(a, B * Hq, st);
   return dtype == DA_F16 ? launch_decode<DA_F16, false>(a, B * Hq, st) : launch_decode<DA_BF16, false>(a, B * Hq, st);
 }
 
@@ -649,8 +823,8 @@ static int decode_attention_check(const void* q, int dtype, int64_t B, int64_t H
                                   const char* who) {
   DA_REQUIRE(q && k_packed && v_packed && counts && lengths && k_exact && v_exact && out,
              "%s: null pointer", who);
-  if (dtype != DA_BF16 && dtype != DA_F16)
-    return set_error(DA_ERR_UNSUPPORTED, "%s: the cache must be bf16 or fp16", who);
+  if (dtype != DA_BF16 && dtype != DA_F16 && dtype != DA_F32)
+    return set_error(DA_ERR_UNSUPPORTED, "%s: the cache must be bf16, fp16 or fp32", who);
   if (D <= 0 || D > kDecD || (D & 7))
     return set_error(DA_ERR_UNSUPPORTED, "%s: head_dim must be a multiple of 8 in [8, %d]", who, kDecD);
   DA_REQUIRE(B > 0 && Hq > 0 && Hkv > 0 && Hq % Hkv == 0, "%s: bad head counts", who);
@@ -659,7 +833,8 @@ static int decode_attention_check(const void* q, int dtype, int64_t B, int64_t H
   // key rows are read 16 bytes at a time, value rows 4 bytes per lane
   DA_REQUIRE(((sp_b | sp_h | sp_s | sx_b | sx_h | sx_s) & 7) == 0 && (((uintptr_t)k_packed | (uintptr_t)k_exact) & 15) == 0,
              "%s: key rows must be 16-byte aligned", who);
-  DA_REQUIRE((((uintptr_t)v_packed | (uintptr_t)v_exact) & 3) == 0, "%s: value rows must be 4-byte aligned", who);
+  DA_REQUIRE((((uintptr_t)v_packed | (uintptr_t)v_exact) & (dtype == DA_F32 ? 7 : 3)) == 0,
+             "%s: value rows must be %d-byte aligned", who, dtype == DA_F32 ? 8 : 4);
   if (decode_slices(capacity, window) > kDecMaxSlices)
     return set_error(DA_ERR_UNSUPPORTED, "%s: cache longer than %d keys", who, kDecMaxSlices * kDecSlice - 1);
   return DA_OK;
@@ -731,7 +906,8 @@ extern "C" int da_decode_step(const DaDecodeStep* s, void* stream) {
   DA_REQUIRE(s->new_k && s->new_v && s->timestamps, "%s: null pointer", who);
   DA_REQUIRE(s->exact_seq_len >= 0 && s->total_seq_len >= 0, "%s: negative lengths", who);
   // the fused path reads the new token's key row like the cache's: 16-byte aligned rows
-  if (((s->sn_b | s->sn_h) & 7) == 0 && (((uintptr_t)s->new_k | (uintptr_t)s->new_v) & 15) == 0)
+  if (s->dtype != DA_F32 && ((s->sn_b | s->sn_h) & 7) == 0 &&
+      (((uintptr_t)s->new_k | (uintptr_t)s->new_v) & 15) == 0)
     return decode_step_fused(s, exact_len, (hipStream_t)stream);
   if (int rc = decode_update_impl(s->new_k, s->new_v, s->dtype, s->B, s->Hkv, s->D, s->sn_b, s->sn_h, s->k_exact,
                                   s->v_exact, s->sx_b, s->sx_h, s->sx_s, s->k_packed, s->v_packed, s->sp_b,

@@ -207,7 +207,8 @@ int da_dense_prefill_varlen(const void* q, const void* k, const void* v, void* o
  * Decode step of the compressed cache.  Replaces fused_hybrid_decode_update_kernel
  * (deltaDecoding.py:9-104) as launched by HybridCompressedCache.update (:181-211).
  *
- * new_k, new_v: [B, Hkv, 1, D] bf16 or fp16 like the cache (strides sn_b, sn_h).
+ * new_k, new_v: [B, Hkv, 1, D] bf16, fp16 or fp32 like the cache (strides sn_b, sn_h;
+ *   even strides, rows 4-byte aligned for 16-bit caches and 8-byte aligned for fp32).
  * k_exact, v_exact: ring [B, Hkv, W, D] (strides sx_*); k_packed, v_packed:
  *   [B, Hkv, capacity, D] (strides sp_*); counts, timestamps: [B, Hkv, capacity]
  *   int32 (strides sc_b, sc_h, packed axis contiguous); lengths: [B * Hkv] int32.
@@ -230,7 +231,7 @@ int da_decode_update(const void* new_k, const void* new_v, int dtype, int64_t B,
  * q_len = 1 attention over the compressed cache.  Replaces fused_hybrid_decode_kernel
  * (deltaDecoding.py:236-362) and its wrapper (modeling_llama.py:453-518).
  *
- * q: [B, Hq, D] bf16 or fp16 like the cache (strides sq_b, sq_h); query head h reads kv
+ * q: [B, Hq, D] bf16, fp16 or fp32 like the cache (strides sq_b, sq_h); query head h reads kv
  * head h / (Hq / Hkv).
  * Scores over the packed anchors [0, lengths[b*Hkv + g]) get + log(count); then the
  * ring slots [0, exact_len) (exact_len = min(exact_seq_len, W)).  out: [B, Hq, D]
@@ -267,7 +268,8 @@ int da_decode_attention(const void* q, int dtype, int64_t B, int64_t Hq, int64_t
  * scored at the end of the key list instead of after the packed anchors, so the output
  * equals the two calls' up to fp32 summation order.  New-token rows that are not 16-byte
  * aligned (sn_b, sn_h multiples of 8 elements, new_k / new_v 16-byte aligned) run the
- * update and attention kernels in sequence instead, bit-identical to the two calls.
+ * update and attention kernels in sequence instead, bit-identical to the two calls; so do
+ * fp32 caches.
  */
 typedef struct DaDecodeStep {
   /* this token */

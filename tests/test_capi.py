@@ -129,8 +129,8 @@ def test_decode_rejects_misaligned_values():
 
 
 def test_decode_shape_limits():
-    """Decode attention takes head dims that are multiples of 8 up to 128 and GQA groups up
-    to 64; other shapes are refused as unsupported before any launch (the accepted ones
+    """Decode attention takes bf16, fp16 or fp32 caches, head dims that are multiples of 8 up
+    to 128 and GQA groups up to 64; other shapes are refused as unsupported before any launch (the accepted ones
     reach the workspace check)."""
     lib = _native.lib()
     a = ctypes.c_void_p(1 << 20)
@@ -142,8 +142,10 @@ def test_decode_shape_limits():
         return lib.da_decode_attention(a, dtype, 1, Hq, Hkv, D, Hq * D, D, a, a, *st_p, a, Hkv * cap, cap, a,
                                        cap, a, a, *st_x, W, 0, f, a, Hq * D, D, ws, ws_bytes, None)
 
-    # the decode cache is 16-bit: fp32 (DA_F32 = 4) is refused as unsupported
-    assert call(8, 8, 64, dtype=4) == -2 and "bf16 or fp16" in _err()
+    # the decode cache is bf16, fp16 or fp32: int32 (DA_I32 = 3) is refused as unsupported,
+    # fp32 (DA_F32 = 4) reaches the workspace check
+    assert call(8, 8, 64, dtype=3) == -2 and "bf16, fp16 or fp32" in _err()
+    assert call(8, 8, 64, dtype=4) == -4 and "workspace" in _err()
 
     for D in (4, 100, 136):
         assert call(8, 8, D) == -2 and "head_dim" in _err(), D
