@@ -262,14 +262,14 @@ def llama3_8b_config(attn_implementation: str = DELTA, num_layers: int = 32):
     return cfg
 
 
-def random_llama(cfg, device: torch.device, seed: int = 0):
-    """A randomly initialised LlamaForCausalLM in bf16 on ``device`` (weights ~ N(0, 0.02);
-    nothing is downloaded)."""
+def random_llama(cfg, device: torch.device, seed: int = 0, dtype: torch.dtype = torch.bfloat16):
+    """A randomly initialised LlamaForCausalLM in ``dtype`` (bf16 by default) on ``device``
+    (weights ~ N(0, 0.02); nothing is downloaded)."""
     from transformers import LlamaForCausalLM
     register()
     torch.manual_seed(seed)
     prev = torch.get_default_dtype()
-    torch.set_default_dtype(torch.bfloat16)
+    torch.set_default_dtype(dtype)
     try:
         with torch.device(device):
             model = LlamaForCausalLM(cfg)

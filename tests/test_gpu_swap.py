@@ -130,10 +130,12 @@ def _assert_cache_equals(cache, st, what):
     assert np.array_equal(cache.v_exact[0].float().cpu().numpy(), st["v_exact"]), what
 
 
-@pytest.mark.parametrize("impl,timed", [("deltaattention", True), ("deltaattention_dense", True),
-                                        ("deltaattention", False)],
-                         ids=["path1", "path2", "path1-fused-step"])
-def test_model_prefill_then_decode_compressed_cache(gpu, monkeypatch, impl, timed):
+@pytest.mark.parametrize("impl,timed,dtype", [("deltaattention", True, torch.bfloat16),
+                                              ("deltaattention_dense", True, torch.bfloat16),
+                                              ("deltaattention", False, torch.bfloat16),
+                                              ("deltaattention", False, torch.float32)],
+                         ids=["path1", "path2", "path1-fused-step", "path1-step-fp32"])
+def test_model_prefill_then_decode_compressed_cache(gpu, monkeypatch, impl, timed, dtype):
     """A 2-layer Llama-3-8B-shaped model (hidden 4096, 32 query / 8 KV heads, head_dim
     128; vocab cut to 1024) prefills 2048 tokens into a HybridCompressedCache through
     llama_swap.install's forward and decodes 64 tokens one at a time.  PATH 1 hands its
@@ -143,7 +145,8 @@ def test_model_prefill_then_decode_compressed_cache(gpu, monkeypatch, impl, time
     under stage timing and as one HybridCompressedCache.decode_step without.  Layer 0 is
     replayed in the oracle from the keys and queries it saw: the cache after the hand-off
     and after the last step is bit-exact, and every step's decode attention is within
-    tolerance."""
+    tolerance.  "path1-step-fp32" runs the same model in fp32 (fp32 prefill kernels, fp32
+    cache, selection in fp32)."""
     from oracle import delta_oracle as O
     from oracle import select_oracle_c as OC
     from test_gpu_dropin import _oracle_cache_from_prefill
@@ -152,7 +155,7 @@ def test_model_prefill_then_decode_compressed_cache(gpu, monkeypatch, impl, time
     N, steps, W, tau = 2048, 64, 64, 20.5   # random-init keys: adjacent dist^2 ~ 420 +- 52
     cfg = llama_swap.llama3_8b_config(impl, num_layers=2)
     cfg.vocab_size = 1024
-    model = llama_swap.random_llama(cfg, gpu, seed=3)
+    model = llama_swap.random_llama(cfg, gpu, seed=3, dtype=dtype)
     for name, val in (("packing_mode", "delta"), ("chunk_size", 512), ("row_delta_threshold", tau),
                       ("row_similarity_metric", "euclidean"), ("delta_decode", True),
                       ("dense_window_size", 128), ("time_internal", timed), ("kv_log_interval", 16),
@@ -160,7 +163,7 @@ def test_model_prefill_then_decode_compressed_cache(gpu, monkeypatch, impl, time
         monkeypatch.setattr(globVR, name, val, raising=False)
     timing.reset()
     rec = _spy_layer0(monkeypatch)
-    cache = HybridCompressedCache(cfg, 1, dtype=torch.bfloat16, exact_window_size=W,
+    cache = HybridCompressedCache(cfg, 1, dtype=dtype, exact_window_size=W,
                                   initial_capacity=256, device="cuda")
     ids = torch.randint(0, cfg.vocab_size, (1, N + steps), generator=torch.Generator().manual_seed(4)).cuda()
     announce(f"model swap {impl}: prefill N={N} into HybridCompressedCache")
@@ -169,7 +172,8 @@ def test_model_prefill_then_decode_compressed_cache(gpu, monkeypatch, impl, time
     assert torch.isfinite(h).all()
     assert cache.get_seq_length(0) == N and cache.get_seq_length(1) == N
     k0, v0 = (t.float().cpu().numpy() for t in rec["prefill"])
-    keep, _ = OC.select_delta(k0, tau, 512, arith="bf16")  # the model and cache are bf16
+    # the selection's native arithmetic: bf16 keys in bf16, fp32 keys in fp32
+    keep, _ = OC.select_delta(k0, tau, 512, arith="bf16" if dtype == torch.bfloat16 else "fp32")
     p = O.pack(k0, v0, keep)
     st = _oracle_cache_from_prefill(p, k0, v0, W, cache.capacity + steps)
     _assert_cache_equals(cache, st, "after the prefill hand-off")
