@@ -844,6 +844,11 @@ def measure_layer(args, N, ratio, headline, inputs=None, shared=None):
         "select_fp32_us": round(1e3 * sel["fp32"], 2),
         "hybrid_tflops": round(hyb_tflops, 1),
         "hybrid_mfma_frac": round(hyb_tflops / BF16_PEAK_TFLOPS, 4),
+        # hardware utilisation at the reference's granularity: 4 D 128 128 per processed
+        # (query block, key block) pair of its schedule; the kernel itself skips work at
+        # 32-key x 64-row granularity, so its MFMA counters read less than this
+        "hybrid_executed_tile_flops": fl["executed_tiles"],
+        "hybrid_tile_tflops": round(fl["executed_tiles"] / (ms_hybrid * 1e-3) / 1e12, 1),
         "dense_tflops": round(dense_tflops, 1),
         "dense_mfma_frac": round(dense_tflops / BF16_PEAK_TFLOPS, 4),
     }
@@ -881,9 +886,11 @@ def measure_layer(args, N, ratio, headline, inputs=None, shared=None):
                      "unit": "TFLOP/s", "frac": round(hyb_tflops / BF16_PEAK_TFLOPS, 4),
                      "traffic": traffic_bytes(args, N, r_real, ratio),
                      "kernel": "attn_w64_kernel<hybrid> (da_hybrid_prefill)",
-                     "algorithmic_flops": fl["algorithmic"]},
+                     "algorithmic_flops": fl["algorithmic"],
+                     "executed_tile_flops": fl["executed_tiles"]},
     }
-    rec.update({k2: v2 for k2, v2 in res.items() if k2 not in ("seq_len", "hybrid_algorithmic_flops")})
+    rec.update({k2: v2 for k2, v2 in res.items()
+                if k2 not in ("seq_len", "hybrid_algorithmic_flops", "hybrid_executed_tile_flops")})
     res["record"] = rec
     res["cpu_inputs"] = (q.cpu(), k.cpu(), v.cpu(), tau)
     return res
