@@ -136,6 +136,28 @@ def test_select_native_arith_bitexact(gpu, dtype, oracle_arith):
     assert not np.array_equal(k32, ok)
 
 
+@pytest.mark.parametrize("scale,tau", [(2e-3, 0.015), (40.0, 250.0)], ids=["subnormal-squares", "near-fp16-max"])
+@pytest.mark.parametrize("H", [4, 64], ids=["one-chunk-per-wave", "two-chunks-per-wave"])
+def test_select_fp16_native_extremes(gpu, scale, tau, H):
+    """fp16 keys in the keys' own arithmetic at the edges of the format, bit-exact against
+    the oracle's fp16 rounding (pinned against torch, subnormals included): keys scaled
+    so that the squared differences are fp16 subnormals (spacing 6e-8) with the threshold
+    among them, and keys whose distances reach the fp16 maximum (65504, spacing 32; sums
+    past it are inf, kept) with tau^2 = 62500 just below it.  Both walk layouts."""
+    from deltaattention_amd import ops, synth
+    N = 16384 if H == 64 else 4096   # 64 heads x 32 chunks: the pair walk's 2048 chunks
+    k = (synth.make_layer_inputs(1, H, H, N, 128, seed=29, rope_base=10000.0)[1].float() * scale).to(torch.float16)
+    assert torch.isfinite(k).all()
+    announce(f"select fp16 extremes scale={scale} tau={tau} H={H} N={N}")
+    keep, cc = ops.select(k.to(gpu), tau, 512, 0, arith="native")
+    ok, occ = OC.select_delta(k.float().numpy(), tau, 512, 0, arith="fp16")
+    assert np.array_equal(cc.cpu().numpy(), occ), "chunk counts differ"
+    assert np.array_equal(keep.cpu().numpy(), ok)
+    kept = int(ok.sum())
+    print(f"fp16 extremes scale={scale}: kept {kept} of {ok.size}", flush=True)
+    assert 0.02 * ok.size < kept < 0.98 * ok.size   # the threshold splits the rows
+
+
 @pytest.mark.parametrize("N,tau", [(3000, 10.0), (777, 7.0), (4096, 0.0)])
 def test_pack_exact(gpu, N, tau):
     from deltaattention_amd import ops
