@@ -327,6 +327,9 @@ def test_hybrid_golden(gpu, case, variant, native):
     (1, 8, 2, 2048, 1e6, 128, "hybrid", False),
     (1, 8, 2, 2048, 1e6, 128, "pure_phase1", False),
     (1, 8, 2, 2048, 1e6, 128, "hybrid", True),
+    (1, 8, 2, 1, 10.0, 128, "hybrid", False),      # one token
+    (2, 8, 2, 77, 9.0, 128, "hybrid", False),      # shorter than the window and one block
+    (1, 4, 2, 77, 9.0, 128, "pure_phase1", False),
 ])
 def test_delta_prefill_vs_oracle(gpu, B, Hq, Hkv, N, tau, W, variant, no_count):
     from deltaattention_amd import ops
