@@ -96,3 +96,18 @@ def test_dtype_code_accepts_one_data_type():
         dtype_code(f, a)
     with pytest.raises(TypeError):
         dtype_code(torch.zeros(2, dtype=torch.float64))
+
+
+def test_bench_refuses_more_than_one_gpu():
+    """bench.py --gpus N with N > 1 exits with status 2 and one JSON line saying why
+    (one GPU per box; the path would shard by KV head)."""
+    import json
+    import os
+    import subprocess
+    import sys
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    r = subprocess.run([sys.executable, os.path.join(root, "bench.py"), "--gpus", "2"],
+                       capture_output=True, text=True, timeout=120)
+    assert r.returncode == 2
+    rec = json.loads(r.stdout.strip().splitlines()[-1])
+    assert rec["n_gpus"] == 2 and "one GPU" in rec["error"]
